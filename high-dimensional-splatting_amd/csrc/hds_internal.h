@@ -1,0 +1,192 @@
+/*
+ * Internal helpers of the HIP library: error reporting behind the C ABI, launch checks, wave64
+ * primitives and the split-bf16 MFMA building blocks. Not part of the public interface
+ * (include/hds_rasterizer.h is).
+ */
+#ifndef HDS_INTERNAL_H
+#define HDS_INTERNAL_H
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "hds_common.h"
+
+/* ------------------------------------------------------------------------------------------- */
+/* Error reporting: every entry point returns an HDS_* status and leaves a thread-local message.  */
+/* ------------------------------------------------------------------------------------------- */
+
+#define HDS_OK 0
+#define HDS_ERR_INVALID 1
+#define HDS_ERR_RUNTIME 2
+
+int hds_set_error(int status, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+bool hds_debug_sync_enabled();
+
+/* Checks the last launch; with HDS_DEBUG set, also synchronises the stream and checks execution. */
+int hds_check_launch(const char* kernel, hipStream_t stream);
+
+#define HDS_LAUNCH_CHECK(name, stream)                         \
+	do {                                                       \
+		int _st = hds_check_launch((name), (stream));          \
+		if (_st != HDS_OK) return _st;                         \
+	} while (0)
+
+#define HDS_REQUIRE(cond, ...)                                 \
+	do {                                                       \
+		if (!(cond)) return hds_set_error(HDS_ERR_INVALID, __VA_ARGS__); \
+	} while (0)
+
+#define HDS_HIP(call)                                                                              \
+	do {                                                                                           \
+		hipError_t _e = (call);                                                                    \
+		if (_e != hipSuccess)                                                                      \
+			return hds_set_error(HDS_ERR_RUNTIME, "%s failed: %s", #call, hipGetErrorString(_e)); \
+	} while (0)
+
+static inline unsigned hds_blocks(int64_t n, int threads) { return (unsigned)((n + threads - 1) / threads); }
+
+/* ------------------------------------------------------------------------------------------- */
+/* Wave64 primitives.                                                                            */
+/* ------------------------------------------------------------------------------------------- */
+
+#define HDS_WAVE 64
+
+__device__ static inline int hds_lane() { return (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)); }
+
+/* Number of set bits of mask in lanes below this one. */
+__device__ static inline int hds_rank_below(uint64_t mask) {
+	return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
+__device__ static inline uint64_t hds_ballot(bool pred) { return (uint64_t)__ballot(pred); }
+
+/* Keeps the compiler from moving LDS accesses of one wave across this point. */
+__device__ static inline void hds_wave_fence() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront"); __builtin_amdgcn_wave_barrier(); __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront"); }
+
+__device__ static inline float hds_shfl_xor(float v, int mask) { return __shfl_xor(v, mask, HDS_WAVE); }
+
+/* Sum over all 64 lanes, result in every lane. */
+__device__ static inline float hds_wave_sum(float v) {
+#pragma unroll
+	for (int off = 32; off > 0; off >>= 1) v += hds_shfl_xor(v, off);
+	return v;
+}
+
+__device__ static inline int hds_wave_max(int v) {
+#pragma unroll
+	for (int off = 32; off > 0; off >>= 1) v = max(v, __shfl_xor(v, off, HDS_WAVE));
+	return v;
+}
+
+/*
+ * Reduce-scatter of 8 values over the wave: afterwards every lane of the octet q = (lane >> 3) & 7
+ * holds the wave-wide sum of v[q]. 10 shuffles instead of the 48 of eight full reductions.
+ */
+__device__ static inline float hds_wave_reduce_scatter8(float v[8], int lane) {
+	{
+		const bool hi = lane & 32;
+#pragma unroll
+		for (int i = 0; i < 4; i++) {
+			const float send = hi ? v[i] : v[i + 4];
+			const float keep = hi ? v[i + 4] : v[i];
+			v[i] = keep + hds_shfl_xor(send, 32);
+		}
+	}
+	{
+		const bool hi = lane & 16;
+#pragma unroll
+		for (int i = 0; i < 2; i++) {
+			const float send = hi ? v[i] : v[i + 2];
+			const float keep = hi ? v[i + 2] : v[i];
+			v[i] = keep + hds_shfl_xor(send, 16);
+		}
+	}
+	{
+		const bool hi = lane & 8;
+		const float send = hi ? v[0] : v[1];
+		const float keep = hi ? v[1] : v[0];
+		v[0] = keep + hds_shfl_xor(send, 8);
+	}
+	v[0] += hds_shfl_xor(v[0], 4);
+	v[0] += hds_shfl_xor(v[0], 2);
+	v[0] += hds_shfl_xor(v[0], 1);
+	return v[0];
+}
+
+/* ------------------------------------------------------------------------------------------- */
+/* Split-bf16 MFMA. CDNA4 has no TF32 matrix path, so an fp32 operand x is carried as           */
+/* hi = bf16(x) and lo = bf16(x - hi) (both round-to-nearest-even) and a product as             */
+/* hi*hi + hi*lo + lo*hi: three v_mfma_f32_16x16x32_bf16 with fp32 accumulation, relative error */
+/* about 2^-16 per product, against TF32's 2^-11. One packed dword per element holds             */
+/* hi (bits 0-15) and lo (bits 16-31), so LDS stores one word per operand element.              */
+/* ------------------------------------------------------------------------------------------- */
+
+typedef __bf16 hds_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float hds_f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t hds_u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ static inline uint32_t hds_bf16_bits(__bf16 h) { return (uint32_t)__builtin_bit_cast(unsigned short, h); }
+
+__device__ static inline uint32_t hds_split_pack(float x) {
+	const __bf16 hi = (__bf16)x;
+	const __bf16 lo = (__bf16)(x - (float)hi);
+	return hds_bf16_bits(hi) | (hds_bf16_bits(lo) << 16);
+}
+
+/* Eight packed words -> the hi and lo bf16x8 operands of one MFMA. */
+__device__ static inline void hds_unpack8(const uint32_t d[8], hds_bf16x8& hi, hds_bf16x8& lo) {
+	hds_u32x4 h, l;
+#pragma unroll
+	for (int i = 0; i < 4; i++) {
+		/* bytes 0,1 of d[2i] and d[2i+1] -> hi pair; bytes 2,3 -> lo pair */
+		h[i] = __builtin_amdgcn_perm(d[2 * i + 1], d[2 * i], 0x05040100u);
+		l[i] = __builtin_amdgcn_perm(d[2 * i + 1], d[2 * i], 0x07060302u);
+	}
+	hi = __builtin_bit_cast(hds_bf16x8, h);
+	lo = __builtin_bit_cast(hds_bf16x8, l);
+}
+
+/* acc += A * B with A, B given as split-bf16 pairs (small terms first). */
+__device__ static inline hds_f32x4 hds_mfma_split(const hds_bf16x8& a_hi, const hds_bf16x8& a_lo,
+												  const hds_bf16x8& b_hi, const hds_bf16x8& b_lo,
+												  hds_f32x4 acc) {
+	acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_lo, b_hi, acc, 0, 0, 0);
+	acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_hi, b_lo, acc, 0, 0, 0);
+	acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_hi, b_hi, acc, 0, 0, 0);
+	return acc;
+}
+
+/* ------------------------------------------------------------------------------------------- */
+/* Blend helpers shared by the forward and backward tile walks.                                 */
+/* ------------------------------------------------------------------------------------------- */
+
+/* Conservative culling box of one gaussian: the alpha extent widened by 0.1% + 0.01 px so
+ * rounding differences in the per-pixel exp never cull a gaussian some pixel still accepts; a
+ * degenerate (NaN) extent keeps the gaussian (features.cu:8-17 does the same). */
+__device__ static inline float4 hds_cull_box(float2 mean, float4 conic_op) {
+	float ex, ey;
+	hds_alpha_extent(conic_op.x, conic_op.y, conic_op.z, conic_op.w, &ex, &ey);
+	ex = ex * 1.001f + 0.01f;
+	ey = ey * 1.001f + 0.01f;
+	if (!(ex >= 0.0f)) ex = 1e30f;
+	if (!(ey >= 0.0f)) ey = 1e30f;
+	return make_float4(mean.x - ex, mean.x + ex, mean.y - ey, mean.y + ey);
+}
+
+/* Does the box reach the rectangle [x0, x1] x [y0, y1] of pixel centres? */
+__device__ static inline bool hds_box_hits(float4 box, float x0, float x1, float y0, float y1) {
+	return box.y >= x0 && box.x <= x1 && box.w >= y0 && box.z <= y1;
+}
+
+/* Raw alpha of a gaussian at a pixel centre, forward.cu:197-208; G and the offsets are returned
+ * for the backward. */
+__device__ static inline float hds_raw_alpha(float px, float py, float2 mean, float4 conic_op, float& G,
+											 float& dx, float& dy) {
+	dx = px - mean.x;
+	dy = py - mean.y;
+	const float m = dx * (conic_op.x * dx + conic_op.y * dy) + dy * (conic_op.y * dx + conic_op.z * dy);
+	G = __expf(-0.5f * m);
+	return conic_op.w * G;
+}
+
+#endif /* HDS_INTERNAL_H */

@@ -1,0 +1,136 @@
+"""Tile-binned alpha blending of projected gaussians into RGB and C-channel feature images.
+
+Mirrors gaussian_splatting/rasterizer/__init__.py of the reference: the same `rasterize` signature and
+return values, the `RasterizeGaussians` autograd node, the `FEATURE_SLICE_WIDTH` knob and
+`_get_rasterizer()`, which here returns the ctypes binding of the HIP library instead of a JIT-built
+CUDA extension. The forward renders RGB and features in one tile walk and the backward replays both
+in one back-to-front walk.
+"""
+from __future__ import annotations
+
+from typing import Any
+
+import torch
+
+from gaussian_splatting.rasterizer._native import HipRasterizer, default_slice_width
+from gaussian_splatting.rasterizer.projection import project_gaussians  # noqa: F401
+
+_rasterizer_module: Any | None = None
+
+# Channels each feature backward work-group owns (32, 64 or 128, dividing C). None picks
+# min(C, 64), which keeps the backward at two waves per SIMD.
+FEATURE_SLICE_WIDTH: int | None = None
+
+
+def _get_rasterizer() -> HipRasterizer:
+    """Loads the HIP library on first use and caches the binding (rasterizer/__init__.py:15-54).
+
+    Returns:
+        An object exposing the reference extension's ten functions (rasterize, rasterize_backward,
+        rasterize_features, rasterize_features_backward, eval_sh, eval_sh_backward_adam, ssim_forward,
+        ssim_backward, project_gaussians, project_gaussians_backward) and the fused bin / render /
+        render_backward calls.
+    """
+    global _rasterizer_module
+    if _rasterizer_module is None:
+        _rasterizer_module = HipRasterizer()
+    return _rasterizer_module
+
+
+class RasterizeGaussians(torch.autograd.Function):
+    """Autograd node wrapping the HIP tile binning and alpha blend (rasterizer/__init__.py:57-165)."""
+
+    @staticmethod
+    def forward(ctx, means2D, depths, radii, conics, colors, opacities, background, features, image_width,
+                image_height):
+        """Bins, then renders the image (and the feature image when features are given) in one walk.
+
+        Returns:
+            [H, W, 3] image, followed by the [H, W, D] feature image when features are given.
+        """
+        ext = _get_rasterizer()
+        width, height = int(image_width), int(image_height)
+        means2D = means2D.contiguous()
+        values_sorted, tile_ranges, conic, color_opacity = ext.bin(
+            means2D, depths.contiguous(), radii.contiguous(), conics.contiguous(), colors.contiguous(),
+            opacities.contiguous(), width, height)
+        if features is not None:
+            features = features.contiguous()
+        image, feature_image, final_T, n_contrib = ext.render(
+            means2D, conic, color_opacity, values_sorted, tile_ranges, width, height, background.contiguous(),
+            features)
+        ctx.image_size = (width, height)
+        ctx.save_for_backward(means2D, conic, color_opacity, values_sorted, tile_ranges, final_T, n_contrib,
+                              background, features)
+        if features is None:
+            return image
+        return image, feature_image
+
+    @staticmethod
+    def backward(ctx, grad_image, grad_features=None):
+        """Replays each pixel's list back to front for RGB and features at once.
+
+        Returns:
+            Gradients for means2D, conics, colors, opacities and features; None for depths, radii,
+            background and the image size.
+        """
+        means2D, conic, color_opacity, values_sorted, tile_ranges, final_T, n_contrib, background, features = (
+            ctx.saved_tensors)
+        width, height = ctx.image_size
+        # Frozen features still shape the geometry gradients, so the feature term runs whenever any of
+        # means2D, conics, opacities or features needs a gradient (rasterizer/__init__.py:150-152).
+        feature_term = (features is not None and grad_features is not None
+                        and any(ctx.needs_input_grad[i] for i in (0, 3, 5, 7)))
+        g_means, g_conics, g_colors, g_opac, g_feat = _get_rasterizer().render_backward(
+            means2D, conic, color_opacity, values_sorted, tile_ranges, final_T, n_contrib, width, height,
+            grad_image=grad_image.contiguous(), background=background,
+            features=features if feature_term else None,
+            grad_feature_image=grad_features.contiguous() if feature_term else None,
+            slice_width=(FEATURE_SLICE_WIDTH or default_slice_width(features.shape[1])) if feature_term else None,
+            want_feature_grad=feature_term and ctx.needs_input_grad[7])
+        return g_means, None, None, g_conics, g_colors, g_opac, None, g_feat, None, None
+
+
+def rasterize(
+    means2D: torch.Tensor,
+    depths: torch.Tensor,
+    radii: torch.Tensor,
+    conics: torch.Tensor,
+    colors: torch.Tensor,
+    opacities: torch.Tensor,
+    image_width: int,
+    image_height: int,
+    background: torch.Tensor | None = None,
+    features: torch.Tensor | None = None,
+) -> torch.Tensor | tuple[torch.Tensor, torch.Tensor]:
+    """Alpha blends projected gaussians into an image, front to back, on 16x16 pixel tiles.
+
+    Same contract as the reference's rasterize (rasterizer/__init__.py:168-211).
+
+    Args:
+        means2D: [N, 2] centers in pixels.
+        depths: [N] camera space depths, used to sort.
+        radii: [N] footprint radii in pixels, 0 for culled gaussians.
+        conics: [N, 3] inverse 2D covariances as (xx, xy, yy).
+        colors: [N, 3] RGB.
+        opacities: [N, 1] in (0, 1).
+        image_width: Output width in pixels.
+        image_height: Output height in pixels.
+        background: [3] RGB shown wherever the gaussians do not cover, black by default.
+        features: [N, D] channels blended with the same weights over a zero background, with D one of
+            32, 64, 128, 256 or 512. None renders RGB only.
+
+    Returns:
+        [H, W, 3] rendered image, or (image, [H, W, D] feature image) when features are given.
+    """
+    n = means2D.shape[0]
+    assert means2D.shape == (n, 2)
+    assert depths.shape == (n,) and radii.shape == (n,)
+    assert conics.shape == (n, 3) and colors.shape == (n, 3)
+    assert opacities.shape == (n, 1)
+    if background is None:
+        background = torch.zeros(3, device=means2D.device, dtype=means2D.dtype)
+    assert background.shape == (3,)
+    assert features is None or (features.ndim == 2 and features.shape[0] == n)
+    return RasterizeGaussians.apply(means2D, depths, radii, conics, colors, opacities, background, features,
+                                    image_width, image_height)

@@ -1,0 +1,339 @@
+"""ctypes binding of libhds_rasterizer.so (include/hds_rasterizer.h) behind the reference's extension API.
+
+`HipRasterizer` exposes the ten functions of the reference's torch extension "gaussian_rasterizer"
+(gaussian_splatting/rasterizer/bindings.cpp:4-42) with the same names, argument order and return
+tuples, taking and returning torch tensors. Outputs are allocated here with the torch caching
+allocator and raw pointers go to the C ABI together with torch's current HIP stream; the library
+itself never allocates. On top of those ten it offers the fused calls the autograd functions use:
+`bin` (binning only), `render` (RGB + features in one tile walk) and `render_backward`.
+
+There is no CPU path: a missing library or a tensor off the GPU raises RuntimeError.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+from pathlib import Path
+
+import torch
+
+_PACKAGE_ROOT = Path(__file__).resolve().parents[2]
+LIBRARY_PATH = Path(os.environ.get("HDS_LIBRARY", _PACKAGE_ROOT / "lib" / "libhds_rasterizer.so"))
+
+SUPPORTED_CHANNELS = (32, 64, 128, 256, 512)
+TILE = 16
+
+_i64, _i32, _f32, _f64, _vp, _sz = (ctypes.c_int64, ctypes.c_int, ctypes.c_float, ctypes.c_double,
+                                    ctypes.c_void_p, ctypes.c_size_t)
+
+# name -> (restype, argtypes), exactly the prototypes of include/hds_rasterizer.h.
+_CAMERA = [_f32, _f32, _f32, _f32, _i32, _i32, _f32, _f32, _f32]
+PROTOTYPES = {
+    "hds_last_error": (ctypes.c_char_p, []),
+    "hds_abi_version": (_i32, []),
+    "hds_project_gaussians": (_i32, [_i64, _vp, _vp, _vp, _vp, _vp] + _CAMERA + [_vp, _vp, _vp, _vp, _vp]),
+    "hds_project_gaussians_backward": (_i32, [_i64, _vp, _vp, _vp, _vp, _vp, _vp] + _CAMERA + [_vp, _vp, _vp, _vp]),
+    "hds_eval_sh": (_i32, [_i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "hds_eval_sh_backward_adam": (_i32, [_i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                         _f64, _f64, _f64, _f64, _f64, _vp, _vp]),
+    "hds_bin_workspace_bytes": (_sz, [_i64, _i32, _i32]),
+    "hds_bin_count": (_i32, [_i64, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _vp, _vp, _vp, _sz,
+                             ctypes.POINTER(ctypes.c_int64), _vp]),
+    "hds_pairs_workspace_bytes": (_sz, [_i64, _i32, _i32]),
+    "hds_bin_emit": (_i32, [_i64, _i64, _i32, _i32, _vp, _vp, _sz, _vp, _vp, _vp]),
+    "hds_render": (_i32, [_i64, _i32, _i32, _i32, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                          _vp]),
+    "hds_render_backward": (_i32, [_i64, _i32, _i32, _i32, _i32, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp,
+                                   _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "hds_ssim_forward": (_i32, [_i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "hds_ssim_backward": (_i32, [_i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+}
+
+_lib: ctypes.CDLL | None = None
+
+
+def load_library() -> ctypes.CDLL:
+    """Loads the HIP library once; raises RuntimeError if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIBRARY_PATH.exists():
+        raise RuntimeError(
+            f"HIP rasterizer library not found at {LIBRARY_PATH}; build it with "
+            "`python -c 'import __graft_entry__; __graft_entry__.build()'` (or make -C high-dimensional-splatting_amd)")
+    lib = ctypes.CDLL(str(LIBRARY_PATH))
+    for name, (restype, argtypes) in PROTOTYPES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    _lib = lib
+    return lib
+
+
+def _check(status: int) -> None:
+    if status != 0:
+        raise RuntimeError(load_library().hds_last_error().decode(errors="replace"))
+
+
+def _ptr(t: torch.Tensor | None):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(device: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _dev(t: torch.Tensor, name: str) -> torch.Tensor:
+    """The reference's TORCH_CHECK(is_cuda / is_contiguous), plus float32 and 16-byte alignment."""
+    if not t.is_cuda:
+        raise RuntimeError(f"{name} must be a CUDA (HIP) tensor")
+    if t.dtype not in (torch.float32, torch.int32):
+        raise RuntimeError(f"{name} must be float32 or int32, got {t.dtype}")
+    if not t.is_contiguous() or t.data_ptr() % 16:
+        t = t.contiguous() if not t.is_contiguous() else t.clone()
+    return t
+
+
+class HipRasterizer:
+    """The reference extension's ten functions (bindings.cpp:4-42) on the HIP library, plus fused calls."""
+
+    def __init__(self) -> None:
+        self.lib = load_library()
+
+    # -- projection ---------------------------------------------------------------------------
+
+    def project_gaussians(self, means, scales, quats, opacities, world_to_camera, fx, fy, cx, cy, width, height,
+                          near_plane, low_pass, fov_scale):
+        """projection.cu:210-231: returns (means2D [N,2], depths [N], radii [N], conics [N,3])."""
+        means, scales, quats = _dev(means, "means"), _dev(scales, "scales"), _dev(quats, "quats")
+        opacities, pose = _dev(opacities, "opacities"), _dev(world_to_camera, "world_to_camera")
+        n = means.shape[0]
+        means2D = torch.empty((n, 2), device=means.device, dtype=torch.float32)
+        depths = torch.empty((n,), device=means.device, dtype=torch.float32)
+        radii = torch.empty((n,), device=means.device, dtype=torch.float32)
+        conics = torch.empty((n, 3), device=means.device, dtype=torch.float32)
+        with torch.cuda.device(means.device):
+            _check(self.lib.hds_project_gaussians(
+                n, _ptr(means), _ptr(scales), _ptr(quats), _ptr(opacities), _ptr(pose), float(fx), float(fy),
+                float(cx), float(cy), int(width), int(height), float(near_plane), float(low_pass), float(fov_scale),
+                _ptr(means2D), _ptr(depths), _ptr(radii), _ptr(conics), _stream(means.device)))
+        return means2D, depths, radii, conics
+
+    def project_gaussians_backward(self, grad_means2D, grad_conics, means, scales, quats, world_to_camera, fx, fy,
+                                   cx, cy, width, height, near_plane, low_pass, fov_scale):
+        """projection.cu:234-253: returns (grad_means, grad_scales, grad_quats)."""
+        gm, gc = _dev(grad_means2D, "grad_means2D"), _dev(grad_conics, "grad_conics")
+        means, scales, quats = _dev(means, "means"), _dev(scales, "scales"), _dev(quats, "quats")
+        pose = _dev(world_to_camera, "world_to_camera")
+        dm, ds, dq = torch.empty_like(means), torch.empty_like(scales), torch.empty_like(quats)
+        with torch.cuda.device(means.device):
+            _check(self.lib.hds_project_gaussians_backward(
+                means.shape[0], _ptr(gm), _ptr(gc), _ptr(means), _ptr(scales), _ptr(quats), _ptr(pose), float(fx),
+                float(fy), float(cx), float(cy), int(width), int(height), float(near_plane), float(low_pass),
+                float(fov_scale), _ptr(dm), _ptr(ds), _ptr(dq), _stream(means.device)))
+        return dm, ds, dq
+
+    # -- spherical harmonics --------------------------------------------------------------------
+
+    def eval_sh(self, sh_dc, sh_rest, dirs, degree, radii):
+        """sh.cu:157-168: returns rgb [N,3]."""
+        sh_dc, sh_rest = _dev(sh_dc, "sh_dc"), _dev(sh_rest, "sh_rest")
+        dirs, radii = _dev(dirs, "dirs"), _dev(radii, "radii")
+        n = sh_dc.shape[0]
+        rgb = torch.empty((n, 3), device=sh_dc.device, dtype=torch.float32)
+        with torch.cuda.device(sh_dc.device):
+            _check(self.lib.hds_eval_sh(n, int(degree), _ptr(sh_dc), _ptr(sh_rest), _ptr(dirs), _ptr(radii),
+                                        _ptr(rgb), _stream(sh_dc.device)))
+        return rgb
+
+    def eval_sh_backward_adam(self, grad_rgb, sh_dc, sh_rest, dirs, degree, radii, m_dc, v_dc, m_rest, v_rest,
+                              step_dc, step_rest, lr_dc, lr_rest, beta1, beta2, eps):
+        """sh.cu:171-190: steps sh_dc / sh_rest and their moments in place, returns grad_dirs [N,3]."""
+        for t, name in ((sh_dc, "sh_dc"), (sh_rest, "sh_rest"), (m_dc, "exp_avg"), (v_dc, "exp_avg_sq"),
+                        (m_rest, "exp_avg"), (v_rest, "exp_avg_sq"), (step_dc, "step"), (step_rest, "step")):
+            if not (t.is_cuda and t.is_contiguous() and t.dtype == torch.float32):
+                raise RuntimeError(f"{name} must be a contiguous float32 CUDA tensor (updated in place)")
+        grad_rgb, dirs, radii = _dev(grad_rgb, "grad_rgb"), _dev(dirs, "dirs"), _dev(radii, "radii")
+        grad_dirs = torch.empty_like(dirs)
+        with torch.cuda.device(sh_dc.device):
+            _check(self.lib.hds_eval_sh_backward_adam(
+                sh_dc.shape[0], int(degree), _ptr(grad_rgb), _ptr(sh_dc), _ptr(sh_rest), _ptr(dirs), _ptr(radii),
+                _ptr(m_dc), _ptr(v_dc), _ptr(m_rest), _ptr(v_rest), _ptr(step_dc), _ptr(step_rest), float(lr_dc),
+                float(lr_rest), float(beta1), float(beta2), float(eps), _ptr(grad_dirs), _stream(sh_dc.device)))
+        return grad_dirs
+
+    # -- binning + blend --------------------------------------------------------------------------
+
+    def bin(self, means2D, depths, radii, conics, colors, opacities, width, height):
+        """Binning of rasterize (forward.cu:284-404).
+
+        Returns (values_sorted [P] int32, tile_ranges [T,2] int32, conic4 [N,4], color_opacity4 [N,4]).
+        """
+        means2D, depths, radii = _dev(means2D, "means2D"), _dev(depths, "depths"), _dev(radii, "radii")
+        conics, opacities = _dev(conics, "conics"), _dev(opacities, "opacities")
+        colors = None if colors is None else _dev(colors, "colors")
+        dev = means2D.device
+        n = means2D.shape[0]
+        width, height = int(width), int(height)
+        tiles = ((width + TILE - 1) // TILE) * ((height + TILE - 1) // TILE)
+        conic4 = torch.empty((n, 4), device=dev, dtype=torch.float32)
+        color_opacity4 = torch.empty((n, 4), device=dev, dtype=torch.float32)
+        tile_ranges = torch.empty((tiles, 2), device=dev, dtype=torch.int32)
+        with torch.cuda.device(dev):
+            stream = _stream(dev)
+            ws = torch.empty(self.lib.hds_bin_workspace_bytes(n, width, height), device=dev, dtype=torch.uint8)
+            pairs = ctypes.c_int64(0)
+            _check(self.lib.hds_bin_count(n, _ptr(means2D), _ptr(depths), _ptr(radii), _ptr(conics), _ptr(colors),
+                                          _ptr(opacities), width, height, _ptr(conic4), _ptr(color_opacity4),
+                                          _ptr(ws), ws.numel(), ctypes.byref(pairs), stream))
+            p = int(pairs.value)
+            values_sorted = torch.empty((p,), device=dev, dtype=torch.int32)
+            pws = torch.empty(self.lib.hds_pairs_workspace_bytes(p, width, height) if p else 0, device=dev,
+                              dtype=torch.uint8)
+            _check(self.lib.hds_bin_emit(n, p, width, height, _ptr(ws), _ptr(pws), pws.numel(), _ptr(values_sorted),
+                                         _ptr(tile_ranges), stream))
+        return values_sorted, tile_ranges, conic4, color_opacity4
+
+    def render(self, means2D, conic4, color_opacity4, values_sorted, tile_ranges, width, height, background=None,
+               features=None, rgb=True):
+        """One front-to-back tile walk (forward.cu:141-237 + features.cu:116-282).
+
+        Returns (image [H,W,3] or None, feature_image [H,W,C] or None, final_T [H,W], n_contrib [H,W]).
+        """
+        dev = means2D.device
+        width, height = int(width), int(height)
+        means2D = _dev(means2D, "means2D")
+        channels = 0
+        if features is not None:
+            features = _dev(features, "features")
+            if features.dtype != torch.float32:
+                raise RuntimeError("features must be a contiguous float32 CUDA tensor")
+            channels = int(features.shape[1])
+            if channels not in SUPPORTED_CHANNELS:
+                raise RuntimeError(f"features must have 32, 64, 128, 256 or 512 channels, got {channels}")
+        image = torch.empty((height, width, 3), device=dev, dtype=torch.float32) if rgb else None
+        feature_image = (torch.empty((height, width, channels), device=dev, dtype=torch.float32)
+                         if features is not None else None)
+        final_T = torch.empty((height, width), device=dev, dtype=torch.float32)
+        n_contrib = torch.empty((height, width), device=dev, dtype=torch.int32)
+        if rgb and background is None:
+            background = torch.zeros(3, device=dev, dtype=torch.float32)
+        with torch.cuda.device(dev):
+            _check(self.lib.hds_render(
+                means2D.shape[0], width, height, channels, _ptr(tile_ranges), _ptr(values_sorted),
+                values_sorted.numel(), _ptr(means2D), _ptr(conic4), _ptr(color_opacity4) if rgb else None,
+                _ptr(background) if rgb else None, _ptr(features), _ptr(image), _ptr(final_T), _ptr(n_contrib),
+                _ptr(feature_image), _stream(dev)))
+        return image, feature_image, final_T, n_contrib
+
+    def render_backward(self, means2D, conic4, color_opacity4, values_sorted, tile_ranges, final_T, n_contrib,
+                        width, height, grad_image=None, background=None, features=None, grad_feature_image=None,
+                        slice_width=None, want_feature_grad=True):
+        """One back-to-front walk (backward.cu:7-164 + features.cu:350-542).
+
+        Returns (grad_means2D [N,2], grad_conics [N,3], grad_colors [N,3] or None, grad_opacities [N,1],
+        grad_features [N,C] or None).
+        """
+        dev = means2D.device
+        n = means2D.shape[0]
+        channels = 0 if features is None else int(features.shape[1])
+        if features is not None:
+            features = _dev(features, "features")
+            grad_feature_image = _dev(grad_feature_image, "grad_feature_image")
+            slice_width = int(slice_width or default_slice_width(channels))
+        if grad_image is not None:
+            grad_image = _dev(grad_image, "grad_image")
+            if background is None:
+                background = torch.zeros(3, device=dev, dtype=torch.float32)
+        f32 = dict(device=dev, dtype=torch.float32)
+        g_means = torch.empty((n, 2), **f32)
+        g_conics = torch.empty((n, 3), **f32)
+        g_colors = torch.empty((n, 3), **f32) if grad_image is not None else None
+        g_opac = torch.empty((n, 1), **f32)
+        g_feat = torch.empty((n, channels), **f32) if features is not None and want_feature_grad else None
+        with torch.cuda.device(dev):
+            _check(self.lib.hds_render_backward(
+                n, int(width), int(height), channels, slice_width or 0, _ptr(tile_ranges), _ptr(values_sorted),
+                values_sorted.numel(), _ptr(_dev(means2D, "means2D")), _ptr(conic4), _ptr(color_opacity4),
+                _ptr(background), _ptr(final_T), _ptr(n_contrib), _ptr(grad_image), _ptr(features),
+                _ptr(grad_feature_image), _ptr(g_means), _ptr(g_conics), _ptr(g_colors), _ptr(g_opac), _ptr(g_feat),
+                _stream(dev)))
+        return g_means, g_conics, g_colors, g_opac, g_feat
+
+    # -- the reference extension's rasterize* entry points --------------------------------------
+
+    def rasterize(self, means2D, depths, radii, conics, colors, opacities, background, image_width, image_height):
+        """forward.cu:239-435: (image, final_T, n_contrib, values_sorted, tile_ranges, conic, color_opacity)."""
+        values, ranges, conic4, color_opacity4 = self.bin(means2D, depths, radii, conics, colors, opacities,
+                                                          image_width, image_height)
+        image, _, final_T, n_contrib = self.render(means2D, conic4, color_opacity4, values, ranges, image_width,
+                                                   image_height, _dev(background, "background"))
+        return image, final_T, n_contrib, values, ranges, conic4, color_opacity4
+
+    def rasterize_backward(self, grad_image, means2D, conic, color_opacity, values_sorted, tile_ranges,
+                           final_transmittance, n_contrib, background, image_width, image_height):
+        """backward.cu:166-226: (grad_means2D, grad_conics, grad_colors, grad_opacities)."""
+        gm, gc, gcol, gop, _ = self.render_backward(means2D, conic, color_opacity, values_sorted, tile_ranges,
+                                                    final_transmittance, n_contrib, image_width, image_height,
+                                                    grad_image=grad_image, background=background)
+        return gm, gc, gcol, gop
+
+    def rasterize_features(self, features, means2D, conic, color_opacity, values_sorted, tile_ranges, image_width,
+                           image_height):
+        """features.cu:299-346: (feature_image, feature_T, feature_contrib)."""
+        _, feature_image, final_T, n_contrib = self.render(means2D, conic, color_opacity, values_sorted,
+                                                           tile_ranges, image_width, image_height,
+                                                           features=features, rgb=False)
+        return feature_image, final_T, n_contrib
+
+    def rasterize_features_backward(self, grad_output, features, means2D, conic, color_opacity, values_sorted,
+                                    tile_ranges, final_transmittance, n_contrib, image_width, image_height,
+                                    slice_width):
+        """features.cu:561-616: (grad_features, grad_means2D, grad_conics, grad_opacities)."""
+        gm, gc, _, gop, gf = self.render_backward(means2D, conic, color_opacity, values_sorted, tile_ranges,
+                                                  final_transmittance, n_contrib, image_width, image_height,
+                                                  features=features, grad_feature_image=grad_output,
+                                                  slice_width=slice_width)
+        return gf, gm, gc, gop
+
+    # -- SSIM -------------------------------------------------------------------------------------
+
+    def ssim_forward(self, rendered, gt):
+        """ssim.cu:116-148: (ssim_map, d_mu, d_aa, d_ab), each [H,W,3]."""
+        rendered, gt = _dev(rendered, "rendered"), _dev(gt, "gt")
+        if rendered.dim() != 3 or rendered.shape[2] != 3 or rendered.shape != gt.shape:
+            raise RuntimeError("ssim inputs must both be [H, W, 3]")
+        h, w = rendered.shape[0], rendered.shape[1]
+        outs = [torch.empty_like(rendered) for _ in range(4)]
+        with torch.cuda.device(rendered.device):
+            _check(self.lib.hds_ssim_forward(h, w, _ptr(rendered), _ptr(gt), *[_ptr(o) for o in outs],
+                                             _stream(rendered.device)))
+        return tuple(outs)
+
+    def ssim_backward(self, grad_mean, rendered, gt, d_mu, d_aa, d_ab):
+        """ssim.cu:151-177: gradient with respect to rendered, [H,W,3]."""
+        rendered, gt = _dev(rendered, "rendered"), _dev(gt, "gt")
+        grad_mean = _dev(grad_mean.reshape(1).to(torch.float32), "grad_mean")
+        grad = torch.empty_like(rendered)
+        h, w = rendered.shape[0], rendered.shape[1]
+        with torch.cuda.device(rendered.device):
+            _check(self.lib.hds_ssim_backward(h, w, _ptr(grad_mean), _ptr(rendered), _ptr(gt), _ptr(_dev(d_mu, "d_mu")),
+                                              _ptr(_dev(d_aa, "d_aa")), _ptr(_dev(d_ab, "d_ab")), _ptr(grad),
+                                              _stream(rendered.device)))
+        return grad
+
+
+def default_slice_width(channels: int) -> int:
+    """Channels per backward work-group when FEATURE_SLICE_WIDTH is None: the widest supported slice
+    whose two dL/dF register layouts still leave room for two waves per SIMD."""
+    return min(channels, 64)
+
+
+def pairs_upper_bound_bytes(num_pairs: int) -> int:
+    """Bytes the pair workspace needs for num_pairs pairs, for capacity planning."""
+    return int(load_library().hds_pairs_workspace_bytes(num_pairs, 1, 1)) if num_pairs else 0
+
+
+def tile_count(width: int, height: int) -> int:
+    return math.ceil(width / TILE) * math.ceil(height / TILE)

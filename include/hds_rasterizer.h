@@ -1,0 +1,156 @@
+/*
+ * C ABI of the MI355X-native high-dimensional splatting rasterizer (libhds_rasterizer.so).
+ *
+ * These entry points replace the ten functions of the reference's torch extension
+ * "gaussian_rasterizer" (gaussian_splatting/rasterizer/bindings.cpp:4-42, api.h:4-119). They take
+ * plain device pointers, sizes and a HIP stream, and hold no torch types, so any host language can
+ * bind them (the Python mirror of the reference's autograd API does so with ctypes).
+ *
+ * Conventions
+ *   - Every pointer is device memory on the current HIP device unless stated, fp32 or int32,
+ *     contiguous, in the reference's layouts: means2D [N,2], conics [N,3] as (xx, xy, yy),
+ *     colors [N,3], opacities [N] (the reference's [N,1]), images [H,W,3], feature images
+ *     [H,W,C], tile_ranges [T,2] with T = ceil(W/16) * ceil(H/16).
+ *   - conic4 [N,4] = (a, b, c, opacity) and color_opacity4 [N,4] = (r, g, b, opacity) are the
+ *     packed per-gaussian records the binning call writes and every render call reads; they play
+ *     the role of the reference's `conic` / `color_opacity` tuple members (forward.cu:274-276).
+ *   - Work is enqueued on `stream` (a hipStream_t; NULL is the default stream). Only
+ *     hds_bin_count blocks the host: it reads the pair count P back once, as forward.cu:321-325.
+ *   - Returns HDS_OK (0) or an error status; hds_last_error() then holds a message for the
+ *     calling thread. Invalid arguments are rejected before anything is enqueued.
+ *   - The library never allocates device memory: scratch comes in as caller-owned workspaces
+ *     whose sizes the *_workspace_bytes queries give.
+ *   - Gradient outputs of the backward calls are zeroed by the library before accumulation.
+ */
+#ifndef HDS_RASTERIZER_H
+#define HDS_RASTERIZER_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HDS_ABI_VERSION 1
+
+#if defined(__GNUC__)
+#define HDS_API __attribute__((visibility("default")))
+#else
+#define HDS_API
+#endif
+
+typedef void* hds_stream_t; /* hipStream_t */
+
+/* Status codes. */
+#define HDS_STATUS_OK 0
+#define HDS_STATUS_INVALID_ARGUMENT 1
+#define HDS_STATUS_RUNTIME_ERROR 2
+
+/* Message of the last failed call on this thread (never NULL). */
+HDS_API const char* hds_last_error(void);
+
+/* HDS_ABI_VERSION of the loaded library. */
+HDS_API int hds_abi_version(void);
+
+/* ---- projection: replaces project_gaussians / project_gaussians_backward ------------------- */
+
+/* projection.cu:210-231 (project_gaussians). world_to_camera is a device [4,4] row-major matrix.
+ * Outputs means2D [N,2], depths [N], radii [N] (0 for culled), conics [N,3]. */
+HDS_API int hds_project_gaussians(int64_t n, const float* means, const float* scales, const float* quats,
+						  const float* opacities, const float* world_to_camera, float fx, float fy,
+						  float cx, float cy, int width, int height, float near_plane,
+						  float low_pass, float fov_scale, float* means2D, float* depths,
+						  float* radii, float* conics, hds_stream_t stream);
+
+/* projection.cu:234-253 (project_gaussians_backward). */
+HDS_API int hds_project_gaussians_backward(int64_t n, const float* grad_means2D, const float* grad_conics,
+								   const float* means, const float* scales, const float* quats,
+								   const float* world_to_camera, float fx, float fy, float cx,
+								   float cy, int width, int height, float near_plane,
+								   float low_pass, float fov_scale, float* grad_means,
+								   float* grad_scales, float* grad_quats, hds_stream_t stream);
+
+/* ---- spherical harmonics: replaces eval_sh / eval_sh_backward_adam ------------------------- */
+
+/* sh.cu:157-168 (eval_sh). sh_dc [N,1,3], sh_rest [N,15,3], dirs [N,3], radii [N] -> rgb [N,3]. */
+HDS_API int hds_eval_sh(int64_t n, int degree, const float* sh_dc, const float* sh_rest, const float* dirs,
+				const float* radii, float* rgb, hds_stream_t stream);
+
+/* sh.cu:171-190 (eval_sh_backward_adam_host). Steps sh_dc, sh_rest and their Adam moments in
+ * place with the device step counters step_dc / step_rest (0-d fp32, already incremented);
+ * writes grad_dirs [N,3]. */
+HDS_API int hds_eval_sh_backward_adam(int64_t n, int degree, const float* grad_rgb, float* sh_dc,
+							  float* sh_rest, const float* dirs, const float* radii, float* m_dc,
+							  float* v_dc, float* m_rest, float* v_rest, const float* step_dc,
+							  const float* step_rest, double lr_dc, double lr_rest, double beta1,
+							  double beta2, double eps, float* grad_dirs, hds_stream_t stream);
+
+/* ---- binning: replaces the binning half of rasterize (forward.cu:239-405) ------------------ */
+
+/* Bytes of the per-gaussian workspace hds_bin_count fills and hds_bin_emit reads. */
+HDS_API size_t hds_bin_workspace_bytes(int64_t n, int width, int height);
+
+/* forward.cu:284-326: culls, packs conic4 / color_opacity4 (colors may be NULL), counts the
+ * tiles of each gaussian, orders the gaussians by depth and prefix-sums their counts. Writes the
+ * total pair count P to *num_pairs (host memory) after the one blocking device-to-host read. */
+HDS_API int hds_bin_count(int64_t n, const float* means2D, const float* depths, const float* radii,
+				  const float* conics, const float* colors, const float* opacities, int width,
+				  int height, float* conic4, float* color_opacity4, void* workspace,
+				  size_t workspace_bytes, int64_t* num_pairs, hds_stream_t stream);
+
+/* Bytes of the per-pair workspace hds_bin_emit needs for P pairs. */
+HDS_API size_t hds_pairs_workspace_bytes(int64_t num_pairs, int width, int height);
+
+/* forward.cu:340-404: emits the (tile, gaussian) pairs, orders them by (tile, depth) keeping
+ * index order on ties, and builds the per-tile [start, end) ranges, (0, 0) when untouched.
+ * values_sorted [P] int32, tile_ranges [T,2] int32. */
+HDS_API int hds_bin_emit(int64_t n, int64_t num_pairs, int width, int height, const void* workspace,
+				 void* pairs_workspace, size_t pairs_workspace_bytes, int32_t* values_sorted,
+				 int32_t* tile_ranges, hds_stream_t stream);
+
+/* ---- blend forward: replaces render_gaussians (forward.cu:406-434) and rasterize_features
+ *      (features.cu:299-346) with one tile walk ------------------------------------------------ */
+
+/* Front-to-back blend of RGB (when image != NULL; background [3] required then) and of C
+ * feature channels (when features != NULL; C in {32, 64, 128, 256, 512}) with the same weights.
+ * final_T [H,W] and n_contrib [H,W] are always written. */
+HDS_API int hds_render(int64_t n, int width, int height, int channels, const int32_t* tile_ranges,
+			   const int32_t* values_sorted, int64_t num_pairs, const float* means2D,
+			   const float* conic4, const float* color_opacity4, const float* background,
+			   const float* features, float* image, float* final_T, int32_t* n_contrib,
+			   float* feature_image, hds_stream_t stream);
+
+/* ---- blend backward: replaces rasterize_backward (backward.cu:166-226) and
+ *      rasterize_features_backward (features.cu:561-616) with one back-to-front walk ----------- */
+
+/* grad_image [H,W,3] (NULL: no RGB term; grad_colors may then be NULL) and, when features !=
+ * NULL, grad_feature_image [H,W,C] with slice_width in {32, 64, 128} dividing C (the channels one
+ * work-group owns). grad_features may be NULL (frozen features still shape the geometry
+ * gradients). Outputs grad_means2D [N,2], grad_conics [N,3], grad_colors [N,3],
+ * grad_opacities [N], grad_features [N,C]; all zeroed here first. */
+HDS_API int hds_render_backward(int64_t n, int width, int height, int channels, int slice_width,
+						const int32_t* tile_ranges, const int32_t* values_sorted, int64_t num_pairs,
+						const float* means2D, const float* conic4, const float* color_opacity4,
+						const float* background, const float* final_T, const int32_t* n_contrib,
+						const float* grad_image, const float* features,
+						const float* grad_feature_image, float* grad_means2D, float* grad_conics,
+						float* grad_colors, float* grad_opacities, float* grad_features,
+						hds_stream_t stream);
+
+/* ---- SSIM: replaces ssim_forward / ssim_backward ------------------------------------------- */
+
+/* ssim.cu:116-148. rendered, gt [H,W,3] -> ssim_map, d_mu, d_aa, d_ab [H,W,3]. */
+HDS_API int hds_ssim_forward(int height, int width, const float* rendered, const float* gt,
+					 float* ssim_map, float* d_mu, float* d_aa, float* d_ab, hds_stream_t stream);
+
+/* ssim.cu:151-177. grad_mean is a device scalar; writes grad_rendered [H,W,3]. */
+HDS_API int hds_ssim_backward(int height, int width, const float* grad_mean, const float* rendered,
+					  const float* gt, const float* d_mu, const float* d_aa, const float* d_ab,
+					  float* grad_rendered, hds_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HDS_RASTERIZER_H */

@@ -1,0 +1,368 @@
+"""HIP path vs the CPU oracle on identical seeded inputs, through the C ABI.
+
+Bars: integer work (visibility, tile counts, sorted pairs, tile ranges) bit-exact; projection
+outputs bit-exact (both sides round every operation identically); images within the reference's
+tolerances (test_render.py:29-58: RGB max 2e-3 / p99 1e-4, features max 1e-3 / p99 5e-4); gradients
+within assert_grads_close (rtol 1e-3, atol 1e-4 * max|want|, < 0.1% outside, max error 2e-3 * max).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from gaussian_splatting.rasterizer import _get_rasterizer, rasterize
+from gaussian_splatting.rasterizer.projection import JACOBIAN_FOV_SCALE, LOW_PASS, NEAR_PLANE
+from tests.scenes import camera, flat_scene, gaussians, synthetic_config
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def np_(t):
+    return t.detach().cpu().numpy()
+
+
+def assert_image_close(got, want, max_error=2e-3, max_perc_99=1e-4):
+    diff = np.abs(np.asarray(got, np.float64) - np.asarray(want, np.float64)).ravel()
+    if diff.size == 0:
+        return
+    p99 = np.sort(diff)[max(0, math.ceil(0.99 * diff.size) - 1)]
+    assert diff.max() < max_error and p99 < max_perc_99, f"max {diff.max():.2e}, 99th {p99:.2e}"
+
+
+def assert_grads_close(names, grads, wants):
+    for name, got, want in zip(names, grads, wants):
+        got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+        assert got.shape == want.shape, f"{name}: shape {got.shape} vs {want.shape}"
+        if want.size == 0:
+            continue
+        scale = np.abs(want).max()
+        bad = ~np.isclose(got, want, rtol=1e-3, atol=1e-4 * scale)
+        assert bad.mean() < 1e-3, f"{name}: {bad.sum()} of {bad.size} outside tolerance"
+        err = np.abs(got - want).max()
+        assert err <= 2e-3 * scale, f"{name}: max error {err:.2e} of max {scale:.2e}"
+
+
+def project_both(wl_means, wl_scales, wl_quats, wl_opac, cam, w2c=None):
+    """Projects on the GPU and in the oracle; returns (gpu tuple, oracle tuple)."""
+    w2c = torch.eye(4) if w2c is None else w2c
+    ext = _get_rasterizer()
+    gpu = ext.project_gaussians(wl_means.to(DEV), wl_scales.to(DEV), wl_quats.to(DEV), wl_opac.to(DEV),
+                                w2c.to(DEV), cam["fx"], cam["fy"], cam["cx"], cam["cy"], cam["width"],
+                                cam["height"], NEAR_PLANE, LOW_PASS, JACOBIAN_FOV_SCALE)
+    cpu = oracle.project_forward(np_(wl_means), np_(wl_scales), np_(wl_quats), np_(wl_opac), np_(w2c), cam["fx"],
+                                 cam["fy"], cam["cx"], cam["cy"], cam["width"], cam["height"])
+    return gpu, cpu
+
+
+def scene(seed, n, width, height):
+    """Reference-style test scene projected by the HIP kernel: (means2D, depths, radii, conics, colors, opac)."""
+    g = gaussians(seed, n)
+    cam = camera(width, height)
+    (m2, d, r, c), _ = project_both(g["means"], g["scales"], g["quats"], g["opacities"], cam)
+    return m2, d, r, c, g["colors"].to(DEV), g["opacities"].to(DEV)
+
+
+# ---- projection -------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("index", [0, 1])
+def test_projection_is_bitwise_equal_to_oracle(index):
+    wl = synthetic_config(index, n=50_000)
+    gpu, cpu = project_both(wl.means, wl.scales, wl.quats, wl.opacities, wl.cam)
+    for name, g, c in zip(("means2D", "depths", "radii", "conics"), gpu, cpu):
+        np.testing.assert_array_equal(np_(g), c, err_msg=name)
+    assert (cpu[2] > 0).mean() > 0.5, "the scene should be mostly visible"
+
+
+def test_projection_with_rotated_camera_is_bitwise_equal():
+    g = gaussians(5, 4000)
+    angle = 0.3
+    w2c = torch.eye(4)
+    w2c[0, 0], w2c[0, 2], w2c[2, 0], w2c[2, 2] = math.cos(angle), math.sin(angle), -math.sin(angle), math.cos(angle)
+    w2c[:3, 3] = torch.tensor([0.2, -0.1, 0.5])
+    gpu, cpu = project_both(g["means"], g["scales"], g["quats"], g["opacities"], camera(160, 120), w2c)
+    for name, a, b in zip(("means2D", "depths", "radii", "conics"), gpu, cpu):
+        np.testing.assert_array_equal(np_(a), b, err_msg=name)
+
+
+def test_projection_backward_matches_oracle():
+    wl = synthetic_config(0, n=20_000)
+    cam = wl.cam
+    gen = torch.Generator().manual_seed(2)
+    gm = torch.randn(wl.n, 2, generator=gen)
+    gc = torch.randn(wl.n, 3, generator=gen)
+    ext = _get_rasterizer()
+    got = ext.project_gaussians_backward(gm.to(DEV), gc.to(DEV), wl.means.to(DEV), wl.scales.to(DEV),
+                                         wl.quats.to(DEV), torch.eye(4, device=DEV), cam["fx"], cam["fy"], cam["cx"],
+                                         cam["cy"], cam["width"], cam["height"], NEAR_PLANE, LOW_PASS,
+                                         JACOBIAN_FOV_SCALE)
+    want = oracle.project_backward(np_(gm), np_(gc), np_(wl.means), np_(wl.scales), np_(wl.quats), np.eye(4),
+                                   cam["fx"], cam["fy"], cam["cx"], cam["cy"], cam["width"], cam["height"])
+    assert_grads_close(("means", "scales", "quats"), [np_(t) for t in got], want)
+
+
+# ---- binning ----------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("index,n", [(0, 10_000), (1, 200_000)])
+def test_binning_is_bitwise_equal_to_oracle(index, n):
+    wl = synthetic_config(index, n=n)
+    (m2, d, r, c), _ = project_both(wl.means, wl.scales, wl.quats, wl.opacities, wl.cam)
+    colors = torch.rand(wl.n, 3, generator=torch.Generator().manual_seed(3)).to(DEV)
+    values, ranges, conic4, color4 = _get_rasterizer().bin(m2, d, r, c, colors, wl.opacities.to(DEV), wl.width,
+                                                           wl.height)
+    counts, want_values, want_ranges = oracle.bin_gaussians(np_(m2), np_(d), np_(r), np_(c), np_(wl.opacities),
+                                                            wl.width, wl.height)
+    assert values.numel() == counts.sum() == want_values.size
+    np.testing.assert_array_equal(np_(values), want_values)
+    np.testing.assert_array_equal(np_(ranges), want_ranges)
+    np.testing.assert_array_equal(np_(conic4[:, :3]), np_(c))
+    np.testing.assert_array_equal(np_(color4), np.concatenate([np_(colors), np_(wl.opacities)], 1))
+
+
+def test_binning_keeps_index_order_on_depth_ties():
+    # 300 gaussians in 5 depth values over a 3x2 tile image: ties must stay in index order.
+    g = torch.Generator().manual_seed(4)
+    n = 300
+    means2D = torch.rand(n, 2, generator=g) * torch.tensor([40.0, 30.0])
+    depths = torch.randint(0, 5, (n,), generator=g).float() + 1.0
+    conics = torch.tensor([[0.05, 0.0, 0.05]]).repeat(n, 1)
+    opac = torch.full((n, 1), 0.5)
+    radii = torch.ones(n)
+    values, ranges, _, _ = _get_rasterizer().bin(means2D.to(DEV), depths.to(DEV), radii.to(DEV), conics.to(DEV),
+                                                 None, opac.to(DEV), 40, 30)
+    _, want_values, want_ranges = oracle.bin_gaussians(np_(means2D), np_(depths), np_(radii), np_(conics),
+                                                       np_(opac), 40, 30)
+    np.testing.assert_array_equal(np_(values), want_values)
+    np.testing.assert_array_equal(np_(ranges), want_ranges)
+
+
+def test_empty_scene_renders_background():
+    ext = _get_rasterizer()
+    bg = torch.tensor([0.3, 0.5, 0.7], device=DEV)
+    z = torch.zeros(0, device=DEV)
+    out = ext.rasterize(torch.zeros(0, 2, device=DEV), z, z, torch.zeros(0, 3, device=DEV),
+                        torch.zeros(0, 3, device=DEV), torch.zeros(0, 1, device=DEV), bg, 37, 21)
+    image, final_T, n_contrib, values, ranges = out[:5]
+    assert torch.equal(image, bg.expand(21, 37, 3))
+    assert torch.equal(final_T, torch.ones(21, 37, device=DEV))
+    assert int(n_contrib.abs().sum()) == 0 and values.numel() == 0 and int(ranges.abs().sum()) == 0
+
+
+# ---- blend forward ----------------------------------------------------------------------------
+
+def oracle_render(inputs, width, height, background=None, features=None):
+    m2, d, r, c, col, op = [np_(t) for t in inputs]
+    _, values, ranges = oracle.bin_gaussians(m2, d, r, c, op, width, height)
+    image, final_T, n_contrib, fimg = oracle.render_forward(
+        width, height, ranges, values, m2, c, op, col,
+        None if background is None else np_(background), None if features is None else np_(features))
+    return image, fimg, final_T, n_contrib, values, ranges
+
+
+def test_rgb_forward_matches_oracle():
+    width, height = 128, 96
+    inputs = scene(0, 3000, width, height)
+    bg = torch.tensor([0.3, 0.5, 0.7], device=DEV)
+    image, final_T, n_contrib, values, ranges, _, _ = _get_rasterizer().rasterize(*inputs, bg, width, height)
+    want_image, _, want_T, want_nc, want_values, want_ranges = oracle_render(inputs, width, height, bg)
+    np.testing.assert_array_equal(np_(values), want_values)
+    assert_image_close(np_(image), want_image)
+    assert_image_close(np_(final_T), want_T)
+    # exp differs by an ulp between libm and the GPU, which can flip a pixel's last contributor
+    # only for a gaussian sitting exactly on the 1/255 or 1e-4 cutoff.
+    assert (np_(n_contrib) != want_nc).mean() < 1e-3
+
+
+@pytest.mark.parametrize("channels", [32, 64, 128, 256, 512])
+def test_features_forward_matches_oracle(channels):
+    width, height = 128, 96
+    inputs = scene(0, 3000, width, height)
+    features = torch.rand(3000, channels, generator=torch.Generator().manual_seed(2)).to(DEV)
+    image, feature_image = rasterize(*inputs, width, height, features=features)
+    assert torch.equal(image, rasterize(*inputs, width, height)), "RGB must not depend on the features"
+    _, want, _, _, _, _ = oracle_render(inputs, width, height, features=features)
+    assert_image_close(np_(feature_image), want, max_error=1e-3, max_perc_99=5e-4)
+
+
+def test_feature_forward_of_config0_matches_oracle():
+    wl = synthetic_config(0)
+    (m2, d, r, c), _ = project_both(wl.means, wl.scales, wl.quats, wl.opacities, wl.cam)
+    colors = torch.rand(wl.n, 3, generator=torch.Generator().manual_seed(3)).to(DEV)
+    inputs = (m2, d, r, c, colors, wl.opacities.to(DEV))
+    image, feature_image = rasterize(*inputs, wl.width, wl.height, features=wl.features.to(DEV))
+    want_image, want_f, _, _, _, _ = oracle_render(inputs, wl.width, wl.height, torch.zeros(3), wl.features)
+    assert_image_close(np_(image), want_image)
+    assert_image_close(np_(feature_image), want_f, max_error=1e-3, max_perc_99=5e-4)
+
+
+# ---- backward ---------------------------------------------------------------------------------
+
+def grads_gpu(inputs, width, height, features, grad_image, grad_feat, background):
+    m2, d, r, c, col, op = inputs
+    leaves = [t.detach().clone().requires_grad_(True) for t in (m2, c, col, op, features)]
+    image, fimg = rasterize(leaves[0], d, r, leaves[1], leaves[2], leaves[3], width, height, background,
+                            features=leaves[4])
+    torch.autograd.backward((image, fimg), (grad_image, grad_feat))
+    return [np_(t.grad) for t in leaves]
+
+
+def grads_oracle(inputs, width, height, features, grad_image, grad_feat, background):
+    m2, d, r, c, col, op = [np_(t) for t in inputs]
+    _, values, ranges = oracle.bin_gaussians(m2, d, r, c, op, width, height)
+    _, T, nc, _ = oracle.render_forward(width, height, ranges, values, m2, c, op, col, np_(background), np_(features))
+    dm, dc, dcol, dop, df = oracle.render_backward(width, height, ranges, values, m2, c, op, col, np_(background), T,
+                                                   nc, np_(grad_image), np_(features), np_(grad_feat))
+    return [dm, dc, dcol, dop, df]
+
+
+@pytest.mark.parametrize("channels,slice_width", [(32, 32), (64, 64), (64, 32), (128, 128), (128, 64), (128, 32),
+                                                  (256, 128), (256, 64), (512, 128), (512, 64)])
+def test_backward_matches_oracle(channels, slice_width, monkeypatch):
+    monkeypatch.setattr("gaussian_splatting.rasterizer.FEATURE_SLICE_WIDTH", slice_width)
+    width, height = 128, 96
+    inputs = scene(0, 3000, width, height)
+    g = torch.Generator().manual_seed(3)
+    features = torch.rand(3000, channels, generator=g).to(DEV)
+    grad_image = torch.rand(height, width, 3, generator=g).to(DEV)
+    grad_feat = torch.rand(height, width, channels, generator=g).to(DEV)
+    bg = torch.tensor([0.3, 0.5, 0.7], device=DEV)
+    got = grads_gpu(inputs, width, height, features, grad_image, grad_feat, bg)
+    want = grads_oracle(inputs, width, height, features, grad_image, grad_feat, bg)
+    assert_grads_close(("means2D", "conics", "colors", "opacities", "features"), got, want)
+
+
+def test_rgb_only_backward_matches_oracle():
+    width, height = 128, 96
+    inputs = scene(1, 3000, width, height)
+    g = torch.Generator().manual_seed(1)
+    grad_image = torch.rand(height, width, 3, generator=g).to(DEV)
+    bg = torch.tensor([0.3, 0.5, 0.7], device=DEV)
+    m2, d, r, c, col, op = inputs
+    leaves = [t.detach().clone().requires_grad_(True) for t in (m2, c, col, op)]
+    rasterize(leaves[0], d, r, leaves[1], leaves[2], leaves[3], width, height, bg).backward(grad_image)
+    mn, cn, coln, opn = [np_(t) for t in inputs][0], np_(c), np_(col), np_(op)
+    _, values, ranges = oracle.bin_gaussians(mn, np_(d), np_(r), cn, opn, width, height)
+    _, T, nc, _ = oracle.render_forward(width, height, ranges, values, mn, cn, opn, coln, np_(bg))
+    want = oracle.render_backward(width, height, ranges, values, mn, cn, opn, coln, np_(bg), T, nc, np_(grad_image))
+    assert_grads_close(("means2D", "conics", "colors", "opacities"), [np_(t.grad) for t in leaves], want[:4])
+
+
+EDGE_CASES = {
+    "depth_ties": ([[7.5, 8.5], [9.5, 8.5]], [2.0, 2.0], [3.0, 3.0], [0.7, 0.7], 16, 16),
+    "min_alpha": ([[4.5, 4.5], [12.5, 4.5]], [1.0, 1.0], [0.5, 0.5], [1.01 / 255, 0.99 / 255], 16, 8),
+    "max_alpha": ([[8.5, 8.5]], [1.0], [2.0], [1.0], 16, 16),
+    "transmittance_floor": ([[8.5, 8.5]] * 50, [1.0 + i for i in range(50)], [4.0] * 50, [0.9] * 50, 16, 16),
+}
+
+
+@pytest.mark.parametrize("case", list(EDGE_CASES))
+def test_edge_case_matches_oracle(case):
+    means, depths, sigmas, opac, width, height = EDGE_CASES[case]
+    inputs = flat_scene(means, depths, sigmas, opac, device=DEV)
+    n = len(depths)
+    g = torch.Generator().manual_seed(7)
+    bg = torch.tensor([0.3, 0.5, 0.7], device=DEV)
+    grad_image = torch.rand(height, width, 3, generator=g).to(DEV)
+    features = torch.rand(n, 128, generator=g).to(DEV)
+    grad_feat = torch.rand(height, width, 128, generator=g).to(DEV)
+    image = rasterize(*inputs, width, height, bg)
+    want_image = oracle_render(inputs, width, height, bg)[0]
+    assert_image_close(np_(image), want_image)
+    got = grads_gpu(inputs, width, height, features, grad_image, grad_feat, bg)
+    want = grads_oracle(inputs, width, height, features, grad_image, grad_feat, bg)
+    assert_grads_close(("means2D", "conics", "colors", "opacities", "features"), got, want)
+
+
+def test_max_alpha_clamp_gives_099_colour():
+    inputs = flat_scene([[8.5, 8.5]], [1.0], [2.0], [1.0], device=DEV)
+    torch.testing.assert_close(rasterize(*inputs, 16, 16)[8, 8], 0.99 * inputs[4][0])
+
+
+def test_min_alpha_threshold_blends_only_above():
+    inputs = flat_scene([[4.5, 4.5], [12.5, 4.5]], [1.0, 1.0], [0.5, 0.5], [1.01 / 255, 0.99 / 255], device=DEV)
+    image = rasterize(*inputs, 16, 8)
+    assert image[4, 4].abs().sum() > 0
+    assert torch.equal(image[4, 12], torch.zeros(3, device=DEV))
+
+
+def test_dense_tile_walks_past_every_batch():
+    g = torch.Generator().manual_seed(11)
+    n = 2000
+    means = (torch.rand(n, 2, generator=g) * 16).tolist()
+    depths = (1 + torch.rand(n, generator=g)).tolist()
+    inputs = flat_scene(means, depths, [12.0] * n, [0.02] * n, device=DEV)
+    bg = torch.zeros(3, device=DEV)
+    out = _get_rasterizer().rasterize(*inputs, bg, 16, 16)
+    assert out[2].min() > 256, f"some pixel stopped at {out[2].min().item()}"
+    want_image = oracle_render(inputs, 16, 16, bg)[0]
+    assert_image_close(np_(out[0]), want_image)
+    gg = torch.Generator().manual_seed(12)
+    features = torch.rand(n, 64, generator=gg).to(DEV)
+    grad_image = torch.rand(16, 16, 3, generator=gg).to(DEV)
+    grad_feat = torch.rand(16, 16, 64, generator=gg).to(DEV)
+    got = grads_gpu(inputs, 16, 16, features, grad_image, grad_feat, bg)
+    want = grads_oracle(inputs, 16, 16, features, grad_image, grad_feat, bg)
+    assert_grads_close(("means2D", "conics", "colors", "opacities", "features"), got, want)
+
+
+def test_unsupported_feature_width_is_rejected():
+    inputs = scene(0, 100, 32, 32)
+    with pytest.raises(RuntimeError, match="32, 64, 128, 256 or 512"):
+        rasterize(*inputs, 32, 32, features=torch.rand(100, 24, device=DEV))
+
+
+# ---- SSIM and SH ------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("height,width", [(64, 64), (37, 53), (11, 11), (546, 979)])
+def test_ssim_matches_oracle(height, width):
+    g = torch.Generator().manual_seed(height * width)
+    gt = torch.rand(height, width, 3, generator=g)
+    rendered = (gt + 0.1 * torch.randn(height, width, 3, generator=g)).clamp(0, 1)
+    ext = _get_rasterizer()
+    got = ext.ssim_forward(rendered.to(DEV), gt.to(DEV))
+    want = oracle.ssim_forward(np_(rendered), np_(gt))
+    for name, a, b in zip(("map", "d_mu", "d_aa", "d_ab"), got, want):
+        np.testing.assert_allclose(np_(a), b, rtol=1e-4, atol=1e-6, err_msg=name)
+    grad = ext.ssim_backward(torch.tensor([0.7], device=DEV), rendered.to(DEV), gt.to(DEV), *got[1:])
+    want_grad = oracle.ssim_backward(0.7, np_(rendered), np_(gt), *want[1:])
+    np.testing.assert_allclose(np_(grad), want_grad, rtol=1e-4, atol=1e-9)
+
+
+@pytest.mark.parametrize("degree", [0, 1, 2, 3])
+def test_eval_sh_matches_oracle(degree):
+    g = torch.Generator().manual_seed(degree)
+    n = 5000
+    sh = torch.randn(n, 16, 3, generator=g) * 0.5
+    dirs = torch.nn.functional.normalize(torch.randn(n, 3, generator=g), dim=-1)
+    radii = (torch.rand(n, generator=g) > 0.1).float()
+    got = _get_rasterizer().eval_sh(sh[:, :1].contiguous().to(DEV), sh[:, 1:].contiguous().to(DEV), dirs.to(DEV),
+                                    degree, radii.to(DEV))
+    want = oracle.eval_sh(np_(sh[:, :1]), np_(sh[:, 1:]), np_(dirs), degree, np_(radii))
+    np.testing.assert_allclose(np_(got), want, rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("degree", [1, 3])
+def test_sh_backward_adam_matches_oracle(degree):
+    g = torch.Generator().manual_seed(10 + degree)
+    n = 5000
+    sh = torch.randn(n, 16, 3, generator=g) * 0.5
+    dirs = torch.nn.functional.normalize(torch.randn(n, 3, generator=g), dim=-1)
+    radii = (torch.rand(n, generator=g) > 0.1).float()
+    grad_rgb = torch.randn(n, 3, generator=g)
+    dc, rest = sh[:, :1].contiguous(), sh[:, 1:].contiguous()
+    state = [torch.rand(n, 1, 3, generator=g) * 0.01, torch.rand(n, 1, 3, generator=g) * 1e-4,
+             torch.rand(n, 15, 3, generator=g) * 0.01, torch.rand(n, 15, 3, generator=g) * 1e-4]
+    dev = [t.to(DEV) for t in (dc, rest, *state)]
+    step = torch.tensor(3.0, device=DEV)
+    gd = _get_rasterizer().eval_sh_backward_adam(grad_rgb.to(DEV), dev[0], dev[1], dirs.to(DEV), degree, radii.to(DEV),
+                                                 dev[2], dev[3], dev[4], dev[5], step, step, 0.0025, 0.0025 / 20,
+                                                 0.9, 0.999, 1e-15)
+    host = [np_(t).copy() for t in (dc, rest, *state)]
+    want_gd = oracle.eval_sh_backward_adam(np_(grad_rgb), host[0], host[1], np_(dirs), degree, np_(radii), host[2],
+                                           host[3], host[4], host[5], 3.0, 3.0, 0.0025, 0.0025 / 20, 0.9, 0.999, 1e-15)
+    np.testing.assert_allclose(np_(gd), want_gd, rtol=1e-4, atol=1e-5)
+    for a, b in zip(dev, host):
+        np.testing.assert_allclose(np_(a), b, rtol=1e-5, atol=1e-7)
