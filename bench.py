@@ -1,0 +1,278 @@
+#!/usr/bin/env python3
+"""Headline benchmark: forward + backward of the splatting hot path on one MI355X.
+
+Workload: 1.18M synthetic gaussians, 979x546 pinhole camera (fx = fy = 580),
+128 fp32 feature channels, inputs resident in HBM. One step is what the reference's harness times
+(bench/harness.py:59-66, 157-177; README scope "projection, binning and blending of the RGB image plus
+the feature image"): normalize(quats) -> project_gaussians -> rasterize(features=F) forward, then
+autograd backward of dL/dimage and dL/dfeature_image (both U[0, 1]) through the blend and the
+projection. Colours are a leaf, as in the harness, so SH is not in the timed region.
+
+Prints ONE JSON line: the metric (ms per fwd+bwd, lower is better), the fwd / bwd split measured the
+harness way (events, median), per-stage HIP-event timings taken inside the timed region, the roofline
+of the dominant kernel (render_backward) against MI355X HBM (8 TB/s) and a CPU baseline: the oracle
+(oracle/hds_oracle.c, OpenMP) running the same frame on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (str(ROOT), str(ROOT / "high-dimensional-splatting_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "fwd+bwd ms at 1.18M gaussians, 979x546, C=128; fraction of HBM roofline"
+HBM_PEAK_GBS = 8000.0
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50, help="timed fwd+bwd steps")
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", type=int, default=2, help="BASELINE.json config index (0-4)")
+    ap.add_argument("--channels", type=int, default=None, help="override the config's feature width")
+    ap.add_argument("--no-cpu-baseline", action="store_true", help="skip timing the CPU oracle")
+    ap.add_argument("--no-split", action="store_true", help="skip the separate fwd / bwd median timing")
+    ap.add_argument("--frozen-features", action="store_true",
+                    help="features without requires_grad: the backward keeps the feature term of the geometry "
+                         "gradients but writes no grad_features (reference test_render.py:118-134)")
+    ap.add_argument("--rgb-only", action="store_true", help="render RGB without features (features=None)")
+    ap.add_argument("--bwd-slice", type=int, default=None,
+                    help="channels per backward work-group (gaussian_splatting.rasterizer.FEATURE_SLICE_WIDTH)")
+    return ap.parse_args()
+
+
+def algorithmic_bytes(n: int, n_vis: int, pairs: int, hw: int, c: int) -> dict[str, float]:
+    """Minimal unique HBM bytes per stage (fp32), the roofline denominators: each input read once,
+    each output written once (gradient outputs counted once, not as zero-fill + read-modify-write)."""
+    return {
+        "project_forward": 44 * n + 28 * n,
+        "binning": 12 * n + 48 * pairs,
+        "render": 4 * pairs + 36 * n_vis + 4 * c * n_vis + 20 * hw + 4 * c * hw,
+        "render_backward": 20 * hw + 4 * pairs + 36 * n_vis + 4 * c * n_vis + 4 * c * hw + 4 * c * n + 36 * n,
+        "project_backward": 60 * n + 40 * n,
+    }
+
+
+def main() -> int:
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU: the rasterizer path has no multi-GPU mode in this build "
+              "(see DESIGN.md for how it would shard over channels). Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+    import torch.nn.functional as F
+
+    from gaussian_splatting.rasterizer import _get_rasterizer, project_gaussians, rasterize
+    from gaussian_splatting.rasterizer._native import StageTimer
+    from gaussian_splatting.utils.sh import eval_sh
+    from tests.scenes import synthetic_config, upstream, view_dirs
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP GPU", file=sys.stderr)
+        return 2
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    wl = synthetic_config(args.config, channels=args.channels)
+    cam = wl.cam
+    W, H, C, N = wl.width, wl.height, wl.channels, wl.n
+    print(f"[bench] {wl.name}: N={N} {W}x{H} C={C}", file=sys.stderr, flush=True)
+    wl_dev = wl.to(dev)
+    w2c = torch.eye(4, device=dev)
+
+    # Colours are a leaf computed once under no_grad, as in bench/harness.py:33-56.
+    with torch.no_grad():
+        _, _, radii0, _ = project_gaussians(wl_dev.means, wl_dev.scales, wl_dev.quats, wl_dev.opacities, w2c,
+                                            cam["fx"], cam["fy"], cam["cx"], cam["cy"], W, H)
+        colors = eval_sh(wl_dev.sh_dc, wl_dev.sh_rest, view_dirs(wl_dev.means), 3, radii0, None)
+    leaves = {
+        "means": wl_dev.means.clone().requires_grad_(True),
+        "scales": wl_dev.scales.clone().requires_grad_(True),
+        "quats": wl_dev.quats.clone().requires_grad_(True),
+        "opacities": wl_dev.opacities[:, 0].clone().requires_grad_(True),
+        "colors": colors.clone().requires_grad_(True),
+        "features": wl_dev.features.clone().requires_grad_(not args.frozen_features),
+    }
+    if args.rgb_only:
+        del leaves["features"]
+    grad_image, grad_features = upstream(2, H, W, C, device=dev)
+    state = {}
+
+    def forward():
+        means2D, depths, radii, conics = project_gaussians(
+            leaves["means"], leaves["scales"], F.normalize(leaves["quats"], dim=-1), leaves["opacities"][:, None],
+            w2c, cam["fx"], cam["fy"], cam["cx"], cam["cy"], W, H)
+        state["out"] = rasterize(means2D, depths, radii, conics, leaves["colors"], leaves["opacities"][:, None],
+                                 W, H, features=leaves.get("features"))
+
+    def backward():
+        if args.rgb_only:
+            torch.autograd.backward(state["out"], grad_image)
+        else:
+            torch.autograd.backward(state["out"], [grad_image, grad_features])
+
+    def reset():
+        for leaf in leaves.values():
+            leaf.grad = None
+
+    def step():
+        reset()
+        forward()
+        backward()
+
+    if args.bwd_slice:
+        import gaussian_splatting.rasterizer as rasterizer_module
+
+        rasterizer_module.FEATURE_SLICE_WIDTH = args.bwd_slice
+    ext = _get_rasterizer()
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    print("[bench] warmup done", file=sys.stderr, flush=True)
+
+    # Timed region: exactly `steps` fwd+bwd steps between two device synchronisations, with the
+    # library's stage timer recording HIP events around every call on the compute stream.
+    timer = StageTimer()
+    ext.timer = timer
+    step_events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                   for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for start, end in step_events:
+        start.record()
+        step()
+        end.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    ext.timer = None
+    stages = timer.summary()
+    step_ms = [s.elapsed_time(e) for s, e in step_events]
+    ms_per_step = wall_ms / args.steps
+    print(f"[bench] timed {args.steps} steps: {ms_per_step:.3f} ms/step wall, median {statistics.median(step_ms):.3f}",
+          file=sys.stderr, flush=True)
+
+    # Counts the roofline needs: visible gaussians and tile-gaussian pairs of this frame.
+    with torch.no_grad():
+        m2, d, r, c = project_gaussians(leaves["means"], leaves["scales"], F.normalize(leaves["quats"], dim=-1),
+                                        leaves["opacities"][:, None], w2c, cam["fx"], cam["fy"], cam["cx"],
+                                        cam["cy"], W, H)
+        n_vis = int((r > 0).sum())
+        pairs = int(ext.bin(m2, d, r, c, None, leaves["opacities"][:, None], W, H)[0].numel())
+    hw = W * H
+    alg = algorithmic_bytes(N, n_vis, pairs, hw, C)
+    stage_report = {}
+    for name, row in stages.items():
+        entry = {"launches_per_step": row["launches"] / args.steps, "mean_ms": round(row["mean_ms"], 4)}
+        if name in alg and row["mean_ms"] > 0:
+            gbs = alg[name] / (row["mean_ms"] * 1e-3) / 1e9
+            entry.update({"algorithmic_MB": round(alg[name] / 1e6, 2), "achieved_GBs": round(gbs, 1),
+                          "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)})
+        stage_report[name] = entry
+
+    split = {}
+    if not args.no_split:
+        # The harness method (bench/harness.py:133-177): events around forward alone, and around
+        # backward alone with an untimed forward before each sample; medians.
+        fwd, bwd = [], []
+        for _ in range(min(args.steps, 20)):
+            reset()
+            torch.cuda.synchronize()
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            forward()
+            e.record()
+            e.synchronize()
+            fwd.append(s.elapsed_time(e))
+            s2, e2 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s2.record()
+            backward()
+            e2.record()
+            e2.synchronize()
+            bwd.append(s2.elapsed_time(e2))
+        split = {"fwd_ms_median": round(statistics.median(fwd), 4), "bwd_ms_median": round(statistics.median(bwd), 4)}
+
+    rb = stage_report.get("render_backward", {})
+    rb_ms = stages["render_backward"]["mean_ms"]
+    achieved = alg["render_backward"] / (rb_ms * 1e-3) / 1e9
+    roofline = {"kernel": "render_backward_kernel (hds_render_backward_accumulate)", "bound": "hbm",
+                "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "algorithmic_bytes": int(alg["render_backward"]), "mean_launch_ms": round(rb_ms, 4)}
+    total_alg = sum(alg.values())
+    step_frac = total_alg / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS
+
+    cpu = None
+    if not args.no_cpu_baseline and not args.rgb_only and not args.frozen_features:
+        cpu = cpu_baseline(wl, colors, grad_image, grad_features)
+
+    line = {
+        "metric": METRIC, "value": round(ms_per_step, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": wl.name + ("-rgb-only" if args.rgb_only else "")
+                   + ("-frozen-features" if args.frozen_features else ""), "gaussians": N, "width": W, "height": H,
+                   "channels": 0 if args.rgb_only else C,
+                   "visible": n_vis, "pairs": pairs, "parallelism": "single-gpu"},
+        "step_ms_median": round(statistics.median(step_ms), 4), **split,
+        "step_hbm_frac": round(step_frac, 4), "step_algorithmic_MB": round(total_alg / 1e6, 1),
+        "roofline": roofline, "stages": stage_report, "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def cpu_baseline(wl, colors, grad_image, grad_features):
+    """The CPU oracle (OpenMP, all host threads) on the same frame: projection, binning, blend forward,
+    blend backward and projection backward, once. Sample = the full frame."""
+    import numpy as np
+
+    import oracle
+
+    np_ = lambda t: t.detach().cpu().numpy()  # noqa: E731
+    cam = wl.cam
+    means, scales = np_(wl.means), np_(wl.scales)
+    quats = np_(wl.quats / wl.quats.norm(dim=-1, keepdim=True))
+    opac, feats = np_(wl.opacities), np_(wl.features)
+    cols, gi, gf = np_(colors), np_(grad_image), np_(grad_features)
+    print("[bench] cpu baseline: oracle fwd+bwd of the full frame", file=sys.stderr, flush=True)
+    t0 = time.perf_counter()
+    m2, d, r, c = oracle.project_forward(means, scales, quats, opac, np.eye(4), cam["fx"], cam["fy"], cam["cx"],
+                                         cam["cy"], cam["width"], cam["height"])
+    _, values, ranges = oracle.bin_gaussians(m2, d, r, c, opac, cam["width"], cam["height"])
+    _, T, nc, _ = oracle.render_forward(cam["width"], cam["height"], ranges, values, m2, c, opac, cols,
+                                        np.zeros(3, np.float32), feats)
+    t1 = time.perf_counter()
+    dm, dc, _, _, _ = oracle.render_backward(cam["width"], cam["height"], ranges, values, m2, c, opac, cols,
+                                            np.zeros(3, np.float32), T, nc, gi, feats, gf)
+    oracle.project_backward(dm, dc, means, scales, quats, np.eye(4), cam["fx"], cam["fy"], cam["cx"], cam["cy"],
+                            cam["width"], cam["height"])
+    t2 = time.perf_counter()
+    return {"value": round((t2 - t0) * 1e3, 1), "unit": "ms", "cores": oracle.num_threads(), "kind": "port",
+            "fwd_ms": round((t1 - t0) * 1e3, 1), "bwd_ms": round((t2 - t1) * 1e3, 1),
+            "sample": f"one full fwd+bwd frame of {wl.name} (same inputs) on the C oracle, OpenMP",
+            "cpu": _cpu_model()}
+
+
+def _cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+if __name__ == "__main__":
+    sys.exit(main())

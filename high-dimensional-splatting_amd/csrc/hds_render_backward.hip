@@ -9,15 +9,19 @@
 // RGB and feature terms are summed into one dL/dalpha per pixel, then opacity, mean and conic
 // gradients follow once (the reference sums two kernels' outputs, rasterizer/__init__.py:160-162).
 //
-// The two channel contractions of the feature backward run on MFMA in split-bf16, for a group of
-// 16 gaussians the wave walks next:
+// Every reduction over the wave's 64 pixels runs on MFMA in split-bf16, once per group of 16
+// gaussians the wave walks next:
 //   dot[px][g]  = sum_c dL/dF[px][c] F[g][c]     (A = dL/dF held in VGPRs, K = channels)
 //   dF[g][c]   += sum_px w[px][g] dL/dF[px][c]   (B = dL/dF held in VGPRs, K = pixels, w = alpha T)
+//   mom[g][j]   = sum_px s[px][g] P[px][j]       (s = G dL/dalpha, P = 1, x, y, x^2, xy, y^2)
+//   rgb[g][c]   = sum_px w[px][g] dL/dRGB[px][c]
 // dL/dF of the wave's 64 pixels lives in registers in both operand layouts for the whole walk, so
 // the feature gradient of a gaussian needs no cross-lane reduction: the MFMA sums over pixels.
-// Geometry gradients (opacity, mean, conic, colour) are reduced over the wave with a
-// reduce-scatter and leave with one atomic per value; slices add their partial dot terms
-// linearly through the same atomics (features.cu:348-349).
+// The six geometry gradients are polynomials in the pixel offsets d = px - mean, so they follow
+// from the six pixel moments of s about the block centre: dopac = sum s, dmean = op Q sum s d,
+// dconic = -op (sum s dx^2 / 2, sum s dx dy, sum s dy^2 / 2). One lane per gaussian then turns
+// moments into gradients and issues the atomics. Slices add their partial dot terms linearly
+// through the same atomics (features.cu:348-349).
 #include "hds_internal.h"
 #include "hds_rasterizer.h"
 
@@ -26,6 +30,7 @@ namespace {
 constexpr int kBatch = 64;
 constexpr int kGroup = 16;       // gaussians per contraction group (N of the dot MFMA, M of dF)
 constexpr int kRowStride = 68;   // words per [group position][pixel] row, 16-byte aligned
+constexpr int kIlp = 4;          // positions whose alpha is evaluated together
 
 struct BackwardArgs {
 	int width, height, tiles_x, channels;
@@ -67,7 +72,9 @@ __global__ __launch_bounds__(256) void render_backward_kernel(const BackwardArgs
 	__shared__ float4 s_box[kBatch];
 	__shared__ __attribute__((aligned(16))) uint32_t s_feat[S > 0 ? (kBatch + 1) * kStride : 1];
 	__shared__ __attribute__((aligned(16))) float s_dot[S > 0 ? 4 * kGroup * kRowStride : 1];
-	__shared__ __attribute__((aligned(16))) uint32_t s_w[S > 0 ? 4 * kGroup * kRowStride : 1];
+	__shared__ __attribute__((aligned(16))) uint32_t s_w[4 * kGroup * kRowStride];
+	__shared__ __attribute__((aligned(16))) uint32_t s_s[4 * kGroup * kRowStride];
+	__shared__ __attribute__((aligned(16))) float s_mom[4 * kGroup * 16];
 	__shared__ int s_slot[4 * kGroup];
 	__shared__ int s_max_last;
 
@@ -81,6 +88,7 @@ __global__ __launch_bounds__(256) void render_backward_kernel(const BackwardArgs
 	const float fx = (float)px + 0.5f, fy = (float)py + 0.5f;
 	const float rx0 = (float)wx0 + 0.5f, rx1 = (float)wx0 + 7.5f;
 	const float ry0 = (float)wy0 + 0.5f, ry1 = (float)wy0 + 7.5f;
+	const float centre_x = (float)wx0 + 4.0f, centre_y = (float)wy0 + 4.0f;
 	const int c0 = slice * S;
 	const bool do_rgb = RGB && slice == 0;
 	const bool want_dF = S > 0 && a.grad_features != nullptr;
@@ -97,6 +105,36 @@ __global__ __launch_bounds__(256) void render_backward_kernel(const BackwardArgs
 	}
 	float rec_r = 0.0f, rec_g = 0.0f, rec_b = 0.0f, last_alpha = 0.0f;
 	float last_r = 0.0f, last_g = 0.0f, last_b = 0.0f, behind_dot = 0.0f;
+
+	// P, the B operand of the moment MFMAs: lane = (pixels 32pk + 8(lane >> 4) + 0..7, column
+	// lane & 15) with columns 1, x, y, x^2, xy, y^2 about the block centre (exact in bf16), then the
+	// pixel's dL/dRGB (split) for the colour gradients, then zeros.
+	hds_bf16x8 p_hi[2], p_lo[2];
+	{
+		const int colj = lane & 15;
+#pragma unroll
+		for (int pk = 0; pk < 2; pk++) {
+			uint32_t d[8];
+#pragma unroll
+			for (int j = 0; j < 8; j++) {
+				const int p = 32 * pk + 8 * (lane >> 4) + j;
+				const float xl = (float)(p & 7) - 3.5f, yl = (float)(p >> 3) - 3.5f;
+				float v = 0.0f;
+				if (colj == 0) v = 1.0f;
+				else if (colj == 1) v = xl;
+				else if (colj == 2) v = yl;
+				else if (colj == 3) v = xl * xl;
+				else if (colj == 4) v = xl * yl;
+				else if (colj == 5) v = yl * yl;
+				else if (colj < 9 && do_rgb) {
+					const int x = wx0 + (p & 7), y = wy0 + (p >> 3);
+					if (x < a.width && y < a.height) v = a.grad_image[((int64_t)y * a.width + x) * 3 + (colj - 6)];
+				}
+				d[j] = hds_split_pack(v);
+			}
+			hds_unpack8(d, p_hi[pk], p_lo[pk]);
+		}
+	}
 
 	// dL/dF of the wave's 64 pixels in both MFMA operand layouts.
 	//   ga: A of dot, lane = (pixel 16m + (lane & 15), channels 32kk + 8(lane >> 4) + 0..7)
@@ -153,6 +191,8 @@ __global__ __launch_bounds__(256) void render_backward_kernel(const BackwardArgs
 	int* slots = s_slot + wave * kGroup;
 	float* dot_rows = s_dot + wave * kGroup * kRowStride;
 	uint32_t* w_rows = s_w + wave * kGroup * kRowStride;
+	uint32_t* s_rows = s_s + wave * kGroup * kRowStride;
+	float* mom = s_mom + wave * kGroup * 16;
 
 	for (int batch_end = num; batch_end > 0; batch_end -= kBatch) {
 		const int cnt = min(kBatch, batch_end);
@@ -169,11 +209,13 @@ __global__ __launch_bounds__(256) void render_backward_kernel(const BackwardArgs
 			s_box[tid] = hds_cull_box(m, co);
 		}
 		if constexpr (S > 0) {
-			__syncthreads();
+			// Feature rows of the batch, each read once for the whole tile; thread groups of S / 4 share
+			// a row, so the gaussian id is one broadcast load.
 			constexpr int kVec = S / 4;
 			for (int i = tid; i < cnt * kVec; i += blockDim.x) {
 				const int row = i / kVec, q = i - row * kVec;
-				const float4 f = *reinterpret_cast<const float4*>(a.features + (size_t)s_gid[row] * a.channels + c0 + 4 * q);
+				const int gid = a.values[range.x + batch_start + row];
+				const float4 f = *reinterpret_cast<const float4*>(a.features + (size_t)gid * a.channels + c0 + 4 * q);
 				*reinterpret_cast<uint4*>(&s_feat[row * kStride + 4 * q]) =
 					make_uint4(hds_split_pack(f.x), hds_split_pack(f.y), hds_split_pack(f.z), hds_split_pack(f.w));
 			}
@@ -218,91 +260,99 @@ __global__ __launch_bounds__(256) void render_backward_kernel(const BackwardArgs
 				hds_wave_fence();
 			}
 
+			// Back-to-front replay of the group, kIlp positions at a time: their alphas are
+			// independent, only T and the behind-sums chain through them.
 			uint32_t active = 0;
-			for (int q = 0; q < count; q++) {
-				const int slot = slots[q];
-				const int idx = batch_start + slot;
-				const float2 m = s_mean[slot];
-				const float4 co = s_conic[slot];
-				float G, dx, dy;
-				const float raw = hds_raw_alpha(fx, fy, m, co, G, dx, dy);
-				const float alpha = fminf(HDS_MAX_ALPHA, raw);
-				const bool contributes = inside && idx < last && alpha >= HDS_MIN_ALPHA;
-				float dL_dalpha = 0.0f, w = 0.0f;
-				if (contributes) {
-					const float inv_1ma = __builtin_amdgcn_rcpf(1.0f - alpha);
-					T *= inv_1ma;
-					w = alpha * T;
-					if (do_rgb) {
-						const float4 col = s_color[slot];
-						rec_r = last_alpha * last_r + (1.0f - last_alpha) * rec_r;
-						rec_g = last_alpha * last_g + (1.0f - last_alpha) * rec_g;
-						rec_b = last_alpha * last_b + (1.0f - last_alpha) * rec_b;
-						last_r = col.x;
-						last_g = col.y;
-						last_b = col.z;
-						last_alpha = alpha;
-						dL_dalpha = ((col.x - rec_r) * gr + (col.y - rec_g) * gg + (col.z - rec_b) * gb) * T -
-									T_final * inv_1ma * dL_dTf;
-					}
-					if constexpr (S > 0) {
-						const float dot = dot_rows[q * kRowStride + lane];
-						dL_dalpha += T * (dot - behind_dot);
-						behind_dot = alpha * dot + (1.0f - alpha) * behind_dot;
-					}
+			for (int q0 = 0; q0 < count; q0 += kIlp) {
+				int slot[kIlp];
+				float raw[kIlp], G[kIlp], dot[kIlp];
+#pragma unroll
+				for (int u = 0; u < kIlp; u++) {
+					slot[u] = slots[min(q0 + u, kGroup - 1)];
+					const int sl = min(slot[u], kBatch - 1);
+					float dx, dy;
+					raw[u] = hds_raw_alpha(fx, fy, s_mean[sl], s_conic[sl], G[u], dx, dy);
+					dot[u] = 0.0f;
+					if constexpr (S > 0) dot[u] = dot_rows[min(q0 + u, kGroup - 1) * kRowStride + lane];
 				}
-				if constexpr (S > 0)
-					if (want_dF) w_rows[q * kRowStride + lane] = hds_split_pack(w);
-				const uint64_t any = hds_ballot(contributes);
-				if (!any) continue;
-				active |= 1u << q;
-				float v[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-				float v_b = 0.0f;
-				if (contributes && raw <= HDS_MAX_ALPHA) {
+#pragma unroll
+				for (int u = 0; u < kIlp; u++) {
+					const int q = q0 + u;
+					if (q >= count) break;
+					const float alpha = fminf(HDS_MAX_ALPHA, raw[u]);
+					const bool contributes = inside && batch_start + slot[u] < last && alpha >= HDS_MIN_ALPHA;
+					float dL_dalpha = 0.0f, w = 0.0f;
+					if (contributes) {
+						const float inv_1ma = __builtin_amdgcn_rcpf(1.0f - alpha);
+						T *= inv_1ma;
+						w = alpha * T;
+						if (do_rgb) {
+							const float4 col = s_color[slot[u]];
+							rec_r = last_alpha * last_r + (1.0f - last_alpha) * rec_r;
+							rec_g = last_alpha * last_g + (1.0f - last_alpha) * rec_g;
+							rec_b = last_alpha * last_b + (1.0f - last_alpha) * rec_b;
+							last_r = col.x;
+							last_g = col.y;
+							last_b = col.z;
+							last_alpha = alpha;
+							dL_dalpha = ((col.x - rec_r) * gr + (col.y - rec_g) * gg + (col.z - rec_b) * gb) * T -
+										T_final * inv_1ma * dL_dTf;
+						}
+						if constexpr (S > 0) {
+							dL_dalpha += T * (dot[u] - behind_dot);
+							behind_dot = alpha * dot[u] + (1.0f - alpha) * behind_dot;
+						}
+					}
 					// A clamped alpha no longer depends on the gaussian (backward.cu:126-135).
-					const float dL_dG = co.w * dL_dalpha;
-					v[0] = G * dL_dalpha;
-					v[1] = dL_dG * G * (co.x * dx + co.y * dy);
-					v[2] = dL_dG * G * (co.y * dx + co.z * dy);
-					v[3] = dL_dG * G * -0.5f * dx * dx;
-					v[4] = dL_dG * G * -dx * dy;
-					v[5] = dL_dG * G * -0.5f * dy * dy;
-				}
-				if (do_rgb) {
-					v[6] = w * gr;
-					v[7] = w * gg;
-					v_b = w * gb;
-				}
-				const float total = hds_wave_reduce_scatter8(v, lane);
-				const int gid = s_gid[slot];
-				const int which = lane >> 3;
-				if ((lane & 7) == 0 && (do_rgb || which < 6)) {
-					float* dst = which == 0   ? &a.grad_opacities[gid]
-								 : which < 3 ? &a.grad_means2D[gid * 2 + (which - 1)]
-								 : which < 6 ? &a.grad_conics[gid * 3 + (which - 3)]
-											 : &a.grad_colors[gid * 3 + (which - 6)];
-					atomicAdd(dst, total);
-				}
-				if (do_rgb) {
-					const float tb = hds_wave_sum(v_b);
-					if (lane == 0) atomicAdd(&a.grad_colors[gid * 3 + 2], tb);
+					const float sg = (contributes && raw[u] <= HDS_MAX_ALPHA) ? G[u] * dL_dalpha : 0.0f;
+					s_rows[q * kRowStride + lane] = hds_split_pack(sg);
+					w_rows[q * kRowStride + lane] = hds_split_pack(w);
+					if (hds_ballot(contributes)) active |= 1u << q;
 				}
 			}
+			if (!active) continue;
+			for (int q = count; q < kGroup; q++) {
+				s_rows[q * kRowStride + lane] = 0u;
+				w_rows[q * kRowStride + lane] = 0u;
+			}
+			hds_wave_fence();
 
-			if constexpr (S > 0) {
-				if (want_dF && active) {
-					for (int q = count; q < kGroup; q++) w_rows[q * kRowStride + lane] = 0u;
-					hds_wave_fence();
-					// dF[g][c]: A = w (positions lane & 15, pixels 32pk + 8(lane >> 4) + 0..7).
-					hds_bf16x8 wa_hi[2], wa_lo[2];
+			// A operands over the 16 positions: lane = (position lane & 15, pixels 32pk + 8(lane >> 4) + 0..7).
+			hds_bf16x8 wa_hi[2], wa_lo[2], sa_hi[2], sa_lo[2];
 #pragma unroll
-					for (int pk = 0; pk < 2; pk++) {
-						const uint32_t* src = w_rows + (lane & 15) * kRowStride + 32 * pk + 8 * (lane >> 4);
-						const uint4 d0 = *reinterpret_cast<const uint4*>(src);
-						const uint4 d1 = *reinterpret_cast<const uint4*>(src + 4);
-						const uint32_t d[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
-						hds_unpack8(d, wa_hi[pk], wa_lo[pk]);
-					}
+			for (int pk = 0; pk < 2; pk++) {
+				const int off = (lane & 15) * kRowStride + 32 * pk + 8 * (lane >> 4);
+				{
+					const uint4 d0 = *reinterpret_cast<const uint4*>(w_rows + off);
+					const uint4 d1 = *reinterpret_cast<const uint4*>(w_rows + off + 4);
+					const uint32_t d[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+					hds_unpack8(d, wa_hi[pk], wa_lo[pk]);
+				}
+				{
+					const uint4 d0 = *reinterpret_cast<const uint4*>(s_rows + off);
+					const uint4 d1 = *reinterpret_cast<const uint4*>(s_rows + off + 4);
+					const uint32_t d[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+					hds_unpack8(d, sa_hi[pk], sa_lo[pk]);
+				}
+			}
+			// Pixel moments of s (columns 0-5) and colour sums of w (columns 6-8).
+			{
+				hds_f32x4 ms = {0.0f, 0.0f, 0.0f, 0.0f}, mw = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+				for (int pk = 0; pk < 2; pk++) {
+					ms = hds_mfma_split(sa_hi[pk], sa_lo[pk], p_hi[pk], p_lo[pk], ms);
+					if (do_rgb) mw = hds_mfma_split(wa_hi[pk], wa_lo[pk], p_hi[pk], p_lo[pk], mw);
+				}
+				const int colj = lane & 15;
+#pragma unroll
+				for (int i = 0; i < 4; i++) {
+					const int q = 4 * (lane >> 4) + i;
+					if (colj < 6) mom[q * 16 + colj] = ms[i];
+					else if (colj < 9) mom[q * 16 + colj] = mw[i];
+				}
+			}
+			if constexpr (S > 0) {
+				if (want_dF) {
 					// D rows = positions 4(lane >> 4) + i, column = channel 16n + (lane & 15).
 					int gid4[4];
 #pragma unroll
@@ -320,9 +370,35 @@ __global__ __launch_bounds__(256) void render_backward_kernel(const BackwardArgs
 						for (int i = 0; i < 4; i++)
 							if (gid4[i] >= 0) atomicAdd(&a.grad_features[(int64_t)gid4[i] * a.channels + c], gacc[i]);
 					}
-					hds_wave_fence();
 				}
 			}
+			hds_wave_fence();
+			// One lane per gaussian: moments about the block centre -> gradients, then the atomics.
+			if (lane < count && ((active >> lane) & 1u)) {
+				const int sl = slots[lane];
+				const int gid = s_gid[sl];
+				const float2 mn = s_mean[sl];
+				const float4 co = s_conic[sl];
+				const float* mq = mom + lane * 16;
+				const float m00 = mq[0], m10 = mq[1], m01 = mq[2], m20 = mq[3], m11 = mq[4], m02 = mq[5];
+				const float mx = mn.x - centre_x, my = mn.y - centre_y;
+				const float sx = m10 - mx * m00, sy = m01 - my * m00;
+				const float sxx = m20 - 2.0f * mx * m10 + mx * mx * m00;
+				const float sxy = m11 - mx * m01 - my * m10 + mx * my * m00;
+				const float syy = m02 - 2.0f * my * m01 + my * my * m00;
+				atomicAdd(&a.grad_opacities[gid], m00);
+				atomicAdd(&a.grad_means2D[gid * 2 + 0], co.w * (co.x * sx + co.y * sy));
+				atomicAdd(&a.grad_means2D[gid * 2 + 1], co.w * (co.y * sx + co.z * sy));
+				atomicAdd(&a.grad_conics[gid * 3 + 0], -0.5f * co.w * sxx);
+				atomicAdd(&a.grad_conics[gid * 3 + 1], -co.w * sxy);
+				atomicAdd(&a.grad_conics[gid * 3 + 2], -0.5f * co.w * syy);
+				if (do_rgb) {
+					atomicAdd(&a.grad_colors[gid * 3 + 0], mq[6]);
+					atomicAdd(&a.grad_colors[gid * 3 + 1], mq[7]);
+					atomicAdd(&a.grad_colors[gid * 3 + 2], mq[8]);
+				}
+			}
+			hds_wave_fence();
 		}
 	}
 }
@@ -348,9 +424,7 @@ int zero(float* p, int64_t count, hipStream_t s) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-}  // namespace
-
-extern "C" int hds_render_backward(int64_t n, int width, int height, int channels, int slice_width,
+int render_backward(bool zero_outputs, int64_t n, int width, int height, int channels, int slice_width,
 								   const int32_t* tile_ranges, const int32_t* values_sorted, int64_t num_pairs,
 								   const float* means2D, const float* conic4, const float* color_opacity4,
 								   const float* background, const float* final_T, const int32_t* n_contrib,
@@ -376,12 +450,14 @@ extern "C" int hds_render_backward(int64_t n, int width, int height, int channel
 	}
 	HDS_REQUIRE(aligned16(conic4) && (!color_opacity4 || aligned16(color_opacity4)), "render_backward: misaligned conic4");
 	hipStream_t s = (hipStream_t)stream;
-	int st;
-	if ((st = zero(grad_means2D, 2 * n, s)) != HDS_OK) return st;
-	if ((st = zero(grad_conics, 3 * n, s)) != HDS_OK) return st;
-	if ((st = zero(grad_opacities, n, s)) != HDS_OK) return st;
-	if (grad_colors && (st = zero(grad_colors, 3 * n, s)) != HDS_OK) return st;
-	if (feats && grad_features && (st = zero(grad_features, (int64_t)channels * n, s)) != HDS_OK) return st;
+	if (zero_outputs) {
+		int st;
+		if ((st = zero(grad_means2D, 2 * n, s)) != HDS_OK) return st;
+		if ((st = zero(grad_conics, 3 * n, s)) != HDS_OK) return st;
+		if ((st = zero(grad_opacities, n, s)) != HDS_OK) return st;
+		if (grad_colors && (st = zero(grad_colors, 3 * n, s)) != HDS_OK) return st;
+		if (feats && grad_features && (st = zero(grad_features, (int64_t)channels * n, s)) != HDS_OK) return st;
+	}
 	if (n == 0 || num_pairs == 0) return HDS_OK;
 
 	const int tiles_x = (width + HDS_TILE - 1) / HDS_TILE, tiles_y = (height + HDS_TILE - 1) / HDS_TILE;
@@ -414,3 +490,20 @@ extern "C" int hds_render_backward(int64_t n, int width, int height, int channel
 		default: return rgb ? launch<128, true>(a, num_tiles, slices, s) : launch<128, false>(a, num_tiles, slices, s);
 	}
 }
+
+}  // namespace
+
+#define HDS_BACKWARD_ARGS                                                                                     \
+	int64_t n, int width, int height, int channels, int slice_width, const int32_t *tile_ranges,               \
+		const int32_t *values_sorted, int64_t num_pairs, const float *means2D, const float *conic4,             \
+		const float *color_opacity4, const float *background, const float *final_T, const int32_t *n_contrib,   \
+		const float *grad_image, const float *features, const float *grad_feature_image, float *grad_means2D,   \
+		float *grad_conics, float *grad_colors, float *grad_opacities, float *grad_features, hds_stream_t stream
+#define HDS_BACKWARD_PASS                                                                                      \
+	n, width, height, channels, slice_width, tile_ranges, values_sorted, num_pairs, means2D, conic4,            \
+		color_opacity4, background, final_T, n_contrib, grad_image, features, grad_feature_image, grad_means2D, \
+		grad_conics, grad_colors, grad_opacities, grad_features, stream
+
+extern "C" int hds_render_backward(HDS_BACKWARD_ARGS) { return render_backward(true, HDS_BACKWARD_PASS); }
+
+extern "C" int hds_render_backward_accumulate(HDS_BACKWARD_ARGS) { return render_backward(false, HDS_BACKWARD_PASS); }

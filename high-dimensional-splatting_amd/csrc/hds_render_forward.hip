@@ -16,6 +16,8 @@
 // and the batch size is fixed, so each output channel sees the same operation sequence whatever
 // C or the slicing is: channels are bitwise independent and RGB is bitwise equal with or without
 // features (the properties tests/test_properties.py pins for the reference).
+#include <cstdlib>
+
 #include "hds_internal.h"
 #include "hds_rasterizer.h"
 
@@ -24,6 +26,7 @@ namespace {
 constexpr int kBatch = 64;      // gaussians staged per LDS batch = one ballot per wave
 constexpr int kGroup = 32;      // K of one MFMA: group positions per flush
 constexpr int kWStride = 66;    // words per weight row: 64 pixels + 2 keeps the 4 lane groups on distinct banks
+constexpr int kIlp = 4;         // hits evaluated together
 
 struct RenderArgs {
 	int width, height, tiles_x, channels;
@@ -55,32 +58,43 @@ __device__ inline void flush_group(hds_f32x4 (&acc)[4][FeatTraits<S>::kNcb], con
 	constexpr int kStride = FeatTraits<S>::kStride;
 	hds_wave_fence();
 	const int kq = lane >> 4, col = lane & 15;
+	// B (weights) for the four 16-pixel blocks stays in registers for the whole flush; A (features)
+	// is fetched one 16-channel block ahead of its MFMAs. The scheduling barriers bound how far the
+	// compiler hoists those fetches, which keeps the C=128 flush inside two waves' register budget.
 	hds_bf16x8 b_hi[4], b_lo[4];
 #pragma unroll
 	for (int m = 0; m < 4; m++) {
-		uint32_t d[8];
+		uint32_t e[8];
 #pragma unroll
-		for (int j = 0; j < 8; j++) d[j] = w_rows[(8 * kq + j) * kWStride + 16 * m + col];
-		hds_unpack8(d, b_hi[m], b_lo[m]);
+		for (int j = 0; j < 8; j++) e[j] = w_rows[(8 * kq + j) * kWStride + 16 * m + col];
+		hds_unpack8(e, b_hi[m], b_lo[m]);
 	}
 	int row[8];
 #pragma unroll
-	for (int j = 0; j < 8; j++) row[j] = slots[8 * kq + j] * kStride;
+	for (int j = 0; j < 8; j++) row[j] = slots[8 * kq + j] * kStride + col;
+	uint32_t d[8];
+#pragma unroll
+	for (int j = 0; j < 8; j++) d[j] = s_feat[row[j]];
 #pragma unroll
 	for (int cb = 0; cb < kNcb; cb++) {
-		uint32_t d[8];
-#pragma unroll
-		for (int j = 0; j < 8; j++) d[j] = s_feat[row[j] + 16 * cb + col];
 		hds_bf16x8 a_hi, a_lo;
 		hds_unpack8(d, a_hi, a_lo);
+		if (cb + 1 < kNcb) {
+#pragma unroll
+			for (int j = 0; j < 8; j++) d[j] = s_feat[row[j] + 16 * (cb + 1)];
+		}
 #pragma unroll
 		for (int m = 0; m < 4; m++) acc[m][cb] = hds_mfma_split(a_hi, a_lo, b_hi[m], b_lo[m], acc[m][cb]);
+		__builtin_amdgcn_sched_barrier(0);
 	}
 	hds_wave_fence();
 }
 
+// Occupancy targets: the 128-channel slice keeps its 128 accumulators in AGPRs at one wave per
+// SIMD; narrower slices fit two or more.
 template <int S, bool RGB>
-__global__ __launch_bounds__(256) void render_forward_kernel(const RenderArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S == 128 ? 1 : (S > 0 ? 2 : 4)))) void render_forward_kernel(
+	const RenderArgs a) {
 	constexpr int kNcb = S > 0 ? FeatTraits<S>::kNcb : 1;
 	constexpr int kStride = S > 0 ? FeatTraits<S>::kStride : 1;
 
@@ -151,38 +165,55 @@ __global__ __launch_bounds__(256) void render_forward_kernel(const RenderArgs a)
 		if (hds_ballot(!done) == 0) continue;
 
 		uint64_t hits = hds_ballot(lane < cnt && hds_box_hits(s_box[lane < cnt ? lane : 0], rx0, rx1, ry0, ry1));
+		// Hits go four at a time: their alphas are independent (only T chains through them), which
+		// gives each wave enough independent work to cover LDS and transcendental latency.
 		while (hits) {
-			const int slot = __builtin_ctzll(hits);
-			hits &= hits - 1;
-			const float2 m = s_mean[slot];
-			const float4 co = s_conic[slot];
-			float G, dx, dy;
-			const float alpha = fminf(HDS_MAX_ALPHA, hds_raw_alpha(fx, fy, m, co, G, dx, dy));
-			float w = 0.0f;
-			if (!done && alpha >= HDS_MIN_ALPHA) {
-				const float test_T = T * (1.0f - alpha);
-				if (test_T < HDS_MIN_TRANSMITTANCE) {
-					done = true;
-				} else {
-					w = alpha * T;
-					if constexpr (RGB) {
-						const float4 col = s_color[slot];
-						cr += w * col.x;
-						cg += w * col.y;
-						cb_ += w * col.z;
-					}
-					T = test_T;
-					last = batch + slot + 1;
+			int slot[kIlp];
+			int nq = 0;
+#pragma unroll
+			for (int q = 0; q < kIlp; q++) {
+				slot[q] = nq > 0 ? slot[0] : 0;
+				if (hits) {
+					slot[q] = __builtin_ctzll(hits);
+					hits &= hits - 1;
+					nq = q + 1;
 				}
 			}
-			if constexpr (S > 0) {
-				if (hds_ballot(w > 0.0f)) {
-					w_rows[k * kWStride + lane] = hds_split_pack(w);
-					if (lane == 0) slots[k] = slot;
-					k++;
-					if (k == kGroup) {
-						flush_group<S>(acc, w_rows, slots, s_feat, lane);
-						k = 0;
+			float alpha[kIlp];
+#pragma unroll
+			for (int q = 0; q < kIlp; q++) {
+				float G, dx, dy;
+				alpha[q] = fminf(HDS_MAX_ALPHA, hds_raw_alpha(fx, fy, s_mean[slot[q]], s_conic[slot[q]], G, dx, dy));
+			}
+#pragma unroll
+			for (int q = 0; q < kIlp; q++) {
+				if (q >= nq) break;
+				float w = 0.0f;
+				if (!done && alpha[q] >= HDS_MIN_ALPHA) {
+					const float test_T = T * (1.0f - alpha[q]);
+					if (test_T < HDS_MIN_TRANSMITTANCE) {
+						done = true;
+					} else {
+						w = alpha[q] * T;
+						if constexpr (RGB) {
+							const float4 col = s_color[slot[q]];
+							cr += w * col.x;
+							cg += w * col.y;
+							cb_ += w * col.z;
+						}
+						T = test_T;
+						last = batch + slot[q] + 1;
+					}
+				}
+				if constexpr (S > 0) {
+					if (hds_ballot(w > 0.0f)) {
+						w_rows[k * kWStride + lane] = hds_split_pack(w);
+						if (lane == 0) slots[k] = slot[q];
+						k++;
+						if (k == kGroup) {
+							flush_group<S>(acc, w_rows, slots, s_feat, lane);
+							k = 0;
+						}
 					}
 				}
 			}
@@ -278,7 +309,13 @@ extern "C" int hds_render(int64_t n, int width, int height, int channels, const 
 		HDS_REQUIRE(rgb, "render: nothing to render (no image and no features)");
 		return launch<0, true>(a, num_tiles, 1, s);
 	}
-	const int width_slice = channels < 128 ? channels : 128;
+	// Channels per work-group: 128 unless HDS_FORWARD_SLICE_WIDTH (32, 64 or 128) asks for less. The
+	// result does not depend on it: every channel runs the same operation sequence.
+	int width_slice = channels < 128 ? channels : 128;
+	if (const char* env = std::getenv("HDS_FORWARD_SLICE_WIDTH")) {
+		const int w = std::atoi(env);
+		if ((w == 32 || w == 64 || w == 128) && w <= channels) width_slice = w;
+	}
 	const int slices = channels / width_slice;
 	switch (width_slice) {
 		case 32: return rgb ? launch<32, true>(a, num_tiles, slices, s) : launch<32, false>(a, num_tiles, slices, s);

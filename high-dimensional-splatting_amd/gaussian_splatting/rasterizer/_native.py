@@ -46,6 +46,8 @@ PROTOTYPES = {
                           _vp]),
     "hds_render_backward": (_i32, [_i64, _i32, _i32, _i32, _i32, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp,
                                    _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "hds_render_backward_accumulate": (_i32, [_i64, _i32, _i32, _i32, _i32, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp,
+                                              _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "hds_ssim_forward": (_i32, [_i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "hds_ssim_backward": (_i32, [_i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
 }
@@ -95,11 +97,50 @@ def _dev(t: torch.Tensor, name: str) -> torch.Tensor:
     return t
 
 
+class StageTimer:
+    """Brackets library calls with HIP events on the stream they run on (the current torch stream).
+
+    The profiling counterpart of the reference's NVTX ranges (rasterizer/__init__.py:135, 153): while
+    enabled, every timed call appends (stage, start, end) events; `summary()` synchronises and
+    returns per-stage launch counts and mean milliseconds.
+    """
+
+    def __init__(self) -> None:
+        self.events: list[tuple[str, torch.cuda.Event, torch.cuda.Event]] = []
+
+    def record(self, stage: str, fn):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        out = fn()
+        end.record()
+        self.events.append((stage, start, end))
+        return out
+
+    def summary(self) -> dict[str, dict[str, float]]:
+        torch.cuda.synchronize()
+        out: dict[str, dict[str, float]] = {}
+        for stage, start, end in self.events:
+            row = out.setdefault(stage, {"launches": 0, "total_ms": 0.0})
+            row["launches"] += 1
+            row["total_ms"] += start.elapsed_time(end)
+        for row in out.values():
+            row["mean_ms"] = row["total_ms"] / row["launches"]
+        return out
+
+
 class HipRasterizer:
     """The reference extension's ten functions (bindings.cpp:4-42) on the HIP library, plus fused calls."""
 
     def __init__(self) -> None:
         self.lib = load_library()
+        self.timer: StageTimer | None = None
+
+    def _run(self, stage: str, fn) -> None:
+        """Runs one C call (raising on error), inside the stage timer when one is installed."""
+        if self.timer is None:
+            _check(fn())
+        else:
+            _check(self.timer.record(stage, fn))
 
     # -- projection ---------------------------------------------------------------------------
 
@@ -114,7 +155,7 @@ class HipRasterizer:
         radii = torch.empty((n,), device=means.device, dtype=torch.float32)
         conics = torch.empty((n, 3), device=means.device, dtype=torch.float32)
         with torch.cuda.device(means.device):
-            _check(self.lib.hds_project_gaussians(
+            self._run("project_forward", lambda: self.lib.hds_project_gaussians(
                 n, _ptr(means), _ptr(scales), _ptr(quats), _ptr(opacities), _ptr(pose), float(fx), float(fy),
                 float(cx), float(cy), int(width), int(height), float(near_plane), float(low_pass), float(fov_scale),
                 _ptr(means2D), _ptr(depths), _ptr(radii), _ptr(conics), _stream(means.device)))
@@ -128,7 +169,7 @@ class HipRasterizer:
         pose = _dev(world_to_camera, "world_to_camera")
         dm, ds, dq = torch.empty_like(means), torch.empty_like(scales), torch.empty_like(quats)
         with torch.cuda.device(means.device):
-            _check(self.lib.hds_project_gaussians_backward(
+            self._run("project_backward", lambda: self.lib.hds_project_gaussians_backward(
                 means.shape[0], _ptr(gm), _ptr(gc), _ptr(means), _ptr(scales), _ptr(quats), _ptr(pose), float(fx),
                 float(fy), float(cx), float(cy), int(width), int(height), float(near_plane), float(low_pass),
                 float(fov_scale), _ptr(dm), _ptr(ds), _ptr(dq), _stream(means.device)))
@@ -143,7 +184,7 @@ class HipRasterizer:
         n = sh_dc.shape[0]
         rgb = torch.empty((n, 3), device=sh_dc.device, dtype=torch.float32)
         with torch.cuda.device(sh_dc.device):
-            _check(self.lib.hds_eval_sh(n, int(degree), _ptr(sh_dc), _ptr(sh_rest), _ptr(dirs), _ptr(radii),
+            self._run("eval_sh", lambda: self.lib.hds_eval_sh(n, int(degree), _ptr(sh_dc), _ptr(sh_rest), _ptr(dirs), _ptr(radii),
                                         _ptr(rgb), _stream(sh_dc.device)))
         return rgb
 
@@ -157,7 +198,7 @@ class HipRasterizer:
         grad_rgb, dirs, radii = _dev(grad_rgb, "grad_rgb"), _dev(dirs, "dirs"), _dev(radii, "radii")
         grad_dirs = torch.empty_like(dirs)
         with torch.cuda.device(sh_dc.device):
-            _check(self.lib.hds_eval_sh_backward_adam(
+            self._run("eval_sh_backward_adam", lambda: self.lib.hds_eval_sh_backward_adam(
                 sh_dc.shape[0], int(degree), _ptr(grad_rgb), _ptr(sh_dc), _ptr(sh_rest), _ptr(dirs), _ptr(radii),
                 _ptr(m_dc), _ptr(v_dc), _ptr(m_rest), _ptr(v_rest), _ptr(step_dc), _ptr(step_rest), float(lr_dc),
                 float(lr_rest), float(beta1), float(beta2), float(eps), _ptr(grad_dirs), _stream(sh_dc.device)))
@@ -184,14 +225,14 @@ class HipRasterizer:
             stream = _stream(dev)
             ws = torch.empty(self.lib.hds_bin_workspace_bytes(n, width, height), device=dev, dtype=torch.uint8)
             pairs = ctypes.c_int64(0)
-            _check(self.lib.hds_bin_count(n, _ptr(means2D), _ptr(depths), _ptr(radii), _ptr(conics), _ptr(colors),
+            self._run("bin_count", lambda: self.lib.hds_bin_count(n, _ptr(means2D), _ptr(depths), _ptr(radii), _ptr(conics), _ptr(colors),
                                           _ptr(opacities), width, height, _ptr(conic4), _ptr(color_opacity4),
                                           _ptr(ws), ws.numel(), ctypes.byref(pairs), stream))
             p = int(pairs.value)
             values_sorted = torch.empty((p,), device=dev, dtype=torch.int32)
             pws = torch.empty(self.lib.hds_pairs_workspace_bytes(p, width, height) if p else 0, device=dev,
                               dtype=torch.uint8)
-            _check(self.lib.hds_bin_emit(n, p, width, height, _ptr(ws), _ptr(pws), pws.numel(), _ptr(values_sorted),
+            self._run("bin_emit", lambda: self.lib.hds_bin_emit(n, p, width, height, _ptr(ws), _ptr(pws), pws.numel(), _ptr(values_sorted),
                                          _ptr(tile_ranges), stream))
         return values_sorted, tile_ranges, conic4, color_opacity4
 
@@ -220,7 +261,7 @@ class HipRasterizer:
         if rgb and background is None:
             background = torch.zeros(3, device=dev, dtype=torch.float32)
         with torch.cuda.device(dev):
-            _check(self.lib.hds_render(
+            self._run("render", lambda: self.lib.hds_render(
                 means2D.shape[0], width, height, channels, _ptr(tile_ranges), _ptr(values_sorted),
                 values_sorted.numel(), _ptr(means2D), _ptr(conic4), _ptr(color_opacity4) if rgb else None,
                 _ptr(background) if rgb else None, _ptr(features), _ptr(image), _ptr(final_T), _ptr(n_contrib),
@@ -246,14 +287,15 @@ class HipRasterizer:
             grad_image = _dev(grad_image, "grad_image")
             if background is None:
                 background = torch.zeros(3, device=dev, dtype=torch.float32)
+        # The walk accumulates with atomics into zeroed buffers.
         f32 = dict(device=dev, dtype=torch.float32)
-        g_means = torch.empty((n, 2), **f32)
-        g_conics = torch.empty((n, 3), **f32)
-        g_colors = torch.empty((n, 3), **f32) if grad_image is not None else None
-        g_opac = torch.empty((n, 1), **f32)
-        g_feat = torch.empty((n, channels), **f32) if features is not None and want_feature_grad else None
+        g_means = torch.zeros((n, 2), **f32)
+        g_conics = torch.zeros((n, 3), **f32)
+        g_colors = torch.zeros((n, 3), **f32) if grad_image is not None else None
+        g_opac = torch.zeros((n, 1), **f32)
+        g_feat = torch.zeros((n, channels), **f32) if features is not None and want_feature_grad else None
         with torch.cuda.device(dev):
-            _check(self.lib.hds_render_backward(
+            self._run("render_backward", lambda: self.lib.hds_render_backward_accumulate(
                 n, int(width), int(height), channels, slice_width or 0, _ptr(tile_ranges), _ptr(values_sorted),
                 values_sorted.numel(), _ptr(_dev(means2D, "means2D")), _ptr(conic4), _ptr(color_opacity4),
                 _ptr(background), _ptr(final_T), _ptr(n_contrib), _ptr(grad_image), _ptr(features),
@@ -307,7 +349,7 @@ class HipRasterizer:
         h, w = rendered.shape[0], rendered.shape[1]
         outs = [torch.empty_like(rendered) for _ in range(4)]
         with torch.cuda.device(rendered.device):
-            _check(self.lib.hds_ssim_forward(h, w, _ptr(rendered), _ptr(gt), *[_ptr(o) for o in outs],
+            self._run("ssim_forward", lambda: self.lib.hds_ssim_forward(h, w, _ptr(rendered), _ptr(gt), *[_ptr(o) for o in outs],
                                              _stream(rendered.device)))
         return tuple(outs)
 
@@ -318,7 +360,7 @@ class HipRasterizer:
         grad = torch.empty_like(rendered)
         h, w = rendered.shape[0], rendered.shape[1]
         with torch.cuda.device(rendered.device):
-            _check(self.lib.hds_ssim_backward(h, w, _ptr(grad_mean), _ptr(rendered), _ptr(gt), _ptr(_dev(d_mu, "d_mu")),
+            self._run("ssim_backward", lambda: self.lib.hds_ssim_backward(h, w, _ptr(grad_mean), _ptr(rendered), _ptr(gt), _ptr(_dev(d_mu, "d_mu")),
                                               _ptr(_dev(d_aa, "d_aa")), _ptr(_dev(d_ab, "d_ab")), _ptr(grad),
                                               _stream(rendered.device)))
         return grad

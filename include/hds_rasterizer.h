@@ -138,6 +138,15 @@ HDS_API int hds_render_backward(int64_t n, int width, int height, int channels, 
 						float* grad_colors, float* grad_opacities, float* grad_features,
 						hds_stream_t stream);
 
+/* As hds_render_backward, but adds into the gradient outputs instead of zeroing them first: the
+ * caller supplies zero-initialised buffers, or accumulates over several views. */
+HDS_API int hds_render_backward_accumulate(
+	int64_t n, int width, int height, int channels, int slice_width, const int32_t* tile_ranges,
+	const int32_t* values_sorted, int64_t num_pairs, const float* means2D, const float* conic4,
+	const float* color_opacity4, const float* background, const float* final_T, const int32_t* n_contrib,
+	const float* grad_image, const float* features, const float* grad_feature_image, float* grad_means2D,
+	float* grad_conics, float* grad_colors, float* grad_opacities, float* grad_features, hds_stream_t stream);
+
 /* ---- SSIM: replaces ssim_forward / ssim_backward ------------------------------------------- */
 
 /* ssim.cu:116-148. rendered, gt [H,W,3] -> ssim_map, d_mu, d_aa, d_ab [H,W,3]. */

@@ -1,0 +1,74 @@
+"""Writes the golden fixtures of tests/golden/ (run from the repo root: python tests/golden/make_golden.py).
+
+hand_solved_pixels.json
+    The four 1x1 pixels of the reference's known-answer test (tests/test_oracle.py:28-37 there):
+    gaussians stacked on the pixel centre front to back, gaussian i coloured with channel i, so each
+    alpha is exactly its opacity clamped to 0.99, over background (0.3, 0.5, 0.7).
+    `float64_reference` holds the reference's hand-solved values; `float32_kernel` the same pixels
+    evaluated with the float32 operation order of the reference kernel (forward.cu:195-236). They
+    differ only in case "clamp_and_floor", where T = (1 - 0.99)^2 sits exactly on the 1e-4 floor:
+    in float32, 1 - 0.99f = 0.00999999 and T * (1 - alpha) = 9.99998e-5 < 1e-4, so the kernel stops
+    before the second gaussian.
+oracle_config0_small.npz
+    Regression vectors of the CPU oracle (after it passes tests/test_oracle_pinning.py) on the first
+    2000 gaussians of BASELINE config 0: projection, binning and the RGB + 8-channel blend.
+"""
+import json
+import sys
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+ROOT = HERE.parents[1]
+sys.path[:0] = [str(ROOT), str(ROOT / "high-dimensional-splatting_amd")]
+
+BACKGROUND = (0.3, 0.5, 0.7)
+CASES = [
+    ("single", [0.5], [0.5 + 0.5 * 0.3, 0.5 * 0.5, 0.5 * 0.7]),
+    ("clamp_and_floor", [1.0, 1.0, 1.0], [0.99 + 1e-4 * 0.3, 0.0099 + 1e-4 * 0.5, 1e-4 * 0.7]),
+    ("skip_at_5e-5", [0.99, 0.5, 0.99], [0.99 + 0.005 * 0.3, 0.005 + 0.005 * 0.5, 0.005 * 0.7]),
+    ("empty", [], list(BACKGROUND)),
+]
+
+
+def float32_pixel(opacities):
+    """One pixel with every gaussian centred on it, in the kernel's float32 operation order."""
+    f = np.float32
+    T, acc = f(1.0), [f(0.0)] * 3
+    for i, op in enumerate(opacities):
+        alpha = min(f(0.99), f(op) * f(1.0))  # exp(0) = 1 at the centre
+        if alpha < f(1.0) / f(255.0):
+            continue
+        test = T * (f(1.0) - alpha)
+        if test < f(1e-4):
+            break
+        acc[i] = acc[i] + alpha * T * f(1.0)
+        T = test
+    return [float(acc[c] + T * f(BACKGROUND[c])) for c in range(3)]
+
+
+def main():
+    cases = [{"name": name, "opacities": ops, "float64_reference": want, "float32_kernel": float32_pixel(ops)}
+             for name, ops, want in CASES]
+    (HERE / "hand_solved_pixels.json").write_text(json.dumps({"background": BACKGROUND, "cases": cases}, indent=1))
+
+    import oracle
+    from tests.scenes import synthetic_config
+
+    n = 2000
+    wl = synthetic_config(0, n=n, channels=8)
+    cam = wl.cam
+    np_ = lambda t: t.numpy()  # noqa: E731
+    m2, d, r, c = oracle.project_forward(np_(wl.means), np_(wl.scales), np_(wl.quats), np_(wl.opacities), np.eye(4),
+                                         cam["fx"], cam["fy"], cam["cx"], cam["cy"], cam["width"], cam["height"])
+    colors = np.random.default_rng(5).uniform(0, 1, (n, 3)).astype(np.float32)
+    _, values, ranges = oracle.bin_gaussians(m2, d, r, c, np_(wl.opacities), cam["width"], cam["height"])
+    image, fimg, _, _, _, _ = oracle.rasterize(m2, d, r, c, colors, np_(wl.opacities), cam["width"], cam["height"],
+                                               np.zeros(3, np.float32), np_(wl.features))
+    np.savez_compressed(HERE / "oracle_config0_small.npz", n=n, means2D=m2, radii=r, values_sorted=values,
+                        tile_ranges=ranges, colors=colors, image=image, feature_image=fimg)
+
+
+if __name__ == "__main__":
+    main()

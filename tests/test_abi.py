@@ -1,0 +1,139 @@
+"""The C-ABI library and the Python mirror of the reference API, checked without a GPU.
+
+The library must load and export every entry point include/hds_rasterizer.h declares, the ctypes
+prototypes must match the header, and argument validation (which runs before anything touches the
+device) must reject bad input with the reference's messages. No kernel is launched here.
+"""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "hds_rasterizer.h"
+
+
+def declared_functions() -> dict[str, int]:
+    """name -> parameter count of every HDS_API function in the public header."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    out = {}
+    for m in re.finditer(r"HDS_API\s+[\w\s\*]+?\b(hds_\w+)\s*\(([^)]*)\)\s*;", text):
+        params = [p for p in m.group(2).split(",") if p.strip() and p.strip() != "void"]
+        out[m.group(1)] = len(params)
+    return out
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from gaussian_splatting.rasterizer._native import load_library
+
+    return load_library()
+
+
+def test_header_declares_the_reference_entry_points():
+    names = declared_functions()
+    # One C entry per reference extension function (bindings.cpp:4-42), rasterize split around the
+    # host read of the pair count.
+    for name in ("hds_project_gaussians", "hds_project_gaussians_backward", "hds_eval_sh",
+                 "hds_eval_sh_backward_adam", "hds_bin_count", "hds_bin_emit", "hds_render", "hds_render_backward",
+                 "hds_ssim_forward", "hds_ssim_backward"):
+        assert name in names, name
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in declared_functions():
+        assert hasattr(lib, name), f"{name} not exported"
+
+
+def test_ctypes_prototypes_match_the_header():
+    from gaussian_splatting.rasterizer._native import PROTOTYPES
+
+    declared = declared_functions()
+    assert set(PROTOTYPES) == set(declared)
+    for name, (_, argtypes) in PROTOTYPES.items():
+        assert len(argtypes) == declared[name], f"{name}: {len(argtypes)} ctypes args vs {declared[name]} declared"
+
+
+def test_abi_version_matches_header(lib):
+    version = int(re.search(r"#define HDS_ABI_VERSION (\d+)", HEADER.read_text()).group(1))
+    assert lib.hds_abi_version() == version
+
+
+def test_workspace_queries_grow_with_the_problem(lib):
+    small = lib.hds_bin_workspace_bytes(1000, 128, 128)
+    big = lib.hds_bin_workspace_bytes(1_000_000, 128, 128)
+    assert 0 < small < big and big >= 7 * 4 * 1_000_000
+    assert lib.hds_pairs_workspace_bytes(10_000, 64, 64) >= 3 * 4 * 10_000
+
+
+def test_unsupported_feature_width_is_rejected_before_launch(lib):
+    fake = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    status = lib.hds_render(10, 32, 32, 24, fake, fake, 10, fake, fake, None, None, fake, None, fake, fake, fake, None)
+    assert status == 1
+    assert b"32, 64, 128, 256 or 512" in lib.hds_last_error()
+
+
+def test_bad_slice_width_is_rejected_before_launch(lib):
+    fake = ctypes.c_void_p(16)
+    status = lib.hds_render_backward(10, 32, 32, 128, 48, fake, fake, 10, fake, fake, None, None, fake, fake, None,
+                                     fake, fake, fake, fake, None, fake, None, None)
+    assert status == 1 and b"slices of 48" in lib.hds_last_error()
+
+
+def test_bad_image_size_and_sh_degree_are_rejected(lib):
+    status = lib.hds_eval_sh(10, 4, None, None, None, None, None, None)
+    assert status == 1 and b"degree 4" in lib.hds_last_error()
+    pairs = ctypes.c_int64(-1)
+    status = lib.hds_bin_count(10, None, None, None, None, None, None, 0, 10, None, None, None, 0,
+                               ctypes.byref(pairs), None)
+    assert status == 1 and b"image size" in lib.hds_last_error() and pairs.value == 0
+
+
+def test_python_api_mirrors_the_reference_module():
+    import gaussian_splatting.rasterizer as rasterizer
+    from gaussian_splatting.rasterizer.projection import JACOBIAN_FOV_SCALE, LOW_PASS, NEAR_PLANE
+    from gaussian_splatting.utils import loss, sh
+
+    assert rasterizer.FEATURE_SLICE_WIDTH is None
+    assert (NEAR_PLANE, LOW_PASS, JACOBIAN_FOV_SCALE) == (0.2, 0.3, 1.3)
+    ext = rasterizer._get_rasterizer()
+    for name in ("rasterize", "rasterize_backward", "rasterize_features", "rasterize_features_backward", "eval_sh",
+                 "eval_sh_backward_adam", "ssim_forward", "ssim_backward", "project_gaussians",
+                 "project_gaussians_backward"):
+        assert callable(getattr(ext, name)), name
+    for name in ("rasterize", "project_gaussians", "RasterizeGaussians", "_get_rasterizer"):
+        assert hasattr(rasterizer, name)
+    for name in ("eval_sh", "rgb_to_sh", "num_sh_coeffs", "EvalSH", "_adam_slot"):
+        assert hasattr(sh, name)
+    for name in ("ssim", "l1_loss", "psnr", "FusedSSIM"):
+        assert hasattr(loss, name)
+    assert sh.num_sh_coeffs(3) == 16
+
+
+def test_host_tensors_are_refused_not_computed_on_the_cpu():
+    from gaussian_splatting.rasterizer import rasterize
+
+    n = 4
+    with pytest.raises(RuntimeError, match="CUDA"):
+        rasterize(torch.zeros(n, 2), torch.ones(n), torch.ones(n), torch.ones(n, 3), torch.ones(n, 3),
+                  torch.full((n, 1), 0.5), 16, 16)
+
+
+def test_rasterize_asserts_shapes_like_the_reference():
+    from gaussian_splatting.rasterizer import rasterize
+
+    with pytest.raises(AssertionError):
+        rasterize(torch.zeros(4, 3), torch.ones(4), torch.ones(4), torch.ones(4, 3), torch.ones(4, 3),
+                  torch.full((4, 1), 0.5), 16, 16)
+
+
+def test_sh_backward_requires_the_named_adam():
+    from gaussian_splatting.utils.sh import EvalSH
+
+    class Ctx:
+        optimizer = None
+
+    with pytest.raises(RuntimeError, match="needs the Adam"):
+        EvalSH.backward(Ctx(), torch.zeros(1, 3))
