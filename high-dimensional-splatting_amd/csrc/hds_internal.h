@@ -146,6 +146,43 @@ __device__ static inline void hds_unpack8(const uint32_t d[8], hds_bf16x8& hi, h
 	lo = __builtin_bit_cast(hds_bf16x8, l);
 }
 
+typedef float hds_f32x16 __attribute__((ext_vector_type(16)));
+
+/* acc += A * B on 32x32x16 tiles, split-bf16 operands. Lane layouts (gfx950, checked on hardware):
+ * A[row = lane % 32][k = 8 (lane / 32) + j], B[k = 8 (lane / 32) + j][col = lane % 32],
+ * D[row = 8 (i / 4) + 4 (lane / 32) + i % 4][col = lane % 32] for the 16 accumulators i. */
+__device__ static inline hds_f32x16 hds_mfma32_split(const hds_bf16x8& a_hi, const hds_bf16x8& a_lo,
+													 const hds_bf16x8& b_hi, const hds_bf16x8& b_lo,
+													 hds_f32x16 acc) {
+	acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_lo, b_hi, acc, 0, 0, 0);
+	acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_hi, b_lo, acc, 0, 0, 0);
+	acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_hi, b_hi, acc, 0, 0, 0);
+	return acc;
+}
+
+/* Two floats -> packed bf16 hi pair and bf16 lo (residual) pair, round-to-nearest-even. */
+__device__ static inline void hds_split_pair(float x0, float x1, uint32_t& hi, uint32_t& lo) {
+	typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+	const bf16x2 h = __builtin_convertvector((float __attribute__((ext_vector_type(2)))){x0, x1}, bf16x2);
+	hi = __builtin_bit_cast(uint32_t, h);
+	const float r0 = x0 - hds_u2f(hi << 16), r1 = x1 - hds_u2f(hi & 0xffff0000u);
+	const bf16x2 l = __builtin_convertvector((float __attribute__((ext_vector_type(2)))){r0, r1}, bf16x2);
+	lo = __builtin_bit_cast(uint32_t, l);
+}
+
+/* XCD-aware work-group order. Work-groups are dispatched round-robin over the 8 XCDs, each with its
+ * own L2, so consecutive block ids land on different L2s. Remapping block b to tile
+ * (b % 8) * ceil(T / 8) + b / 8 gives every XCD a contiguous band of tiles: neighbouring tiles, which
+ * share most of their gaussians, then read them through the same L2. Returns -1 for the padding
+ * blocks of a grid rounded up to a multiple of 8. */
+#define HDS_XCDS 8
+static inline unsigned hds_xcd_grid(int num_tiles) { return (unsigned)(((num_tiles + HDS_XCDS - 1) / HDS_XCDS) * HDS_XCDS); }
+__device__ static inline int hds_xcd_tile(int block, int num_tiles) {
+	const int per_xcd = (num_tiles + HDS_XCDS - 1) / HDS_XCDS;
+	const int tile = (block % HDS_XCDS) * per_xcd + block / HDS_XCDS;
+	return tile < num_tiles ? tile : -1;
+}
+
 /* acc += A * B with A, B given as split-bf16 pairs (small terms first). */
 __device__ static inline hds_f32x4 hds_mfma_split(const hds_bf16x8& a_hi, const hds_bf16x8& a_lo,
 												  const hds_bf16x8& b_hi, const hds_bf16x8& b_lo,

@@ -8,14 +8,17 @@
 // (forward.cu:181-225): alpha = min(0.99, op * exp(-m/2)), skip below 1/255, stop before T would
 // drop below 1e-4, n_contrib = 1-based list index of the last blended gaussian.
 //
-// Features: every gaussian some lane blended becomes one position of the wave's current group;
-// its per-pixel weights w = alpha * T go to LDS. A full group of 32 is one contraction
+// Features: the wave's box-hits are taken 16 at a time, in list order, as the K dimension of
 //   out[c][px] += sum_k F[k][c] * W[k][px],
-// 16 channels x 16 pixels per v_mfma_f32_16x16x32_bf16 tile, with both operands in split-bf16
-// (3 MFMAs per tile, ~2^-16 relative error; CDNA4 has no TF32). Groups depend on geometry only
-// and the batch size is fixed, so each output channel sees the same operation sequence whatever
-// C or the slicing is: channels are bitwise independent and RGB is bitwise equal with or without
-// features (the properties tests/test_properties.py pins for the reference).
+// one v_mfma_f32_32x32x16_bf16 per 32 channels x 32 pixels, both operands in split-bf16 (3 MFMAs
+// per tile, ~2^-16 relative error; CDNA4 has no TF32). Each lane keeps its own pixel's 16 weights
+// w = alpha * T (0 where it did not blend) in registers as packed bf16 pairs; one
+// v_permlane32_swap per register pair then forms the B operands of the two 32-pixel halves, so the
+// weights never touch LDS. The 16-hit groups depend on geometry only and the batch size is fixed,
+// so each output channel sees the same operation sequence whatever C or the slicing is: channels
+// are bitwise independent and RGB is bitwise equal with or without features (the properties the
+// reference's tests/test_properties.py pins). The accumulators (S registers per lane) stay in
+// AGPRs and everything else fits in 128 VGPRs, so the 128-channel slice runs two waves per SIMD.
 #include <cstdlib>
 
 #include "hds_internal.h"
@@ -23,13 +26,12 @@
 
 namespace {
 
-constexpr int kBatch = 64;      // gaussians staged per LDS batch = one ballot per wave
-constexpr int kGroup = 32;      // K of one MFMA: group positions per flush
-constexpr int kWStride = 66;    // words per weight row: 64 pixels + 2 keeps the 4 lane groups on distinct banks
-constexpr int kIlp = 4;         // hits evaluated together
+constexpr int kBatch = 64;  // gaussians staged per LDS batch = one ballot per wave
+constexpr int kGroup = 16;  // K of one MFMA: box-hits per group
+constexpr int kIlp = 4;     // hits whose alpha is evaluated together
 
 struct RenderArgs {
-	int width, height, tiles_x, channels;
+	int width, height, tiles_x, channels, num_tiles;
 	const int2* ranges;
 	const int* values;
 	const float2* means2D;
@@ -45,71 +47,73 @@ struct RenderArgs {
 
 template <int S>
 struct FeatTraits {
-	static constexpr int kNcb = S / 16;          // 16-channel MFMA row blocks
-	static constexpr int kStride = S + 4;        // words per staged feature row (16-byte aligned)
+	static constexpr int kNcb = S / 32;    // 32-channel MFMA row blocks
+	static constexpr int kStride = S + 4;  // words per staged feature row (16-byte aligned)
 };
 
-// acc[m][cb] += F^T W for the wave's group: A = features (rows = 16 channels, K = 32 positions),
-// B = weights (K = 32 positions, cols = 16 pixels of block m).
+// acc[m][cb] += F^T W for one group. w_hi / w_lo hold this lane's pixel's packed weights for
+// positions (2i, 2i+1); after the swaps, words 0-3 are the B operand of pixels 0-31 and words 4-7
+// that of pixels 32-63. A = features: lane = (channel lane % 32, positions 8 (lane / 32) + 0..7).
 template <int S>
-__device__ inline void flush_group(hds_f32x4 (&acc)[4][FeatTraits<S>::kNcb], const uint32_t* w_rows, const int* slots,
-								   const uint32_t* s_feat, int lane) {
+__device__ inline void flush_group(hds_f32x16 (&acc)[2][FeatTraits<S>::kNcb], uint32_t (&w_hi)[8], uint32_t (&w_lo)[8],
+								   const int (&slot)[kGroup], const uint32_t* s_feat, int lane) {
 	constexpr int kNcb = FeatTraits<S>::kNcb;
 	constexpr int kStride = FeatTraits<S>::kStride;
-	hds_wave_fence();
-	const int kq = lane >> 4, col = lane & 15;
-	// B (weights) for the four 16-pixel blocks stays in registers for the whole flush; A (features)
-	// is fetched one 16-channel block ahead of its MFMAs. The scheduling barriers bound how far the
-	// compiler hoists those fetches, which keeps the C=128 flush inside two waves' register budget.
-	hds_bf16x8 b_hi[4], b_lo[4];
 #pragma unroll
-	for (int m = 0; m < 4; m++) {
-		uint32_t e[8];
-#pragma unroll
-		for (int j = 0; j < 8; j++) e[j] = w_rows[(8 * kq + j) * kWStride + 16 * m + col];
-		hds_unpack8(e, b_hi[m], b_lo[m]);
+	for (int i = 0; i < 4; i++) {
+		const auto h = __builtin_amdgcn_permlane32_swap(w_hi[i], w_hi[4 + i], false, false);
+		w_hi[i] = h[0];
+		w_hi[4 + i] = h[1];
+		const auto l = __builtin_amdgcn_permlane32_swap(w_lo[i], w_lo[4 + i], false, false);
+		w_lo[i] = l[0];
+		w_lo[4 + i] = l[1];
 	}
+	hds_bf16x8 b_hi[2], b_lo[2];
+#pragma unroll
+	for (int m = 0; m < 2; m++) {
+		b_hi[m] = __builtin_bit_cast(hds_bf16x8, hds_u32x4{w_hi[4 * m], w_hi[4 * m + 1], w_hi[4 * m + 2], w_hi[4 * m + 3]});
+		b_lo[m] = __builtin_bit_cast(hds_bf16x8, hds_u32x4{w_lo[4 * m], w_lo[4 * m + 1], w_lo[4 * m + 2], w_lo[4 * m + 3]});
+	}
+	const bool upper = lane >= 32;
+	const int col = lane & 31;
 	int row[8];
 #pragma unroll
-	for (int j = 0; j < 8; j++) row[j] = slots[8 * kq + j] * kStride + col;
-	uint32_t d[8];
-#pragma unroll
-	for (int j = 0; j < 8; j++) d[j] = s_feat[row[j]];
+	for (int j = 0; j < 8; j++) {
+		// Select the values, not the array half: an indexed pointer select would put slot in scratch.
+		const int lo = slot[j], hi = slot[8 + j];
+		row[j] = (upper ? hi : lo) * kStride + col;
+	}
 #pragma unroll
 	for (int cb = 0; cb < kNcb; cb++) {
+		uint32_t d[8];
+#pragma unroll
+		for (int j = 0; j < 8; j++) d[j] = s_feat[row[j] + 32 * cb];
 		hds_bf16x8 a_hi, a_lo;
 		hds_unpack8(d, a_hi, a_lo);
-		if (cb + 1 < kNcb) {
 #pragma unroll
-			for (int j = 0; j < 8; j++) d[j] = s_feat[row[j] + 16 * (cb + 1)];
-		}
-#pragma unroll
-		for (int m = 0; m < 4; m++) acc[m][cb] = hds_mfma_split(a_hi, a_lo, b_hi[m], b_lo[m], acc[m][cb]);
-		__builtin_amdgcn_sched_barrier(0);
+		for (int m = 0; m < 2; m++) acc[m][cb] = hds_mfma32_split(a_hi, a_lo, b_hi[m], b_lo[m], acc[m][cb]);
 	}
-	hds_wave_fence();
 }
 
-// Occupancy targets: the 128-channel slice keeps its 128 accumulators in AGPRs at one wave per
-// SIMD; narrower slices fit two or more.
+// Occupancy: the accumulators (S per lane) live in AGPRs next to at most 128 VGPRs, two waves per
+// SIMD with features, more without.
 template <int S, bool RGB>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S == 128 ? 1 : (S > 0 ? 2 : 4)))) void render_forward_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S > 0 ? 2 : 4))) void render_forward_kernel(
 	const RenderArgs a) {
 	constexpr int kNcb = S > 0 ? FeatTraits<S>::kNcb : 1;
 	constexpr int kStride = S > 0 ? FeatTraits<S>::kStride : 1;
 
-	__shared__ int s_gid[kBatch];
 	__shared__ float2 s_mean[kBatch];
 	__shared__ float4 s_conic[kBatch];
 	__shared__ float4 s_color[RGB ? kBatch : 1];
 	__shared__ float4 s_box[kBatch];
-	// Row kBatch stays zero: padding positions of a partial group point at it.
+	// Row kBatch stays zero: positions past the end of a partial group point at it.
 	__shared__ __attribute__((aligned(16))) uint32_t s_feat[S > 0 ? (kBatch + 1) * kStride : 1];
-	__shared__ uint32_t s_w[S > 0 ? 4 * kGroup * kWStride : 1];
-	__shared__ int s_slot[S > 0 ? 4 * kGroup : 1];
 
+	const int tile = hds_xcd_tile(blockIdx.x, a.num_tiles);
+	if (tile < 0) return;
 	const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-	const int tile = blockIdx.x, slice = blockIdx.y;
+	const int slice = blockIdx.y;
 	const int tx0 = (tile % a.tiles_x) * HDS_TILE, ty0 = (tile / a.tiles_x) * HDS_TILE;
 	const int wx0 = tx0 + (wave & 1) * 8, wy0 = ty0 + (wave >> 1) * 8;
 	const int px = wx0 + (lane & 7), py = wy0 + (lane >> 3);
@@ -125,14 +129,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S == 128 ? 
 	bool done = !inside;
 	int last = 0;
 	float cr = 0.0f, cg = 0.0f, cb_ = 0.0f;
-	hds_f32x4 acc[4][kNcb];
+	hds_f32x16 acc[2][kNcb];
 #pragma unroll
-	for (int m = 0; m < 4; m++)
+	for (int m = 0; m < 2; m++)
 #pragma unroll
-		for (int c = 0; c < kNcb; c++) acc[m][c] = hds_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-	int k = 0;
-	uint32_t* w_rows = s_w + wave * kGroup * kWStride;
-	int* slots = s_slot + wave * kGroup;
+		for (int c = 0; c < kNcb; c++) acc[m][c] = hds_f32x16{};
 
 	if constexpr (S > 0)
 		for (int i = tid; i < kStride; i += blockDim.x) s_feat[kBatch * kStride + i] = 0u;
@@ -145,89 +146,79 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S == 128 ? 
 			const int gid = a.values[range.x + batch + tid];
 			const float2 m = a.means2D[gid];
 			const float4 co = a.conic4[gid];
-			s_gid[tid] = gid;
 			s_mean[tid] = m;
 			s_conic[tid] = co;
 			if constexpr (RGB) s_color[tid] = a.color_op4[gid];
 			s_box[tid] = hds_cull_box(m, co);
 		}
 		if constexpr (S > 0) {
-			__syncthreads();
+			// Feature rows, split-packed once per tile; S / 4 consecutive threads share a row, so the
+			// gaussian id is one broadcast load.
 			constexpr int kVec = S / 4;
 			for (int i = tid; i < cnt * kVec; i += blockDim.x) {
 				const int row = i / kVec, q = i - row * kVec;
-				const float4 f = *reinterpret_cast<const float4*>(a.features + (size_t)s_gid[row] * a.channels + c0 + 4 * q);
-				uint4 packed = make_uint4(hds_split_pack(f.x), hds_split_pack(f.y), hds_split_pack(f.z), hds_split_pack(f.w));
-				*reinterpret_cast<uint4*>(&s_feat[row * kStride + 4 * q]) = packed;
+				const int gid = a.values[range.x + batch + row];
+				const float4 f = *reinterpret_cast<const float4*>(a.features + (size_t)gid * a.channels + c0 + 4 * q);
+				*reinterpret_cast<uint4*>(&s_feat[row * kStride + 4 * q]) =
+					make_uint4(hds_split_pack(f.x), hds_split_pack(f.y), hds_split_pack(f.z), hds_split_pack(f.w));
 			}
 		}
 		__syncthreads();
 		if (hds_ballot(!done) == 0) continue;
 
 		uint64_t hits = hds_ballot(lane < cnt && hds_box_hits(s_box[lane < cnt ? lane : 0], rx0, rx1, ry0, ry1));
-		// Hits go four at a time: their alphas are independent (only T chains through them), which
-		// gives each wave enough independent work to cover LDS and transcendental latency.
 		while (hits) {
-			int slot[kIlp];
-			int nq = 0;
+			// The next group: up to 16 box-hits in list order; missing positions use the zero row.
+			int slot[kGroup];
+			int count = 0;
 #pragma unroll
-			for (int q = 0; q < kIlp; q++) {
-				slot[q] = nq > 0 ? slot[0] : 0;
+			for (int q = 0; q < kGroup; q++) {
+				slot[q] = kBatch;
 				if (hits) {
 					slot[q] = __builtin_ctzll(hits);
 					hits &= hits - 1;
-					nq = q + 1;
+					count = q + 1;
 				}
 			}
-			float alpha[kIlp];
+			float w[kGroup];
 #pragma unroll
-			for (int q = 0; q < kIlp; q++) {
-				float G, dx, dy;
-				alpha[q] = fminf(HDS_MAX_ALPHA, hds_raw_alpha(fx, fy, s_mean[slot[q]], s_conic[slot[q]], G, dx, dy));
-			}
+			for (int q0 = 0; q0 < kGroup; q0 += kIlp) {
+				float alpha[kIlp];
 #pragma unroll
-			for (int q = 0; q < kIlp; q++) {
-				if (q >= nq) break;
-				float w = 0.0f;
-				if (!done && alpha[q] >= HDS_MIN_ALPHA) {
-					const float test_T = T * (1.0f - alpha[q]);
-					if (test_T < HDS_MIN_TRANSMITTANCE) {
-						done = true;
-					} else {
-						w = alpha[q] * T;
-						if constexpr (RGB) {
-							const float4 col = s_color[slot[q]];
-							cr += w * col.x;
-							cg += w * col.y;
-							cb_ += w * col.z;
-						}
-						T = test_T;
-						last = batch + slot[q] + 1;
-					}
+				for (int u = 0; u < kIlp; u++) {
+					const int sl = min(slot[q0 + u], kBatch - 1);
+					float G, dx, dy;
+					alpha[u] = fminf(HDS_MAX_ALPHA, hds_raw_alpha(fx, fy, s_mean[sl], s_conic[sl], G, dx, dy));
 				}
-				if constexpr (S > 0) {
-					if (hds_ballot(w > 0.0f)) {
-						w_rows[k * kWStride + lane] = hds_split_pack(w);
-						if (lane == 0) slots[k] = slot[q];
-						k++;
-						if (k == kGroup) {
-							flush_group<S>(acc, w_rows, slots, s_feat, lane);
-							k = 0;
+#pragma unroll
+				for (int u = 0; u < kIlp; u++) {
+					const int q = q0 + u;
+					w[q] = 0.0f;
+					if (q < count && !done && alpha[u] >= HDS_MIN_ALPHA) {
+						const float test_T = T * (1.0f - alpha[u]);
+						if (test_T < HDS_MIN_TRANSMITTANCE) {
+							done = true;
+						} else {
+							w[q] = alpha[u] * T;
+							if constexpr (RGB) {
+								const float4 col = s_color[slot[q]];
+								cr += w[q] * col.x;
+								cg += w[q] * col.y;
+								cb_ += w[q] * col.z;
+							}
+							T = test_T;
+							last = batch + slot[q] + 1;
 						}
 					}
 				}
+			}
+			if constexpr (S > 0) {
+				uint32_t w_hi[8], w_lo[8];
+#pragma unroll
+				for (int i = 0; i < 8; i++) hds_split_pair(w[2 * i], w[2 * i + 1], w_hi[i], w_lo[i]);
+				flush_group<S>(acc, w_hi, w_lo, slot, s_feat, lane);
 			}
 			if (hds_ballot(!done) == 0) break;
-		}
-		if constexpr (S > 0) {
-			// The next batch overwrites the staged features: flush the partial group now, its
-			// free positions carrying zero weights and the zero feature row.
-			if (k > 0) {
-				for (int q = k; q < kGroup; q++) w_rows[q * kWStride + lane] = 0u;
-				if (lane < kGroup - k) slots[k + lane] = kBatch;
-				flush_group<S>(acc, w_rows, slots, s_feat, lane);
-				k = 0;
-			}
 		}
 	}
 
@@ -242,25 +233,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S == 128 ? 
 		a.n_contrib[pix] = last;
 	}
 	if constexpr (S > 0) {
-		// D layout of the 16x16 tile: lane holds channels 4*(lane>>4)+0..3 of pixel lane & 15.
+		// D of a 32x32 tile: lane holds pixel 32m + lane % 32 and, for each group g of four
+		// accumulators, channels 8g + 4 (lane / 32) + 0..3.
 #pragma unroll
-		for (int m = 0; m < 4; m++) {
-			const int p = 16 * m + (lane & 15);
+		for (int m = 0; m < 2; m++) {
+			const int p = 32 * m + (lane & 31);
 			const int x = wx0 + (p & 7), y = wy0 + (p >> 3);
 			if (x >= a.width || y >= a.height) continue;
-			float* dst = a.feature_image + ((int64_t)y * a.width + x) * a.channels + c0 + 4 * (lane >> 4);
+			float* dst = a.feature_image + ((int64_t)y * a.width + x) * a.channels + c0 + 4 * (lane >> 5);
 #pragma unroll
-			for (int c = 0; c < kNcb; c++) {
-				const hds_f32x4 v = acc[m][c];
-				*reinterpret_cast<float4*>(dst + 16 * c) = make_float4(v[0], v[1], v[2], v[3]);
-			}
+			for (int c = 0; c < kNcb; c++)
+#pragma unroll
+				for (int g = 0; g < 4; g++) {
+					const hds_f32x16 v = acc[m][c];
+					*reinterpret_cast<float4*>(dst + 32 * c + 8 * g) = make_float4(v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]);
+				}
 		}
 	}
 }
 
 template <int S, bool RGB>
 int launch(const RenderArgs& a, int num_tiles, int slices, hipStream_t s) {
-	render_forward_kernel<S, RGB><<<dim3((unsigned)num_tiles, (unsigned)slices), 256, 0, s>>>(a);
+	render_forward_kernel<S, RGB><<<dim3(hds_xcd_grid(num_tiles), (unsigned)slices), 256, 0, s>>>(a);
 	return hds_check_launch(RGB ? (S > 0 ? "render_rgb_features" : "render_rgb") : "render_features", s);
 }
 
@@ -293,6 +287,7 @@ extern "C" int hds_render(int64_t n, int width, int height, int channels, const 
 				 height,
 				 tiles_x,
 				 feats ? channels : 0,
+				 num_tiles,
 				 reinterpret_cast<const int2*>(tile_ranges),
 				 values_sorted,
 				 reinterpret_cast<const float2*>(means2D),
