@@ -170,6 +170,18 @@ __device__ static inline void hds_split_pair(float x0, float x1, uint32_t& hi, u
 	lo = __builtin_bit_cast(uint32_t, l);
 }
 
+/* Pins a value in a VGPR of its own. This compiler (ROCm 7.2 clang) folds v_permlane16/32_swap
+ * calls whose operands are different elements of one MFMA result vector into a single swap, so
+ * every element after the first silently receives the first one's result; passing each element
+ * through this opaque move first keeps the swaps apart. */
+__device__ static inline uint32_t hds_opaque(uint32_t v) {
+	asm volatile("" : "+v"(v));
+	return v;
+}
+
+/* One MFMA result element as an independent 32-bit operand for a lane swap. */
+__device__ static inline uint32_t hds_swap_operand(float v) { return hds_opaque(__builtin_bit_cast(uint32_t, v)); }
+
 /* XCD-aware work-group order. Work-groups are dispatched round-robin over the 8 XCDs, each with its
  * own L2, so consecutive block ids land on different L2s. Remapping block b to tile
  * (b % 8) * ceil(T / 8) + b / 8 gives every XCD a contiguous band of tiles: neighbouring tiles, which

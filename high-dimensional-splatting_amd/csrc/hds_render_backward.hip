@@ -1,39 +1,44 @@
-// Back-to-front replay of the blend: RGB and feature gradients in one walk.
+// Replay of the blend for the gradients: two kernels over the same tile lists.
 //
 // Layout as in the forward: work-group = tile x slice of S channels, wave = 8x8 pixel block,
-// lane = pixel. Each lane restarts from its final T and n_contrib and walks its tile's list back
-// to front (backward.cu:53-163, features.cu:419-541):
+// lane = pixel, and a wave only visits the gaussians whose culling box reaches its block.
+//
+// backward_geometry_kernel walks each tile's list back to front from every pixel's final T and
+// n_contrib (backward.cu:53-163, features.cu:419-541):
 //   T <- T / (1 - alpha);  RGB: accum_rec recurrence, dL/dalpha = (c - rec).g T - T_f/(1-a) bg.g;
 //   features: dL/dalpha += T (dot - behind_dot), behind_dot <- a dot + (1 - a) behind_dot,
 //   with dot = f . dL/dF[pixel];  geometry gradients only where the raw alpha <= 0.99.
-// RGB and feature terms are summed into one dL/dalpha per pixel, then opacity, mean and conic
-// gradients follow once (the reference sums two kernels' outputs, rasterizer/__init__.py:160-162).
-//
-// Every reduction over the wave's 64 pixels runs on MFMA in split-bf16, once per group of 16
-// gaussians the wave walks next:
-//   dot[px][g]  = sum_c dL/dF[px][c] F[g][c]     (A = dL/dF held in VGPRs, K = channels)
-//   dF[g][c]   += sum_px w[px][g] dL/dF[px][c]   (B = dL/dF held in VGPRs, K = pixels, w = alpha T)
-//   mom[g][j]   = sum_px s[px][g] P[px][j]       (s = G dL/dalpha, P = 1, x, y, x^2, xy, y^2)
-//   rgb[g][c]   = sum_px w[px][g] dL/dRGB[px][c]
-// dL/dF of the wave's 64 pixels lives in registers in both operand layouts for the whole walk, so
-// the feature gradient of a gaussian needs no cross-lane reduction: the MFMA sums over pixels.
+// RGB and feature terms go into one dL/dalpha per pixel (the reference sums two kernels' outputs,
+// rasterizer/__init__.py:160-162). Slices add their partial dot terms linearly through the same
+// atomics (features.cu:348-349). Per group of up to 16 gaussians the wave does, in split-bf16:
+//   dot[g][px]  = sum_c F[g][c] dL/dF[px][c]   (16x16x32 MFMA, dL/dF^T held in VGPRs; a 4x4
+//                                                 lane-group transpose leaves each lane its pixel)
+//   mom[j][g]   = sum_px P[px][j] s[px][g]      (s = G dL/dalpha, P = 1, x, y, x^2, xy, y^2)
+//   rgb[c][g]   = sum_px dL/dRGB[px][c] w[px][g] (w = alpha T)
 // The six geometry gradients are polynomials in the pixel offsets d = px - mean, so they follow
 // from the six pixel moments of s about the block centre: dopac = sum s, dmean = op Q sum s d,
-// dconic = -op (sum s dx^2 / 2, sum s dx dy, sum s dy^2 / 2). One lane per gaussian then turns
-// moments into gradients and issues the atomics. Slices add their partial dot terms linearly
-// through the same atomics (features.cu:348-349).
+// dconic = -op (sum s dx^2 / 2, sum s dx dy, sum s dy^2 / 2). One lane per gaussian issues them.
+//
+// backward_features_kernel replays the blend front to back with the forward's own arithmetic, so
+// its weights w = alpha T equal the forward's bit for bit, and contracts them with dL/dF over the
+// block's pixels, dF[g][c] += sum_px w[px][g] dL/dF[px][c] (features.cu:486-513), on 32x32x16 MFMA
+// in groups of 32 gaussians that run across batches. dL/dF (K = pixels) stays in VGPRs; the weights
+// are written once to LDS as rows per gaussian and read back as the A operand. The result of each
+// lane is 32 consecutive channels of one gaussian, so the atomics are whole cache lines and a
+// gaussian's gradient row sees one atomic per 8x8 block it touches.
 #include "hds_internal.h"
 #include "hds_rasterizer.h"
 
 namespace {
 
 constexpr int kBatch = 64;
-constexpr int kGroup = 16;       // gaussians per contraction group (N of the dot MFMA, M of dF)
-constexpr int kRowStride = 68;   // words per [group position][pixel] row, 16-byte aligned
-constexpr int kIlp = 4;          // positions whose alpha is evaluated together
+constexpr int kIlp = 4;         // positions whose alpha is evaluated together
+constexpr int kGeoGroup = 16;   // gaussians per geometry group
+constexpr int kFeatGroup = 32;  // gaussians per feature-gradient group
+constexpr int kRowStride = 68;  // words per [position][pixel] row, 16-byte aligned
 
 struct BackwardArgs {
-	int width, height, tiles_x, channels;
+	int width, height, tiles_x, channels, num_tiles;
 	const int2* ranges;
 	const int* values;
 	const float2* means2D;
@@ -52,34 +57,43 @@ struct BackwardArgs {
 	float* grad_features;
 };
 
-template <int S>
-struct Slice {
-	static constexpr int kKc = S / 32;      // K steps over channels (dot)
-	static constexpr int kNcb = S / 16;     // 16-channel blocks (dF)
-	static constexpr int kStride = S + 4;   // words per staged feature row
-};
+__device__ inline float hds_swap16_from_odd(float v) {
+	// Lanes of even 16-lane rows receive v of the row above them.
+	const uint32_t u = hds_swap_operand(v);
+	const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+	return __builtin_bit_cast(float, (uint32_t)r[1]);
+}
+
+// Tile-wide maximum of n_contrib: nothing past the deepest contributor can matter (backward.cu:53-60).
+__device__ inline int tile_max_last(int last, int* s_max_last) {
+	if (threadIdx.x == 0) *s_max_last = 0;
+	__syncthreads();
+	if (last > 0) atomicMax(s_max_last, last);
+	__syncthreads();
+	return *s_max_last;
+}
 
 template <int S, bool RGB>
-__global__ __launch_bounds__(256) void render_backward_kernel(const BackwardArgs a) {
-	constexpr int kKc = S > 0 ? Slice<S>::kKc : 1;
-	constexpr int kNcb = S > 0 ? Slice<S>::kNcb : 1;
-	constexpr int kStride = S > 0 ? Slice<S>::kStride : 1;
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void backward_geometry_kernel(const BackwardArgs a) {
+	constexpr int kKc = S > 0 ? S / 32 : 1;       // K steps of the dot over channels
+	constexpr int kStride = S > 0 ? S + 4 : 1;    // words per staged feature row
 
 	__shared__ int s_gid[kBatch];
 	__shared__ float2 s_mean[kBatch];
 	__shared__ float4 s_conic[kBatch];
 	__shared__ float4 s_color[RGB ? kBatch : 1];
 	__shared__ float4 s_box[kBatch];
+	// Row kBatch stays zero: positions past the end of a partial group point at it.
 	__shared__ __attribute__((aligned(16))) uint32_t s_feat[S > 0 ? (kBatch + 1) * kStride : 1];
-	__shared__ __attribute__((aligned(16))) float s_dot[S > 0 ? 4 * kGroup * kRowStride : 1];
-	__shared__ __attribute__((aligned(16))) uint32_t s_w[4 * kGroup * kRowStride];
-	__shared__ __attribute__((aligned(16))) uint32_t s_s[4 * kGroup * kRowStride];
-	__shared__ __attribute__((aligned(16))) float s_mom[4 * kGroup * 16];
-	__shared__ int s_slot[4 * kGroup];
+	// Per wave: s and w of the group as rows per position (the B operands of the moment MFMAs).
+	__shared__ __attribute__((aligned(16))) uint32_t s_tr[4][2][kGeoGroup * kRowStride];
+	__shared__ int s_slot[4][kGeoGroup];
 	__shared__ int s_max_last;
 
+	const int tile = hds_xcd_tile(blockIdx.x, a.num_tiles);
+	if (tile < 0) return;
 	const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-	const int tile = blockIdx.x, slice = blockIdx.y;
+	const int slice = blockIdx.y;
 	const int tx0 = (tile % a.tiles_x) * HDS_TILE, ty0 = (tile / a.tiles_x) * HDS_TILE;
 	const int wx0 = tx0 + (wave & 1) * 8, wy0 = ty0 + (wave >> 1) * 8;
 	const int px = wx0 + (lane & 7), py = wy0 + (lane >> 3);
@@ -91,7 +105,6 @@ __global__ __launch_bounds__(256) void render_backward_kernel(const BackwardArgs
 	const float centre_x = (float)wx0 + 4.0f, centre_y = (float)wy0 + 4.0f;
 	const int c0 = slice * S;
 	const bool do_rgb = RGB && slice == 0;
-	const bool want_dF = S > 0 && a.grad_features != nullptr;
 
 	const float T_final = inside ? a.final_T[pix] : 0.0f;
 	const int last = inside ? a.n_contrib[pix] : 0;
@@ -106,44 +119,43 @@ __global__ __launch_bounds__(256) void render_backward_kernel(const BackwardArgs
 	float rec_r = 0.0f, rec_g = 0.0f, rec_b = 0.0f, last_alpha = 0.0f;
 	float last_r = 0.0f, last_g = 0.0f, last_b = 0.0f, behind_dot = 0.0f;
 
-	// P, the B operand of the moment MFMAs: lane = (pixels 32pk + 8(lane >> 4) + 0..7, column
-	// lane & 15) with columns 1, x, y, x^2, xy, y^2 about the block centre (exact in bf16), then the
-	// pixel's dL/dRGB (split) for the colour gradients, then zeros.
-	hds_bf16x8 p_hi[2], p_lo[2];
+	// P^T, the A operand of the moment MFMAs: row lane % 16 = column j of P, k = pixels
+	// 32kk + 8(lane / 16) + 0..7. Rows 0-5: 1, x, y, x^2, xy, y^2 about the block centre (exact in
+	// bf16); rows 8-10: the pixel's dL/dRGB (split); other rows zero.
+	hds_bf16x8 pt_hi[2], pt_lo[2];
 	{
-		const int colj = lane & 15;
+		const int row = lane & 15;
 #pragma unroll
-		for (int pk = 0; pk < 2; pk++) {
+		for (int kk = 0; kk < 2; kk++) {
 			uint32_t d[8];
 #pragma unroll
 			for (int j = 0; j < 8; j++) {
-				const int p = 32 * pk + 8 * (lane >> 4) + j;
+				const int p = 32 * kk + 8 * (lane >> 4) + j;
 				const float xl = (float)(p & 7) - 3.5f, yl = (float)(p >> 3) - 3.5f;
 				float v = 0.0f;
-				if (colj == 0) v = 1.0f;
-				else if (colj == 1) v = xl;
-				else if (colj == 2) v = yl;
-				else if (colj == 3) v = xl * xl;
-				else if (colj == 4) v = xl * yl;
-				else if (colj == 5) v = yl * yl;
-				else if (colj < 9 && do_rgb) {
+				if (row == 0) v = 1.0f;
+				else if (row == 1) v = xl;
+				else if (row == 2) v = yl;
+				else if (row == 3) v = xl * xl;
+				else if (row == 4) v = xl * yl;
+				else if (row == 5) v = yl * yl;
+				else if (row >= 8 && row < 11 && do_rgb) {
 					const int x = wx0 + (p & 7), y = wy0 + (p >> 3);
-					if (x < a.width && y < a.height) v = a.grad_image[((int64_t)y * a.width + x) * 3 + (colj - 6)];
+					if (x < a.width && y < a.height) v = a.grad_image[((int64_t)y * a.width + x) * 3 + (row - 8)];
 				}
 				d[j] = hds_split_pack(v);
 			}
-			hds_unpack8(d, p_hi[pk], p_lo[pk]);
+			hds_unpack8(d, pt_hi[kk], pt_lo[kk]);
 		}
 	}
 
-	// dL/dF of the wave's 64 pixels in both MFMA operand layouts.
-	//   ga: A of dot, lane = (pixel 16m + (lane & 15), channels 32kk + 8(lane >> 4) + 0..7)
-	//   gb: B of dF,  lane = (pixels 32pk + 8(lane >> 4) + 0..7, channel 16n + (lane & 15))
-	hds_bf16x8 ga_hi[4][kKc], ga_lo[4][kKc], gb_hi[2][kNcb], gb_lo[2][kNcb];
+	// dL/dF^T, the B operand of the dot MFMAs, for pixel blocks n = 0..3:
+	// B[k = 8(lane / 16) + j][col = lane % 16] = dL/dF[pixel 16n + lane % 16][channel c0 + 32kk + 8(lane / 16) + j].
+	hds_bf16x8 gb_hi[4][kKc], gb_lo[4][kKc];
 	if constexpr (S > 0) {
 #pragma unroll
-		for (int m = 0; m < 4; m++) {
-			const int p = 16 * m + (lane & 15);
+		for (int n = 0; n < 4; n++) {
+			const int p = 16 * n + (lane & 15);
 			const int x = wx0 + (p & 7), y = wy0 + (p >> 3);
 			const bool in = x < a.width && y < a.height;
 			const float* src = a.grad_feature_image + ((int64_t)y * a.width + x) * a.channels + c0 + 8 * (lane >> 4);
@@ -154,45 +166,24 @@ __global__ __launch_bounds__(256) void render_backward_kernel(const BackwardArgs
 					v0 = *reinterpret_cast<const float4*>(src + 32 * kk);
 					v1 = *reinterpret_cast<const float4*>(src + 32 * kk + 4);
 				}
-				const uint32_t d[8] = {hds_split_pack(v0.x), hds_split_pack(v0.y), hds_split_pack(v0.z), hds_split_pack(v0.w),
-									   hds_split_pack(v1.x), hds_split_pack(v1.y), hds_split_pack(v1.z), hds_split_pack(v1.w)};
-				hds_unpack8(d, ga_hi[m][kk], ga_lo[m][kk]);
-			}
-		}
-#pragma unroll
-		for (int pk = 0; pk < 2; pk++) {
-#pragma unroll
-			for (int n = 0; n < kNcb; n++) {
-				uint32_t d[8];
-#pragma unroll
-				for (int j = 0; j < 8; j++) {
-					const int p = 32 * pk + 8 * (lane >> 4) + j;
-					const int x = wx0 + (p & 7), y = wy0 + (p >> 3);
-					float v = 0.0f;
-					if (x < a.width && y < a.height)
-						v = a.grad_feature_image[((int64_t)y * a.width + x) * a.channels + c0 + 16 * n + (lane & 15)];
-					d[j] = hds_split_pack(v);
-				}
-				hds_unpack8(d, gb_hi[pk][n], gb_lo[pk][n]);
+				uint32_t h[4], l[4];
+				hds_split_pair(v0.x, v0.y, h[0], l[0]);
+				hds_split_pair(v0.z, v0.w, h[1], l[1]);
+				hds_split_pair(v1.x, v1.y, h[2], l[2]);
+				hds_split_pair(v1.z, v1.w, h[3], l[3]);
+				gb_hi[n][kk] = __builtin_bit_cast(hds_bf16x8, hds_u32x4{h[0], h[1], h[2], h[3]});
+				gb_lo[n][kk] = __builtin_bit_cast(hds_bf16x8, hds_u32x4{l[0], l[1], l[2], l[3]});
 			}
 		}
 		for (int i = tid; i < kStride; i += blockDim.x) s_feat[kBatch * kStride + i] = 0u;
 	}
 
-	// Nothing past the deepest contributor of the tile can matter (backward.cu:53-60).
-	if (tid == 0) s_max_last = 0;
-	__syncthreads();
-	if (last > 0) atomicMax(&s_max_last, last);
-	__syncthreads();
 	const int2 range = a.ranges[tile];
-	const int num = min(range.y - range.x, s_max_last);
+	const int num = min(range.y - range.x, tile_max_last(last, &s_max_last));
 	const int wave_last = hds_wave_max(last);
-
-	int* slots = s_slot + wave * kGroup;
-	float* dot_rows = s_dot + wave * kGroup * kRowStride;
-	uint32_t* w_rows = s_w + wave * kGroup * kRowStride;
-	uint32_t* s_rows = s_s + wave * kGroup * kRowStride;
-	float* mom = s_mom + wave * kGroup * 16;
+	uint32_t* tr_s = s_tr[wave][0];
+	uint32_t* tr_w = s_tr[wave][1];
+	int* slots = s_slot[wave];
 
 	for (int batch_end = num; batch_end > 0; batch_end -= kBatch) {
 		const int cnt = min(kBatch, batch_end);
@@ -221,166 +212,169 @@ __global__ __launch_bounds__(256) void render_backward_kernel(const BackwardArgs
 			}
 		}
 		__syncthreads();
+		if (batch_start >= wave_last) continue;
 
 		uint64_t hits = hds_ballot(lane < cnt && batch_start + lane < wave_last &&
 								   hds_box_hits(s_box[lane < cnt ? lane : 0], rx0, rx1, ry0, ry1));
 		while (hits) {
-			// Next group: up to 16 candidates, deepest first.
-			int count = 0;
-			while (hits && count < kGroup) {
-				const int slot = 63 - __builtin_clzll(hits);
-				hits &= ~(1ull << slot);
-				if (lane == 0) slots[count] = slot;
-				count++;
+			// Next group: the (up to) 16 deepest hits. Hit bit b is position (number of hits above b).
+			const int count = min(kGeoGroup, __builtin_popcountll(hits));
+			{
+				const bool set = (hits >> lane) & 1ull;
+				const int rank = __builtin_popcountll((hits >> lane) >> 1);
+				const bool take = set && rank < kGeoGroup;
+				if (take) slots[rank] = lane;
+				if (lane >= count && lane < kGeoGroup) slots[lane] = kBatch;
+				hits &= ~hds_ballot(take);
 			}
-			if (lane >= count && lane < kGroup) slots[lane] = kBatch;
 			hds_wave_fence();
 
+			// dot[position 4h + i][own pixel] = dot[h][i] (zero without features).
+			float dot[4][4];
+#pragma unroll
+			for (int h = 0; h < 4; h++)
+#pragma unroll
+				for (int i = 0; i < 4; i++) dot[h][i] = 0.0f;
 			if constexpr (S > 0) {
-				// dot[px][g]: B = F^T, lane = (channels 32kk + 8(lane >> 4) + 0..7, position lane & 15).
+				// A = F: row lane % 16 = position, k = channels 32kk + 8(lane / 16) + 0..7.
 				const uint32_t* frow = s_feat + slots[lane & 15] * kStride + 8 * (lane >> 4);
-				hds_bf16x8 fb_hi[kKc], fb_lo[kKc];
+				hds_f32x4 X[4];
+#pragma unroll
+				for (int n = 0; n < 4; n++) X[n] = hds_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
 				for (int kk = 0; kk < kKc; kk++) {
 					const uint4 d0 = *reinterpret_cast<const uint4*>(frow + 32 * kk);
 					const uint4 d1 = *reinterpret_cast<const uint4*>(frow + 32 * kk + 4);
 					const uint32_t d[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
-					hds_unpack8(d, fb_hi[kk], fb_lo[kk]);
+					hds_bf16x8 f_hi, f_lo;
+					hds_unpack8(d, f_hi, f_lo);
+#pragma unroll
+					for (int n = 0; n < 4; n++) X[n] = hds_mfma_split(f_hi, f_lo, gb_hi[n][kk], gb_lo[n][kk], X[n]);
+				}
+				// X[n] of lane group h holds positions 4h + 0..3 of pixel 16n + lane % 16: transpose the
+				// 4x4 (group, block) arrangement, first across halves, then across neighbouring rows.
+				uint32_t t[4][4];
+#pragma unroll
+				for (int n = 0; n < 4; n++)
+#pragma unroll
+					for (int i = 0; i < 4; i++) t[n][i] = hds_swap_operand(X[n][i]);
+#pragma unroll
+				for (int i = 0; i < 4; i++) {
+#pragma unroll
+					for (int n = 0; n < 2; n++) {
+						const auto r = __builtin_amdgcn_permlane32_swap(t[n][i], t[n + 2][i], false, false);
+						t[n][i] = r[0];
+						t[n + 2][i] = r[1];
+					}
+#pragma unroll
+					for (int n = 0; n < 4; n += 2) {
+						const auto r = __builtin_amdgcn_permlane16_swap(t[n][i], t[n + 1][i], false, false);
+						t[n][i] = r[0];
+						t[n + 1][i] = r[1];
+					}
 				}
 #pragma unroll
-				for (int m = 0; m < 4; m++) {
-					hds_f32x4 dacc = {0.0f, 0.0f, 0.0f, 0.0f};
+				for (int h = 0; h < 4; h++)
 #pragma unroll
-					for (int kk = 0; kk < kKc; kk++)
-						dacc = hds_mfma_split(ga_hi[m][kk], ga_lo[m][kk], fb_hi[kk], fb_lo[kk], dacc);
-					// D: rows = pixels 16m + 4(lane >> 4) + i, column = position lane & 15.
-					*reinterpret_cast<float4*>(&dot_rows[(lane & 15) * kRowStride + 16 * m + 4 * (lane >> 4)]) =
-						make_float4(dacc[0], dacc[1], dacc[2], dacc[3]);
-				}
-				hds_wave_fence();
+					for (int i = 0; i < 4; i++) dot[h][i] = __builtin_bit_cast(float, t[h][i]);
 			}
 
 			// Back-to-front replay of the group, kIlp positions at a time: their alphas are
 			// independent, only T and the behind-sums chain through them.
 			uint32_t active = 0;
-			for (int q0 = 0; q0 < count; q0 += kIlp) {
-				int slot[kIlp];
-				float raw[kIlp], G[kIlp], dot[kIlp];
 #pragma unroll
-				for (int u = 0; u < kIlp; u++) {
-					slot[u] = slots[min(q0 + u, kGroup - 1)];
-					const int sl = min(slot[u], kBatch - 1);
-					float dx, dy;
-					raw[u] = hds_raw_alpha(fx, fy, s_mean[sl], s_conic[sl], G[u], dx, dy);
-					dot[u] = 0.0f;
-					if constexpr (S > 0) dot[u] = dot_rows[min(q0 + u, kGroup - 1) * kRowStride + lane];
-				}
-#pragma unroll
-				for (int u = 0; u < kIlp; u++) {
-					const int q = q0 + u;
-					if (q >= count) break;
-					const float alpha = fminf(HDS_MAX_ALPHA, raw[u]);
-					const bool contributes = inside && batch_start + slot[u] < last && alpha >= HDS_MIN_ALPHA;
-					float dL_dalpha = 0.0f, w = 0.0f;
-					if (contributes) {
-						const float inv_1ma = __builtin_amdgcn_rcpf(1.0f - alpha);
-						T *= inv_1ma;
-						w = alpha * T;
-						if (do_rgb) {
-							const float4 col = s_color[slot[u]];
-							rec_r = last_alpha * last_r + (1.0f - last_alpha) * rec_r;
-							rec_g = last_alpha * last_g + (1.0f - last_alpha) * rec_g;
-							rec_b = last_alpha * last_b + (1.0f - last_alpha) * rec_b;
-							last_r = col.x;
-							last_g = col.y;
-							last_b = col.z;
-							last_alpha = alpha;
-							dL_dalpha = ((col.x - rec_r) * gr + (col.y - rec_g) * gg + (col.z - rec_b) * gb) * T -
-										T_final * inv_1ma * dL_dTf;
-						}
-						if constexpr (S > 0) {
-							dL_dalpha += T * (dot[u] - behind_dot);
-							behind_dot = alpha * dot[u] + (1.0f - alpha) * behind_dot;
-						}
+			for (int q0 = 0; q0 < kGeoGroup; q0 += kIlp) {
+				// Unrolled with no early exit, so every dot[][] index stays static.
+				if (q0 < count) {
+					int slot[kIlp];
+					float raw[kIlp], G[kIlp];
+	#pragma unroll
+					for (int u = 0; u < kIlp; u++) {
+						slot[u] = slots[q0 + u];
+						const int sl = min(slot[u], kBatch - 1);
+						float dx, dy;
+						raw[u] = hds_raw_alpha(fx, fy, s_mean[sl], s_conic[sl], G[u], dx, dy);
 					}
-					// A clamped alpha no longer depends on the gaussian (backward.cu:126-135).
-					const float sg = (contributes && raw[u] <= HDS_MAX_ALPHA) ? G[u] * dL_dalpha : 0.0f;
-					s_rows[q * kRowStride + lane] = hds_split_pack(sg);
-					w_rows[q * kRowStride + lane] = hds_split_pack(w);
-					if (hds_ballot(contributes)) active |= 1u << q;
+	#pragma unroll
+					for (int u = 0; u < kIlp; u++) {
+						const int q = q0 + u;
+						const float alpha = fminf(HDS_MAX_ALPHA, raw[u]);
+						const bool contributes = q < count && batch_start + slot[u] < last && alpha >= HDS_MIN_ALPHA;
+						float dL_dalpha = 0.0f, w = 0.0f;
+						if (contributes) {
+							const float inv_1ma = __builtin_amdgcn_rcpf(1.0f - alpha);
+							T *= inv_1ma;
+							w = alpha * T;
+							if (do_rgb) {
+								const float4 col = s_color[slot[u]];
+								rec_r = last_alpha * last_r + (1.0f - last_alpha) * rec_r;
+								rec_g = last_alpha * last_g + (1.0f - last_alpha) * rec_g;
+								rec_b = last_alpha * last_b + (1.0f - last_alpha) * rec_b;
+								last_r = col.x;
+								last_g = col.y;
+								last_b = col.z;
+								last_alpha = alpha;
+								dL_dalpha = ((col.x - rec_r) * gr + (col.y - rec_g) * gg + (col.z - rec_b) * gb) * T -
+											T_final * inv_1ma * dL_dTf;
+							}
+							if constexpr (S > 0) {
+								dL_dalpha += T * (dot[q >> 2][q & 3] - behind_dot);
+								behind_dot = alpha * dot[q >> 2][q & 3] + (1.0f - alpha) * behind_dot;
+							}
+						}
+						// A clamped alpha no longer depends on the gaussian (backward.cu:126-135).
+						const float sg = (contributes && raw[u] <= HDS_MAX_ALPHA) ? G[u] * dL_dalpha : 0.0f;
+						tr_s[q * kRowStride + lane] = hds_split_pack(sg);
+						if (do_rgb) tr_w[q * kRowStride + lane] = hds_split_pack(w);
+						if (hds_ballot(contributes)) active |= 1u << q;
+					}
 				}
 			}
 			if (!active) continue;
-			for (int q = count; q < kGroup; q++) {
-				s_rows[q * kRowStride + lane] = 0u;
-				w_rows[q * kRowStride + lane] = 0u;
+#pragma unroll
+			for (int q = 0; q < kGeoGroup; q++) {
+				if (q >= count) {
+					tr_s[q * kRowStride + lane] = 0u;
+					if (do_rgb) tr_w[q * kRowStride + lane] = 0u;
+				}
 			}
 			hds_wave_fence();
 
-			// A operands over the 16 positions: lane = (position lane & 15, pixels 32pk + 8(lane >> 4) + 0..7).
-			hds_bf16x8 wa_hi[2], wa_lo[2], sa_hi[2], sa_lo[2];
+			// mom[j][position] = sum_px P^T[j][px] s[px][position]; B lane = (pixels 32kk + 8(lane / 16)
+			// + 0..7, position lane % 16). D: row 4(lane / 16) + i = j, column lane % 16 = position.
+			hds_f32x4 ms = {0.0f, 0.0f, 0.0f, 0.0f}, mw = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-			for (int pk = 0; pk < 2; pk++) {
-				const int off = (lane & 15) * kRowStride + 32 * pk + 8 * (lane >> 4);
+			for (int kk = 0; kk < 2; kk++) {
+				const int off = (lane & 15) * kRowStride + 32 * kk + 8 * (lane >> 4);
 				{
-					const uint4 d0 = *reinterpret_cast<const uint4*>(w_rows + off);
-					const uint4 d1 = *reinterpret_cast<const uint4*>(w_rows + off + 4);
+					const uint4 d0 = *reinterpret_cast<const uint4*>(tr_s + off);
+					const uint4 d1 = *reinterpret_cast<const uint4*>(tr_s + off + 4);
 					const uint32_t d[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
-					hds_unpack8(d, wa_hi[pk], wa_lo[pk]);
+					hds_bf16x8 b_hi, b_lo;
+					hds_unpack8(d, b_hi, b_lo);
+					ms = hds_mfma_split(pt_hi[kk], pt_lo[kk], b_hi, b_lo, ms);
 				}
-				{
-					const uint4 d0 = *reinterpret_cast<const uint4*>(s_rows + off);
-					const uint4 d1 = *reinterpret_cast<const uint4*>(s_rows + off + 4);
+				if (do_rgb) {
+					const uint4 d0 = *reinterpret_cast<const uint4*>(tr_w + off);
+					const uint4 d1 = *reinterpret_cast<const uint4*>(tr_w + off + 4);
 					const uint32_t d[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
-					hds_unpack8(d, sa_hi[pk], sa_lo[pk]);
+					hds_bf16x8 b_hi, b_lo;
+					hds_unpack8(d, b_hi, b_lo);
+					mw = hds_mfma_split(pt_hi[kk], pt_lo[kk], b_hi, b_lo, mw);
 				}
 			}
-			// Pixel moments of s (columns 0-5) and colour sums of w (columns 6-8).
-			{
-				hds_f32x4 ms = {0.0f, 0.0f, 0.0f, 0.0f}, mw = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-				for (int pk = 0; pk < 2; pk++) {
-					ms = hds_mfma_split(sa_hi[pk], sa_lo[pk], p_hi[pk], p_lo[pk], ms);
-					if (do_rgb) mw = hds_mfma_split(wa_hi[pk], wa_lo[pk], p_hi[pk], p_lo[pk], mw);
-				}
-				const int colj = lane & 15;
-#pragma unroll
-				for (int i = 0; i < 4; i++) {
-					const int q = 4 * (lane >> 4) + i;
-					if (colj < 6) mom[q * 16 + colj] = ms[i];
-					else if (colj < 9) mom[q * 16 + colj] = mw[i];
-				}
-			}
-			if constexpr (S > 0) {
-				if (want_dF) {
-					// D rows = positions 4(lane >> 4) + i, column = channel 16n + (lane & 15).
-					int gid4[4];
-#pragma unroll
-					for (int i = 0; i < 4; i++) {
-						const int q = 4 * (lane >> 4) + i;
-						gid4[i] = ((active >> q) & 1u) ? s_gid[min(slots[q], kBatch - 1)] : -1;
-					}
-#pragma unroll
-					for (int n = 0; n < kNcb; n++) {
-						hds_f32x4 gacc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-						for (int pk = 0; pk < 2; pk++) gacc = hds_mfma_split(wa_hi[pk], wa_lo[pk], gb_hi[pk][n], gb_lo[pk][n], gacc);
-						const int c = c0 + 16 * n + (lane & 15);
-#pragma unroll
-						for (int i = 0; i < 4; i++)
-							if (gid4[i] >= 0) atomicAdd(&a.grad_features[(int64_t)gid4[i] * a.channels + c], gacc[i]);
-					}
-				}
-			}
-			hds_wave_fence();
-			// One lane per gaussian: moments about the block centre -> gradients, then the atomics.
-			if (lane < count && ((active >> lane) & 1u)) {
-				const int sl = slots[lane];
+			// Rows 4, 5 (xy, y^2) live in lane group 1; bring them to group 0 beside rows 0-3.
+			const float m11 = hds_swap16_from_odd(ms[0]);
+			const float m02 = hds_swap16_from_odd(ms[1]);
+			const int q = lane & 15;
+			const bool mine = q < count && ((active >> q) & 1u);
+			if (lane < 16 && mine) {
+				// Moments about the block centre -> gradients (backward.cu:136-160, in moment form).
+				const int sl = slots[q];
 				const int gid = s_gid[sl];
 				const float2 mn = s_mean[sl];
 				const float4 co = s_conic[sl];
-				const float* mq = mom + lane * 16;
-				const float m00 = mq[0], m10 = mq[1], m01 = mq[2], m20 = mq[3], m11 = mq[4], m02 = mq[5];
+				const float m00 = ms[0], m10 = ms[1], m01 = ms[2], m20 = ms[3];
 				const float mx = mn.x - centre_x, my = mn.y - centre_y;
 				const float sx = m10 - mx * m00, sy = m01 - my * m00;
 				const float sxx = m20 - 2.0f * mx * m10 + mx * mx * m00;
@@ -392,23 +386,192 @@ __global__ __launch_bounds__(256) void render_backward_kernel(const BackwardArgs
 				atomicAdd(&a.grad_conics[gid * 3 + 0], -0.5f * co.w * sxx);
 				atomicAdd(&a.grad_conics[gid * 3 + 1], -co.w * sxy);
 				atomicAdd(&a.grad_conics[gid * 3 + 2], -0.5f * co.w * syy);
-				if (do_rgb) {
-					atomicAdd(&a.grad_colors[gid * 3 + 0], mq[6]);
-					atomicAdd(&a.grad_colors[gid * 3 + 1], mq[7]);
-					atomicAdd(&a.grad_colors[gid * 3 + 2], mq[8]);
-				}
+			}
+			if (do_rgb && lane >= 32 && lane < 48 && mine) {
+				// Rows 8-10: the colour gradients sum_px w dL/dRGB (backward.cu:112-118).
+				const int gid = s_gid[slots[q]];
+				atomicAdd(&a.grad_colors[gid * 3 + 0], mw[0]);
+				atomicAdd(&a.grad_colors[gid * 3 + 1], mw[1]);
+				atomicAdd(&a.grad_colors[gid * 3 + 2], mw[2]);
 			}
 			hds_wave_fence();
 		}
 	}
 }
 
+// dF[position][c] += sum_px W[position][px] dL/dF[px][c] for one group of 32 positions, then one
+// atomic per (position, channel). rows: W as [position][pixel] split-packed; gids: -1 where no
+// pixel of the wave took the gaussian.
+template <int S>
+__device__ inline void flush_features(const hds_bf16x8 (&gb_hi)[4][S / 32], const hds_bf16x8 (&gb_lo)[4][S / 32],
+									  const uint32_t* rows, const int* gids, float* grad_features, int channels, int c0,
+									  int lane) {
+	hds_wave_fence();
+	// A = W: row lane % 32 = position, k = pixels 16kp + 8(lane / 32) + 0..7.
+	hds_bf16x8 a_hi[4], a_lo[4];
+#pragma unroll
+	for (int kp = 0; kp < 4; kp++) {
+		const uint32_t* r = rows + (lane & 31) * kRowStride + 16 * kp + 8 * (lane >> 5);
+		const uint4 d0 = *reinterpret_cast<const uint4*>(r);
+		const uint4 d1 = *reinterpret_cast<const uint4*>(r + 4);
+		const uint32_t d[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+		hds_unpack8(d, a_hi[kp], a_lo[kp]);
+	}
+#pragma unroll
+	for (int cb = 0; cb < S / 32; cb++) {
+		hds_f32x16 acc = {};
+#pragma unroll
+		for (int kp = 0; kp < 4; kp++) acc = hds_mfma32_split(a_hi[kp], a_lo[kp], gb_hi[kp][cb], gb_lo[kp][cb], acc);
+		// D rows = positions 8(i / 4) + 4(lane / 32) + i % 4.
+		int gid[16];
+#pragma unroll
+		for (int g = 0; g < 4; g++) {
+			const int4 v = *reinterpret_cast<const int4*>(gids + 8 * g + 4 * (lane >> 5));
+			gid[4 * g + 0] = v.x;
+			gid[4 * g + 1] = v.y;
+			gid[4 * g + 2] = v.z;
+			gid[4 * g + 3] = v.w;
+		}
+		float* dst = grad_features + c0 + 32 * cb + (lane & 31);
+#pragma unroll
+		for (int i = 0; i < 16; i++)
+			if (gid[i] >= 0) atomicAdd(dst + (int64_t)gid[i] * channels, acc[i]);
+	}
+	hds_wave_fence();
+}
+
+template <int S>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S >= 128 ? 2 : 3))) void backward_features_kernel(
+	const BackwardArgs a) {
+	constexpr int kNcb = S / 32;
+
+	__shared__ int s_gid[kBatch];
+	__shared__ float2 s_mean[kBatch];
+	__shared__ float4 s_conic[kBatch];
+	__shared__ float4 s_box[kBatch];
+	__shared__ __attribute__((aligned(16))) uint32_t s_w[4][kFeatGroup * kRowStride];
+	__shared__ __attribute__((aligned(16))) int s_ggid[4][kFeatGroup];
+	__shared__ int s_max_last;
+
+	const int tile = hds_xcd_tile(blockIdx.x, a.num_tiles);
+	if (tile < 0) return;
+	const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+	const int slice = blockIdx.y;
+	const int tx0 = (tile % a.tiles_x) * HDS_TILE, ty0 = (tile / a.tiles_x) * HDS_TILE;
+	const int wx0 = tx0 + (wave & 1) * 8, wy0 = ty0 + (wave >> 1) * 8;
+	const int px = wx0 + (lane & 7), py = wy0 + (lane >> 3);
+	const bool inside = px < a.width && py < a.height;
+	const float fx = (float)px + 0.5f, fy = (float)py + 0.5f;
+	const float rx0 = (float)wx0 + 0.5f, rx1 = (float)wx0 + 7.5f;
+	const float ry0 = (float)wy0 + 0.5f, ry1 = (float)wy0 + 7.5f;
+	const int c0 = slice * S;
+	const int last = inside ? a.n_contrib[(int64_t)py * a.width + px] : 0;
+
+	// dL/dF, the B operand with K = pixels, for pixel steps kp = 0..3:
+	// B[k = 8(lane / 32) + j][col = lane % 32] = dL/dF[pixel 16kp + 8(lane / 32) + j][channel c0 + 32cb + lane % 32].
+	hds_bf16x8 gb_hi[4][kNcb], gb_lo[4][kNcb];
+#pragma unroll
+	for (int kp = 0; kp < 4; kp++) {
+#pragma unroll
+		for (int cb = 0; cb < kNcb; cb++) {
+			float v[8];
+#pragma unroll
+			for (int j = 0; j < 8; j++) {
+				const int p = 16 * kp + 8 * (lane >> 5) + j;
+				const int x = wx0 + (p & 7), y = wy0 + (p >> 3);
+				v[j] = 0.0f;
+				if (x < a.width && y < a.height)
+					v[j] = a.grad_feature_image[((int64_t)y * a.width + x) * a.channels + c0 + 32 * cb + (lane & 31)];
+			}
+			uint32_t h[4], l[4];
+#pragma unroll
+			for (int i = 0; i < 4; i++) hds_split_pair(v[2 * i], v[2 * i + 1], h[i], l[i]);
+			gb_hi[kp][cb] = __builtin_bit_cast(hds_bf16x8, hds_u32x4{h[0], h[1], h[2], h[3]});
+			gb_lo[kp][cb] = __builtin_bit_cast(hds_bf16x8, hds_u32x4{l[0], l[1], l[2], l[3]});
+		}
+	}
+
+	const int2 range = a.ranges[tile];
+	const int num = min(range.y - range.x, tile_max_last(last, &s_max_last));
+	const int wave_last = hds_wave_max(last);
+	uint32_t* rows = s_w[wave];
+	int* gids = s_ggid[wave];
+
+	float T = 1.0f;
+	int q = 0;  // filled positions of the wave's current group
+	for (int batch = 0; batch < num; batch += kBatch) {
+		const int cnt = min(kBatch, num - batch);
+		__syncthreads();
+		if (tid < cnt) {
+			const int gid = a.values[range.x + batch + tid];
+			const float2 m = a.means2D[gid];
+			const float4 co = a.conic4[gid];
+			s_gid[tid] = gid;
+			s_mean[tid] = m;
+			s_conic[tid] = co;
+			s_box[tid] = hds_cull_box(m, co);
+		}
+		__syncthreads();
+		if (batch >= wave_last) continue;
+
+		uint64_t hits = hds_ballot(lane < cnt && batch + lane < wave_last &&
+								   hds_box_hits(s_box[lane < cnt ? lane : 0], rx0, rx1, ry0, ry1));
+		while (hits) {
+			// The next (up to) kIlp hits in list order, as many as the group has room for.
+			const int take = min(min(kIlp, __builtin_popcountll(hits)), kFeatGroup - q);
+			int slot[kIlp];
+			float alpha[kIlp];
+#pragma unroll
+			for (int u = 0; u < kIlp; u++) {
+				slot[u] = kBatch - 1;
+				if (u < take) {
+					slot[u] = __builtin_ctzll(hits);
+					hits &= hits - 1;
+				}
+				float G, dx, dy;
+				alpha[u] = fminf(HDS_MAX_ALPHA, hds_raw_alpha(fx, fy, s_mean[slot[u]], s_conic[slot[u]], G, dx, dy));
+			}
+#pragma unroll
+			for (int u = 0; u < kIlp; u++) {
+				if (u >= take) break;
+				// The forward's test, with its termination read from n_contrib.
+				const bool contributes = batch + slot[u] < last && alpha[u] >= HDS_MIN_ALPHA;
+				float w = 0.0f;
+				if (contributes) {
+					const float test_T = T * (1.0f - alpha[u]);
+					w = alpha[u] * T;
+					T = test_T;
+				}
+				rows[(q + u) * kRowStride + lane] = hds_split_pack(w);
+				const bool any = hds_ballot(contributes) != 0;
+				if (lane == 0) gids[q + u] = any ? s_gid[slot[u]] : -1;
+			}
+			q += take;
+			if (q == kFeatGroup) {
+				flush_features<S>(gb_hi, gb_lo, rows, gids, a.grad_features, a.channels, c0, lane);
+				q = 0;
+			}
+		}
+	}
+	if (q > 0) {
+		for (int r = q; r < kFeatGroup; r++) rows[r * kRowStride + lane] = 0u;
+		if (lane >= q && lane < kFeatGroup) gids[lane] = -1;
+		flush_features<S>(gb_hi, gb_lo, rows, gids, a.grad_features, a.channels, c0, lane);
+	}
+}
+
 template <int S, bool RGB>
-int launch(const BackwardArgs& a, int num_tiles, int slices, hipStream_t s) {
-	render_backward_kernel<S, RGB><<<dim3((unsigned)num_tiles, (unsigned)slices), 256, 0, s>>>(a);
-	return hds_check_launch(RGB ? (S > 0 ? "render_backward_rgb_features" : "render_backward_rgb")
-								: "render_backward_features",
+int launch_geometry(const BackwardArgs& a, int slices, hipStream_t s) {
+	backward_geometry_kernel<S, RGB><<<dim3(hds_xcd_grid(a.num_tiles), (unsigned)slices), 256, 0, s>>>(a);
+	return hds_check_launch(RGB ? (S > 0 ? "backward_geometry_rgb_features" : "backward_geometry_rgb")
+								: "backward_geometry_features",
 							s);
+}
+
+template <int S>
+int launch_features(const BackwardArgs& a, int slices, hipStream_t s) {
+	backward_features_kernel<S><<<dim3(hds_xcd_grid(a.num_tiles), (unsigned)slices), 256, 0, s>>>(a);
+	return hds_check_launch("backward_features", s);
 }
 
 __global__ __launch_bounds__(256) void zero_kernel(float* __restrict__ p, int64_t count) {
@@ -466,6 +629,7 @@ int render_backward(bool zero_outputs, int64_t n, int width, int height, int cha
 				   height,
 				   tiles_x,
 				   feats ? channels : 0,
+				   num_tiles,
 				   reinterpret_cast<const int2*>(tile_ranges),
 				   values_sorted,
 				   reinterpret_cast<const float2*>(means2D),
@@ -482,12 +646,19 @@ int render_backward(bool zero_outputs, int64_t n, int width, int height, int cha
 				   grad_colors,
 				   grad_opacities,
 				   feats ? grad_features : nullptr};
-	if (!feats) return launch<0, true>(a, num_tiles, 1, s);
+	if (!feats) return launch_geometry<0, true>(a, 1, s);
 	const int slices = channels / slice_width;
+	int st;
 	switch (slice_width) {
-		case 32: return rgb ? launch<32, true>(a, num_tiles, slices, s) : launch<32, false>(a, num_tiles, slices, s);
-		case 64: return rgb ? launch<64, true>(a, num_tiles, slices, s) : launch<64, false>(a, num_tiles, slices, s);
-		default: return rgb ? launch<128, true>(a, num_tiles, slices, s) : launch<128, false>(a, num_tiles, slices, s);
+		case 32: st = rgb ? launch_geometry<32, true>(a, slices, s) : launch_geometry<32, false>(a, slices, s); break;
+		case 64: st = rgb ? launch_geometry<64, true>(a, slices, s) : launch_geometry<64, false>(a, slices, s); break;
+		default: st = rgb ? launch_geometry<128, true>(a, slices, s) : launch_geometry<128, false>(a, slices, s); break;
+	}
+	if (st != HDS_OK || !grad_features) return st;
+	switch (slice_width) {
+		case 32: return launch_features<32>(a, slices, s);
+		case 64: return launch_features<64>(a, slices, s);
+		default: return launch_features<128>(a, slices, s);
 	}
 }
 
