@@ -45,6 +45,9 @@ def parse_args():
                     help="features without requires_grad: the backward keeps the feature term of the geometry "
                          "gradients but writes no grad_features (reference test_render.py:118-134)")
     ap.add_argument("--rgb-only", action="store_true", help="render RGB without features (features=None)")
+    ap.add_argument("--calibrate-copy-mib", type=int, default=0,
+                    help="after the run, copy a buffer of this many MiB device to device once: the plain copy "
+                         "kernel whose FETCH_SIZE / WRITE_SIZE calibrate the --pmc traffic figures")
     ap.add_argument("--bwd-slice", type=int, default=None,
                     help="channels per backward work-group (gaussian_splatting.rasterizer.FEATURE_SLICE_WIDTH)")
     return ap.parse_args()
@@ -75,7 +78,7 @@ def main() -> int:
     import torch.nn.functional as F
 
     from gaussian_splatting.rasterizer import _get_rasterizer, project_gaussians, rasterize
-    from gaussian_splatting.rasterizer._native import StageTimer
+    from gaussian_splatting.rasterizer._native import KernelProfile, StageTimer
     from gaussian_splatting.utils.sh import eval_sh
     from tests.scenes import synthetic_config, upstream, view_dirs
 
@@ -148,14 +151,16 @@ def main() -> int:
     step_events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                    for _ in range(args.steps)]
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for start, end in step_events:
-        start.record()
-        step()
-        end.record()
-    torch.cuda.synchronize()
-    wall_ms = (time.perf_counter() - t0) * 1e3
+    with KernelProfile() as kprof:
+        t0 = time.perf_counter()
+        for start, end in step_events:
+            start.record()
+            step()
+            end.record()
+        torch.cuda.synchronize()
+        wall_ms = (time.perf_counter() - t0) * 1e3
     ext.timer = None
+    kernels = kprof.summary()
     stages = timer.summary()
     step_ms = [s.elapsed_time(e) for s, e in step_events]
     ms_per_step = wall_ms / args.steps
@@ -202,13 +207,19 @@ def main() -> int:
             bwd.append(s2.elapsed_time(e2))
         split = {"fwd_ms_median": round(statistics.median(fwd), 4), "bwd_ms_median": round(statistics.median(bwd), 4)}
 
-    rb = stage_report.get("render_backward", {})
-    rb_ms = stages["render_backward"]["mean_ms"]
-    achieved = alg["render_backward"] / (rb_ms * 1e-3) / 1e9
-    roofline = {"kernel": "render_backward_kernel (hds_render_backward_accumulate)", "bound": "hbm",
+    # Roofline of the blend backward: its two kernels (back-to-front geometry/colour gradients and
+    # front-to-back feature gradients) are one hds_render_backward call; their HIP-event durations,
+    # recorded per launch inside the library over the timed region, are summed per step.
+    bwd_names = [k for k in ("backward_geometry_kernel", "backward_features_kernel") if k in kernels]
+    bwd_ms = sum(kernels[k]["total_ms"] for k in bwd_names) / args.steps
+    achieved = alg["render_backward"] / (bwd_ms * 1e-3) / 1e9
+    roofline = {"kernel": " + ".join(bwd_names) + " (hds_render_backward_accumulate)", "bound": "hbm",
                 "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                "algorithmic_bytes": int(alg["render_backward"]), "mean_launch_ms": round(rb_ms, 4)}
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_per_step(bwd_names),
+                "algorithmic_bytes": int(alg["render_backward"]), "ms_per_step": round(bwd_ms, 4),
+                "kernel_mean_ms": {k: round(kernels[k]["mean_ms"], 4) for k in bwd_names}}
+    kernel_report = {k: {"launches_per_step": round(v["launches"] / args.steps, 2), "mean_ms": round(v["mean_ms"], 4)}
+                     for k, v in sorted(kernels.items(), key=lambda kv: -kv[1]["total_ms"])}
     total_alg = sum(alg.values())
     step_frac = total_alg / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS
 
@@ -226,10 +237,38 @@ def main() -> int:
                    "visible": n_vis, "pairs": pairs, "parallelism": "single-gpu"},
         "step_ms_median": round(statistics.median(step_ms), 4), **split,
         "step_hbm_frac": round(step_frac, 4), "step_algorithmic_MB": round(total_alg / 1e6, 1),
-        "roofline": roofline, "stages": stage_report, "cpu_baseline": cpu,
+        "roofline": roofline, "stages": stage_report, "kernels": kernel_report, "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+    if args.calibrate_copy_mib > 0:
+        n_floats = args.calibrate_copy_mib * (1 << 20) // 4
+        src = torch.ones(n_floats, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"[bench] calibration copy: {n_floats * 4} bytes read and written", file=sys.stderr, flush=True)
     return 0
+
+
+TRAFFIC_FILE = ROOT / "profiles" / "render_backward_headline_c128_pmc.md"
+
+
+def traffic_per_step(kernel_names) -> int | None:
+    """HBM bytes the named kernels move per step, from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by a copy kernel of known size); None if that
+    summary does not cover every one of them."""
+    if not TRAFFIC_FILE.exists():
+        return None
+    per_kernel = {}
+    for line in TRAFFIC_FILE.read_text().splitlines():
+        # rows of the form "| kernel | ... | traffic_bytes |" with the bytes in the last column
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) >= 2 and cells[0] in kernel_names and cells[-1].isdigit():
+            per_kernel[cells[0]] = int(cells[-1])
+    if not kernel_names or any(k not in per_kernel for k in kernel_names):
+        return None
+    return sum(per_kernel[k] for k in kernel_names)
 
 
 def cpu_baseline(wl, colors, grad_image, grad_features):

@@ -151,11 +151,17 @@ __global__ __launch_bounds__(kThreads) void scan_apply_kernel(const uint32_t* __
 int exclusive_scan(const uint32_t* in, const uint32_t* idx, int64_t n, uint32_t* out, uint32_t* sums,
 				   uint64_t* total, hipStream_t s) {
 	const int64_t blocks = tiles_of(n);
+	HdsKernelTimer timer1("scan_reduce_kernel", s);
 	scan_reduce_kernel<<<(unsigned)blocks, kThreads, 0, s>>>(in, idx, n, sums);
+	timer1.stop();
 	HDS_LAUNCH_CHECK("scan_reduce", s);
+	HdsKernelTimer timer2("scan_top_kernel", s);
 	scan_top_kernel<<<1, 1024, 0, s>>>(sums, blocks, total);
+	timer2.stop();
 	HDS_LAUNCH_CHECK("scan_top", s);
+	HdsKernelTimer timer3("scan_apply_kernel", s);
 	scan_apply_kernel<<<(unsigned)blocks, kThreads, 0, s>>>(in, idx, n, sums, out);
+	timer3.stop();
 	HDS_LAUNCH_CHECK("scan_apply", s);
 	return HDS_OK;
 }
@@ -249,13 +255,17 @@ int radix_sort(uint32_t* keys_a, uint32_t* vals_a, uint32_t* keys_b, uint32_t* v
 	const int passes = (bits + kRadixBits - 1) / kRadixBits;
 	uint32_t *kin = keys_a, *vin = vals_a, *kout = keys_b, *vout = vals_b;
 	for (int p = 0; p < passes; p++) {
+		HdsKernelTimer timer4("radix_hist_kernel", s);
 		radix_hist_kernel<<<(unsigned)blocks, kThreads, 0, s>>>(kin, n, p * kRadixBits, (uint32_t)blocks, hist);
+		timer4.stop();
 		HDS_LAUNCH_CHECK("radix_hist", s);
 		int st = exclusive_scan(hist, nullptr, (int64_t)kRadix * blocks, hist, sums, nullptr, s);
 		if (st != HDS_OK) return st;
 		const bool last = p == passes - 1;
+		HdsKernelTimer timer5("radix_scatter_kernel", s);
 		radix_scatter_kernel<<<(unsigned)blocks, kThreads, 0, s>>>(kin, vin, (last && !keys_final_needed) ? nullptr : kout,
 																   vout, n, p * kRadixBits, (uint32_t)blocks, hist);
+		timer5.stop();
 		HDS_LAUNCH_CHECK("radix_scatter", s);
 		uint32_t* t;
 		t = kin; kin = kout; kout = t;
@@ -441,9 +451,11 @@ extern "C" int hds_bin_count(int64_t n, const float* means2D, const float* depth
 	uint32_t* sums = at<uint32_t>(workspace, g.sums);
 	uint64_t* total = at<uint64_t>(workspace, g.total);
 
+	HdsKernelTimer timer6("prepare_kernel", s);
 	prepare_kernel<<<hds_blocks(n, kThreads), kThreads, 0, s>>>(
 		n, means2D, depths, radii, conics, colors, opacities, tiles_x, tiles_y, reinterpret_cast<float4*>(conic4),
 		reinterpret_cast<float4*>(color_opacity4), counts, rects, keys_a, vals_a);
+	timer6.stop();
 	HDS_LAUNCH_CHECK("prepare_gaussians", s);
 	// 4 passes: the depth order ends back in (keys_a, vals_a).
 	int st = radix_sort(keys_a, vals_a, keys_b, vals_b, n, 32, hist, sums, false, s);
@@ -469,8 +481,10 @@ extern "C" int hds_bin_emit(int64_t n, int64_t num_pairs, int width, int height,
 	const int tiles_x = (width + HDS_TILE - 1) / HDS_TILE, tiles_y = (height + HDS_TILE - 1) / HDS_TILE;
 	const int64_t num_tiles = (int64_t)tiles_x * tiles_y;
 	hipStream_t s = (hipStream_t)stream;
+	HdsKernelTimer timer7("fill_kernel", s);
 	fill_kernel<<<hds_blocks(2 * num_tiles, kThreads), kThreads, 0, s>>>(reinterpret_cast<uint32_t*>(tile_ranges),
 																		  2 * num_tiles, 0u);
+	timer7.stop();
 	HDS_LAUNCH_CHECK("fill_tile_ranges", s);
 	if (num_pairs == 0) return HDS_OK;
 	const PairSpace p = pair_space(num_pairs);
@@ -496,14 +510,18 @@ extern "C" int hds_bin_emit(int64_t n, int64_t num_pairs, int width, int height,
 	uint32_t* vals_a = (passes % 2 == 0) ? out : vals_tmp;
 	uint32_t* vals_b = (passes % 2 == 0) ? vals_tmp : out;
 
+	HdsKernelTimer timer8("emit_kernel", s);
 	emit_kernel<<<hds_blocks(num_pairs, kThreads), kThreads, 0, s>>>(n, num_pairs, offsets, order, rects, tiles_x,
 																	  keys_a, vals_a);
+	timer8.stop();
 	HDS_LAUNCH_CHECK("emit_pairs", s);
 	int st = radix_sort(keys_a, vals_a, keys_b, vals_b, num_pairs, bits, hist, sums, true, s);
 	if (st != HDS_OK) return st;
 	const uint32_t* keys_sorted = (passes % 2 == 0) ? keys_a : keys_b;
+	HdsKernelTimer timer9("ranges_kernel", s);
 	ranges_kernel<<<hds_blocks(num_pairs, kThreads), kThreads, 0, s>>>(num_pairs, keys_sorted,
 																		reinterpret_cast<int2*>(tile_ranges));
+	timer9.stop();
 	HDS_LAUNCH_CHECK("identify_tile_ranges", s);
 	return HDS_OK;
 }

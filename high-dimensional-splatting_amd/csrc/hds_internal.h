@@ -43,6 +43,20 @@ int hds_check_launch(const char* kernel, hipStream_t stream);
 			return hds_set_error(HDS_ERR_RUNTIME, "%s failed: %s", #call, hipGetErrorString(_e)); \
 	} while (0)
 
+/* Brackets one kernel launch with HIP events while hds_profile_begin() recording is on (no-op
+ * otherwise): construct it right before the launch and call stop() right after it. */
+class HdsKernelTimer {
+   public:
+	HdsKernelTimer(const char* name, hipStream_t stream);
+	void stop();
+	HdsKernelTimer(const HdsKernelTimer&) = delete;
+	HdsKernelTimer& operator=(const HdsKernelTimer&) = delete;
+
+   private:
+	int64_t slot_;
+	hipStream_t stream_;
+};
+
 static inline unsigned hds_blocks(int64_t n, int threads) { return (unsigned)((n + threads - 1) / threads); }
 
 /* ------------------------------------------------------------------------------------------- */

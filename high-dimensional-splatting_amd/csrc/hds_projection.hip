@@ -230,8 +230,10 @@ extern "C" int hds_project_gaussians(int64_t n, const float* means, const float*
 				"project_gaussians: null pointer argument");
 	hipStream_t s = (hipStream_t)stream;
 	const Camera cam = make_camera(fx, fy, cx, cy, width, height, near_plane, low_pass, fov_scale);
+	HdsKernelTimer timer1("project_forward_kernel", s);
 	project_forward_kernel<<<hds_blocks(n, 256), 256, 0, s>>>(n, cam, world_to_camera, means, scales, quats,
 															  opacities, means2D, depths, radii, conics);
+	timer1.stop();
 	HDS_LAUNCH_CHECK("project_forward", s);
 	return HDS_OK;
 }
@@ -249,9 +251,11 @@ extern "C" int hds_project_gaussians_backward(int64_t n, const float* grad_means
 				"project_gaussians_backward: null pointer argument");
 	hipStream_t s = (hipStream_t)stream;
 	const Camera cam = make_camera(fx, fy, cx, cy, width, height, near_plane, low_pass, fov_scale);
+	HdsKernelTimer timer2("project_backward_kernel", s);
 	project_backward_kernel<<<hds_blocks(n, 256), 256, 0, s>>>(n, cam, world_to_camera, means, scales, quats,
 															   grad_means2D, grad_conics, grad_means, grad_scales,
 															   grad_quats);
+	timer2.stop();
 	HDS_LAUNCH_CHECK("project_backward", s);
 	return HDS_OK;
 }

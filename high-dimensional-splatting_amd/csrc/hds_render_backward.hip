@@ -562,7 +562,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S >= 128 ? 
 
 template <int S, bool RGB>
 int launch_geometry(const BackwardArgs& a, int slices, hipStream_t s) {
+	HdsKernelTimer timer1("backward_geometry_kernel", s);
 	backward_geometry_kernel<S, RGB><<<dim3(hds_xcd_grid(a.num_tiles), (unsigned)slices), 256, 0, s>>>(a);
+	timer1.stop();
 	return hds_check_launch(RGB ? (S > 0 ? "backward_geometry_rgb_features" : "backward_geometry_rgb")
 								: "backward_geometry_features",
 							s);
@@ -570,7 +572,9 @@ int launch_geometry(const BackwardArgs& a, int slices, hipStream_t s) {
 
 template <int S>
 int launch_features(const BackwardArgs& a, int slices, hipStream_t s) {
+	HdsKernelTimer timer2("backward_features_kernel", s);
 	backward_features_kernel<S><<<dim3(hds_xcd_grid(a.num_tiles), (unsigned)slices), 256, 0, s>>>(a);
+	timer2.stop();
 	return hds_check_launch("backward_features", s);
 }
 
@@ -581,7 +585,9 @@ __global__ __launch_bounds__(256) void zero_kernel(float* __restrict__ p, int64_
 
 int zero(float* p, int64_t count, hipStream_t s) {
 	if (!p || count == 0) return HDS_OK;
+	HdsKernelTimer timer3("zero_kernel", s);
 	zero_kernel<<<hds_blocks(count, 256), 256, 0, s>>>(p, count);
+	timer3.stop();
 	return hds_check_launch("zero_gradients", s);
 }
 

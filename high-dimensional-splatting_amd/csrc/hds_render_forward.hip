@@ -254,7 +254,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S > 0 ? 2 :
 
 template <int S, bool RGB>
 int launch(const RenderArgs& a, int num_tiles, int slices, hipStream_t s) {
+	HdsKernelTimer timer1("render_forward_kernel", s);
 	render_forward_kernel<S, RGB><<<dim3(hds_xcd_grid(num_tiles), (unsigned)slices), 256, 0, s>>>(a);
+	timer1.stop();
 	return hds_check_launch(RGB ? (S > 0 ? "render_rgb_features" : "render_rgb") : "render_features", s);
 }
 

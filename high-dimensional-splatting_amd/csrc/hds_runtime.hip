@@ -5,6 +5,8 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
+#include <mutex>
+#include <vector>
 
 #include "hds_internal.h"
 #include "hds_rasterizer.h"
@@ -39,3 +41,65 @@ int hds_check_launch(const char* kernel, hipStream_t stream) {
 extern "C" const char* hds_last_error(void) { return g_last_error; }
 
 extern "C" int hds_abi_version(void) { return HDS_ABI_VERSION; }
+
+// Kernel timing: a pool of event pairs reused across recordings, one pair per recorded launch.
+namespace {
+struct ProfileRecord {
+	const char* name;
+	hipEvent_t start, stop;
+};
+std::mutex g_profile_mutex;
+bool g_profile_on = false;
+std::vector<ProfileRecord> g_profile;
+int64_t g_profile_used = 0;
+}  // namespace
+
+HdsKernelTimer::HdsKernelTimer(const char* name, hipStream_t stream) : slot_(-1), stream_(stream) {
+	std::lock_guard<std::mutex> lock(g_profile_mutex);
+	if (!g_profile_on) return;
+	if (g_profile_used == (int64_t)g_profile.size()) {
+		ProfileRecord r{name, nullptr, nullptr};
+		if (hipEventCreate(&r.start) != hipSuccess) return;
+		if (hipEventCreate(&r.stop) != hipSuccess) {
+			(void)hipEventDestroy(r.start);
+			return;
+		}
+		g_profile.push_back(r);
+	}
+	ProfileRecord& r = g_profile[g_profile_used];
+	r.name = name;
+	if (hipEventRecord(r.start, stream) != hipSuccess) return;
+	slot_ = g_profile_used++;
+}
+
+void HdsKernelTimer::stop() {
+	if (slot_ < 0) return;
+	std::lock_guard<std::mutex> lock(g_profile_mutex);
+	(void)hipEventRecord(g_profile[slot_].stop, stream_);
+	slot_ = -1;
+}
+
+extern "C" int hds_profile_begin(void) {
+	std::lock_guard<std::mutex> lock(g_profile_mutex);
+	g_profile_used = 0;
+	g_profile_on = true;
+	return HDS_OK;
+}
+
+extern "C" int64_t hds_profile_end(void) {
+	std::lock_guard<std::mutex> lock(g_profile_mutex);
+	g_profile_on = false;
+	for (int64_t i = 0; i < g_profile_used; i++) {
+		const hipError_t e = hipEventSynchronize(g_profile[i].stop);
+		if (e != hipSuccess) return -hds_set_error(HDS_ERR_RUNTIME, "hds_profile_end: %s", hipGetErrorString(e));
+	}
+	return g_profile_used;
+}
+
+extern "C" int hds_profile_record(int64_t i, const char** name, float* ms) {
+	std::lock_guard<std::mutex> lock(g_profile_mutex);
+	HDS_REQUIRE(i >= 0 && i < g_profile_used && name && ms, "hds_profile_record: no record %lld", (long long)i);
+	*name = g_profile[i].name;
+	HDS_HIP(hipEventElapsedTime(ms, g_profile[i].start, g_profile[i].stop));
+	return HDS_OK;
+}

@@ -194,7 +194,9 @@ extern "C" int hds_eval_sh(int64_t n, int degree, const float* sh_dc, const floa
 	if (n == 0) return HDS_OK;
 	HDS_REQUIRE(sh_dc && sh_rest && dirs && radii && rgb, "eval_sh: null pointer argument");
 	hipStream_t s = (hipStream_t)stream;
+	HdsKernelTimer timer1("eval_sh_kernel", s);
 	eval_sh_kernel<<<hds_blocks(n, 256), 256, 0, s>>>(n, (degree + 1) * (degree + 1), sh_dc, sh_rest, dirs, radii, rgb);
+	timer1.stop();
 	HDS_LAUNCH_CHECK("eval_sh_forward", s);
 	return HDS_OK;
 }
@@ -214,9 +216,11 @@ extern "C" int hds_eval_sh_backward_adam(int64_t n, int degree, const float* gra
 	// 1 - beta is formed in double, as torch does (sh.cu:85, 179-180).
 	AdamArgs a{(float)lr_dc, (float)lr_rest, (float)beta1, (float)beta2, (float)(1.0 - beta1), (float)(1.0 - beta2),
 			   (float)eps};
+	HdsKernelTimer timer2("eval_sh_backward_adam_kernel", s);
 	eval_sh_backward_adam_kernel<<<hds_blocks(n, kShAdamBlock), kShAdamBlock, 0, s>>>(
 		n, (degree + 1) * (degree + 1), grad_rgb, sh_dc, sh_rest, dirs, radii, m_dc, v_dc, m_rest, v_rest, step_dc,
 		step_rest, a, grad_dirs);
+	timer2.stop();
 	HDS_LAUNCH_CHECK("eval_sh_backward_adam", s);
 	return HDS_OK;
 }

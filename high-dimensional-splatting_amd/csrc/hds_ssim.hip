@@ -173,7 +173,9 @@ extern "C" int hds_ssim_forward(int height, int width, const float* rendered, co
 	if (st != HDS_OK) return st;
 	hipStream_t s = (hipStream_t)stream;
 	const dim3 grid((unsigned)((width + kTx - 1) / kTx), (unsigned)((height + kTy - 1) / kTy));
+	HdsKernelTimer timer1("ssim_forward_kernel", s);
 	ssim_forward_kernel<<<grid, 256, 0, s>>>(height, width, rendered, gt, ssim_map, d_mu, d_aa, d_ab);
+	timer1.stop();
 	HDS_LAUNCH_CHECK("ssim_forward", s);
 	return HDS_OK;
 }
@@ -187,7 +189,9 @@ extern "C" int hds_ssim_backward(int height, int width, const float* grad_mean, 
 	if (st != HDS_OK) return st;
 	hipStream_t s = (hipStream_t)stream;
 	const dim3 grid((unsigned)((width + kTx - 1) / kTx), (unsigned)((height + kTy - 1) / kTy));
+	HdsKernelTimer timer2("ssim_backward_kernel", s);
 	ssim_backward_kernel<<<grid, 256, 0, s>>>(height, width, grad_mean, rendered, gt, d_mu, d_aa, d_ab, grad_rendered);
+	timer2.stop();
 	HDS_LAUNCH_CHECK("ssim_backward", s);
 	return HDS_OK;
 }

@@ -158,6 +158,19 @@ HDS_API int hds_ssim_backward(int height, int width, const float* grad_mean, con
 					  const float* gt, const float* d_mu, const float* d_aa, const float* d_ab,
 					  float* grad_rendered, hds_stream_t stream);
 
+/* ---- kernel timing (no counterpart in the reference; for benchmarks) ------------------------ */
+
+/* Starts recording: from now on every hot-path kernel launch (projection, blend forward, the two
+ * blend-backward kernels) is bracketed by HIP events on its own stream. Clears earlier records. */
+HDS_API int hds_profile_begin(void);
+
+/* Stops recording, waits for the recorded events and returns how many launches were recorded
+ * (negative on error). */
+HDS_API int64_t hds_profile_end(void);
+
+/* Kernel name and duration in ms of record i (0 <= i < the count hds_profile_end returned). */
+HDS_API int hds_profile_record(int64_t i, const char** name, float* ms);
+
 #ifdef __cplusplus
 }
 #endif

@@ -61,6 +61,19 @@ def test_abi_version_matches_header(lib):
     assert lib.hds_abi_version() == version
 
 
+def test_kernel_profile_records_nothing_without_launches(lib):
+    """hds_profile_* brackets kernel launches with events; with no launch in between there is nothing
+    to record, and asking for a record that does not exist is an error with a message."""
+    from gaussian_splatting.rasterizer._native import KernelProfile
+
+    with KernelProfile() as prof:
+        pass
+    assert prof.records == [] and prof.summary() == {}
+    name, ms = ctypes.c_char_p(), ctypes.c_float()
+    assert lib.hds_profile_record(0, ctypes.byref(name), ctypes.byref(ms)) != 0
+    assert b"no record 0" in lib.hds_last_error()
+
+
 def test_workspace_queries_grow_with_the_problem(lib):
     small = lib.hds_bin_workspace_bytes(1000, 128, 128)
     big = lib.hds_bin_workspace_bytes(1_000_000, 128, 128)
