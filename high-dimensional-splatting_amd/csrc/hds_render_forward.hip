@@ -23,6 +23,7 @@
 
 #include "hds_internal.h"
 #include "hds_rasterizer.h"
+#include "hds_stage.h"
 
 namespace {
 
@@ -45,20 +46,13 @@ struct RenderArgs {
 	float* feature_image;
 };
 
-template <int S>
-struct FeatTraits {
-	static constexpr int kNcb = S / 32;    // 32-channel MFMA row blocks
-	static constexpr int kStride = S + 4;  // words per staged feature row (16-byte aligned)
-};
-
 // acc[m][cb] += F^T W for one group. w_hi / w_lo hold this lane's pixel's packed weights for
 // positions (2i, 2i+1); after the swaps, words 0-3 are the B operand of pixels 0-31 and words 4-7
-// that of pixels 32-63. A = features: lane = (channel lane % 32, positions 8 (lane / 32) + 0..7).
+// that of pixels 32-63. A = features: lane = (channel lane % 32, positions 8 (lane / 32) + 0..7),
+// read as raw fp32 from the staged rows (S floats each) and split here.
 template <int S>
-__device__ inline void flush_group(hds_f32x16 (&acc)[2][FeatTraits<S>::kNcb], uint32_t (&w_hi)[8], uint32_t (&w_lo)[8],
-								   const int (&slot)[kGroup], const uint32_t* s_feat, int lane) {
-	constexpr int kNcb = FeatTraits<S>::kNcb;
-	constexpr int kStride = FeatTraits<S>::kStride;
+__device__ inline void flush_group(hds_f32x16 (&acc)[2][S / 32], uint32_t (&w_hi)[8], uint32_t (&w_lo)[8],
+								   const int (&slot)[kGroup], const float* feat, int lane) {
 #pragma unroll
 	for (int i = 0; i < 4; i++) {
 		const auto h = __builtin_amdgcn_permlane32_swap(w_hi[i], w_hi[4 + i], false, false);
@@ -81,34 +75,49 @@ __device__ inline void flush_group(hds_f32x16 (&acc)[2][FeatTraits<S>::kNcb], ui
 	for (int j = 0; j < 8; j++) {
 		// Select the values, not the array half: an indexed pointer select would put slot in scratch.
 		const int lo = slot[j], hi = slot[8 + j];
-		row[j] = (upper ? hi : lo) * kStride + col;
+		row[j] = (upper ? hi : lo) * S + col;
 	}
 #pragma unroll
-	for (int cb = 0; cb < kNcb; cb++) {
-		uint32_t d[8];
+	for (int cb = 0; cb < S / 32; cb++) {
+		float v[8];
 #pragma unroll
-		for (int j = 0; j < 8; j++) d[j] = s_feat[row[j] + 32 * cb];
+		for (int j = 0; j < 8; j++) v[j] = feat[row[j] + 32 * cb];
 		hds_bf16x8 a_hi, a_lo;
-		hds_unpack8(d, a_hi, a_lo);
+		hds_split8(v, a_hi, a_lo);
 #pragma unroll
 		for (int m = 0; m < 2; m++) acc[m][cb] = hds_mfma32_split(a_hi, a_lo, b_hi[m], b_lo[m], acc[m][cb]);
 	}
 }
 
-// Occupancy: the accumulators (S per lane) live in AGPRs next to at most 128 VGPRs, two waves per
-// SIMD with features, more without.
+// Per-lane state of the walk.
+struct Pixel {
+	float T;
+	bool done;
+	int last;
+	float r, g, b;
+};
+
+// Occupancy: S accumulators per lane plus the walk's registers, two waves per SIMD with features.
+//
+// Pipeline per batch b (parity p): gids of b+1 are in s_gid[p^1] and its feature rows are already
+// on their way into the other buffer; while b is walked, the headers of b+1 come into registers and
+// the gids of b+2 are read; the headers of b+1 and the gids of b+2 go to LDS at the end, and one
+// barrier (after each wave has waited for its copies) hands the next batch over.
 template <int S, bool RGB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S > 0 ? 2 : 4))) void render_forward_kernel(
 	const RenderArgs a) {
-	constexpr int kNcb = S > 0 ? FeatTraits<S>::kNcb : 1;
-	constexpr int kStride = S > 0 ? FeatTraits<S>::kStride : 1;
+	constexpr int kNcb = S > 0 ? S / 32 : 1;
+	constexpr int kRows = S > 0 ? (kBatch + 1) * S : 1;
 
-	__shared__ float2 s_mean[kBatch];
-	__shared__ float4 s_conic[kBatch];
-	__shared__ float4 s_color[RGB ? kBatch : 1];
-	__shared__ float4 s_box[kBatch];
-	// Row kBatch stays zero: positions past the end of a partial group point at it.
-	__shared__ __attribute__((aligned(16))) uint32_t s_feat[S > 0 ? (kBatch + 1) * kStride : 1];
+	__shared__ int s_gid[2][kBatch];
+	__shared__ float2 s_mean[2][kBatch];
+	__shared__ float4 s_conic[2][kBatch];
+	__shared__ float4 s_color[2][RGB ? kBatch : 1];
+	__shared__ float4 s_box[2][kBatch];
+	// Feature rows of the batch being walked and of the next one; row kBatch stays zero (positions
+	// past the end of a partial group point at it).
+	__shared__ __attribute__((aligned(16))) float s_feat0[kRows];
+	__shared__ __attribute__((aligned(16))) float s_feat1[kRows];
 
 	const int tile = hds_xcd_tile(blockIdx.x, a.num_tiles);
 	if (tile < 0) return;
@@ -123,114 +132,142 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S > 0 ? 2 :
 	const float ry0 = (float)wy0 + 0.5f, ry1 = (float)wy0 + 7.5f;
 	const int2 range = a.ranges[tile];
 	const int num = range.y - range.x;
+	const int num_batches = (num + kBatch - 1) / kBatch;
 	const int c0 = slice * S;
+	auto batch_count = [&](int b) { return b < num_batches ? min(kBatch, num - b * kBatch) : 0; };
 
-	float T = 1.0f;
-	bool done = !inside;
-	int last = 0;
-	float cr = 0.0f, cg = 0.0f, cb_ = 0.0f;
+	Pixel st{1.0f, !inside, 0, 0.0f, 0.0f, 0.0f};
 	hds_f32x16 acc[2][kNcb];
 #pragma unroll
 	for (int m = 0; m < 2; m++)
 #pragma unroll
 		for (int c = 0; c < kNcb; c++) acc[m][c] = hds_f32x16{};
 
-	if constexpr (S > 0)
-		for (int i = tid; i < kStride; i += blockDim.x) s_feat[kBatch * kStride + i] = 0u;
-
-	for (int batch = 0; batch < num; batch += kBatch) {
-		// Also the barrier between the last batch's LDS reads and this batch's writes.
-		if (__syncthreads_count(done) == (int)blockDim.x) break;
-		const int cnt = min(kBatch, num - batch);
-		if (tid < cnt) {
-			const int gid = a.values[range.x + batch + tid];
+	if (num_batches == 0) goto write_out;
+	{
+		// Prologue: batch 0 staged synchronously, the gids of batch 1 read.
+		if constexpr (S > 0)
+			for (int i = tid; i < S; i += blockDim.x) s_feat0[kBatch * S + i] = s_feat1[kBatch * S + i] = 0.0f;
+		const int cnt0 = batch_count(0), cnt1 = batch_count(1);
+		if (tid < cnt0) {
+			const int gid = a.values[range.x + tid];
 			const float2 m = a.means2D[gid];
 			const float4 co = a.conic4[gid];
-			s_mean[tid] = m;
-			s_conic[tid] = co;
-			if constexpr (RGB) s_color[tid] = a.color_op4[gid];
-			s_box[tid] = hds_cull_box(m, co);
+			s_gid[0][tid] = gid;
+			s_mean[0][tid] = m;
+			s_conic[0][tid] = co;
+			if constexpr (RGB) s_color[0][tid] = a.color_op4[gid];
+			s_box[0][tid] = hds_cull_box(m, co);
 		}
-		if constexpr (S > 0) {
-			// Feature rows, split-packed once per tile; S / 4 consecutive threads share a row, so the
-			// gaussian id is one broadcast load.
-			constexpr int kVec = S / 4;
-			for (int i = tid; i < cnt * kVec; i += blockDim.x) {
-				const int row = i / kVec, q = i - row * kVec;
-				const int gid = a.values[range.x + batch + row];
-				const float4 f = *reinterpret_cast<const float4*>(a.features + (size_t)gid * a.channels + c0 + 4 * q);
-				*reinterpret_cast<uint4*>(&s_feat[row * kStride + 4 * q]) =
-					make_uint4(hds_split_pack(f.x), hds_split_pack(f.y), hds_split_pack(f.z), hds_split_pack(f.w));
-			}
-		}
+		if (tid < cnt1) s_gid[1][tid] = a.values[range.x + kBatch + tid];
 		__syncthreads();
-		if (hds_ballot(!done) == 0) continue;
+		if constexpr (S > 0) hds_stage_rows_async<S, false>(s_feat0, a.features, a.channels, c0, s_gid[0], cnt0, tid);
+		hds_wait_vmem();
+		__syncthreads();
+	}
 
-		uint64_t hits = hds_ballot(lane < cnt && hds_box_hits(s_box[lane < cnt ? lane : 0], rx0, rx1, ry0, ry1));
-		while (hits) {
-			// The next group: up to 16 box-hits in list order; missing positions use the zero row.
-			int slot[kGroup];
-			int count = 0;
-#pragma unroll
-			for (int q = 0; q < kGroup; q++) {
-				slot[q] = kBatch;
-				if (hits) {
-					slot[q] = __builtin_ctzll(hits);
-					hits &= hits - 1;
-					count = q + 1;
-				}
+	{
+		// One batch: prefetch b+1 / b+2, walk b, publish b+1. Returns true when every pixel is done.
+		auto step = [&](int b, int p, const float* feat, float* feat_next) -> bool {
+			const int cnt = batch_count(b), cnt1 = batch_count(b + 1), cnt2 = batch_count(b + 2);
+			if constexpr (S > 0)
+				if (cnt1 > 0) hds_stage_rows_async<S, false>(feat_next, a.features, a.channels, c0, s_gid[p ^ 1], cnt1, tid);
+			float2 m1 = make_float2(0.0f, 0.0f);
+			float4 co1 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), col1 = co1;
+			int g2 = 0;
+			if (tid < cnt1) {
+				const int gid = s_gid[p ^ 1][tid];
+				m1 = a.means2D[gid];
+				co1 = a.conic4[gid];
+				if constexpr (RGB) col1 = a.color_op4[gid];
 			}
-			float w[kGroup];
+			if (tid < cnt2) g2 = a.values[range.x + (b + 2) * kBatch + tid];
+
+			if (hds_ballot(!st.done) != 0) {
+				const int batch = b * kBatch;
+				uint64_t hits =
+					hds_ballot(lane < cnt && hds_box_hits(s_box[p][lane < cnt ? lane : 0], rx0, rx1, ry0, ry1));
+				while (hits) {
+					// The next group: up to 16 box-hits in list order; missing positions use the zero row.
+					int slot[kGroup];
+					int count = 0;
 #pragma unroll
-			for (int q0 = 0; q0 < kGroup; q0 += kIlp) {
-				float alpha[kIlp];
-#pragma unroll
-				for (int u = 0; u < kIlp; u++) {
-					const int sl = min(slot[q0 + u], kBatch - 1);
-					float G, dx, dy;
-					alpha[u] = fminf(HDS_MAX_ALPHA, hds_raw_alpha(fx, fy, s_mean[sl], s_conic[sl], G, dx, dy));
-				}
-#pragma unroll
-				for (int u = 0; u < kIlp; u++) {
-					const int q = q0 + u;
-					w[q] = 0.0f;
-					if (q < count && !done && alpha[u] >= HDS_MIN_ALPHA) {
-						const float test_T = T * (1.0f - alpha[u]);
-						if (test_T < HDS_MIN_TRANSMITTANCE) {
-							done = true;
-						} else {
-							w[q] = alpha[u] * T;
-							if constexpr (RGB) {
-								const float4 col = s_color[slot[q]];
-								cr += w[q] * col.x;
-								cg += w[q] * col.y;
-								cb_ += w[q] * col.z;
-							}
-							T = test_T;
-							last = batch + slot[q] + 1;
+					for (int q = 0; q < kGroup; q++) {
+						slot[q] = kBatch;
+						if (hits) {
+							slot[q] = __builtin_ctzll(hits);
+							hits &= hits - 1;
+							count = q + 1;
 						}
 					}
+					float w[kGroup];
+#pragma unroll
+					for (int q0 = 0; q0 < kGroup; q0 += kIlp) {
+						float alpha[kIlp];
+#pragma unroll
+						for (int u = 0; u < kIlp; u++) {
+							const int sl = min(slot[q0 + u], kBatch - 1);
+							float G, dx, dy;
+							alpha[u] = fminf(HDS_MAX_ALPHA, hds_raw_alpha(fx, fy, s_mean[p][sl], s_conic[p][sl], G, dx, dy));
+						}
+#pragma unroll
+						for (int u = 0; u < kIlp; u++) {
+							const int q = q0 + u;
+							w[q] = 0.0f;
+							if (q < count && !st.done && alpha[u] >= HDS_MIN_ALPHA) {
+								const float test_T = st.T * (1.0f - alpha[u]);
+								if (test_T < HDS_MIN_TRANSMITTANCE) {
+									st.done = true;
+								} else {
+									w[q] = alpha[u] * st.T;
+									if constexpr (RGB) {
+										const float4 col = s_color[p][slot[q]];
+										st.r += w[q] * col.x;
+										st.g += w[q] * col.y;
+										st.b += w[q] * col.z;
+									}
+									st.T = test_T;
+									st.last = batch + slot[q] + 1;
+								}
+							}
+						}
+					}
+					if constexpr (S > 0) {
+						uint32_t w_hi[8], w_lo[8];
+#pragma unroll
+						for (int i = 0; i < 8; i++) hds_split_pair(w[2 * i], w[2 * i + 1], w_hi[i], w_lo[i]);
+						flush_group<S>(acc, w_hi, w_lo, slot, feat, lane);
+					}
+					if (hds_ballot(!st.done) == 0) break;
 				}
 			}
-			if constexpr (S > 0) {
-				uint32_t w_hi[8], w_lo[8];
-#pragma unroll
-				for (int i = 0; i < 8; i++) hds_split_pair(w[2 * i], w[2 * i + 1], w_hi[i], w_lo[i]);
-				flush_group<S>(acc, w_hi, w_lo, slot, s_feat, lane);
+
+			if (tid < cnt1) {
+				s_mean[p ^ 1][tid] = m1;
+				s_conic[p ^ 1][tid] = co1;
+				if constexpr (RGB) s_color[p ^ 1][tid] = col1;
+				s_box[p ^ 1][tid] = hds_cull_box(m1, co1);
 			}
-			if (hds_ballot(!done) == 0) break;
+			if (tid < cnt2) s_gid[p][tid] = g2;
+			hds_wait_vmem();
+			return __syncthreads_count(st.done) == (int)blockDim.x;
+		};
+		for (int b = 0; b < num_batches; b += 2) {
+			if (step(b, 0, s_feat0, s_feat1) || b + 1 >= num_batches) break;
+			if (step(b + 1, 1, s_feat1, s_feat0)) break;
 		}
 	}
 
+write_out:
 	if (inside && slice == 0) {
 		const int64_t pix = (int64_t)py * a.width + px;
 		if constexpr (RGB) {
-			a.image[pix * 3 + 0] = cr + T * a.background[0];
-			a.image[pix * 3 + 1] = cg + T * a.background[1];
-			a.image[pix * 3 + 2] = cb_ + T * a.background[2];
+			a.image[pix * 3 + 0] = st.r + st.T * a.background[0];
+			a.image[pix * 3 + 1] = st.g + st.T * a.background[1];
+			a.image[pix * 3 + 2] = st.b + st.T * a.background[2];
 		}
-		a.final_T[pix] = T;
-		a.n_contrib[pix] = last;
+		a.final_T[pix] = st.T;
+		a.n_contrib[pix] = st.last;
 	}
 	if constexpr (S > 0) {
 		// D of a 32x32 tile: lane holds pixel 32m + lane % 32 and, for each group g of four

@@ -1,0 +1,61 @@
+/*
+ * Asynchronous staging of a tile's gaussian batches for the blend kernels.
+ *
+ * The walks read each batch of 64 gaussians of a tile list from LDS. Staging the next batch while
+ * the current one is processed hides the gather latency (feature rows are 64 scattered 128-512 byte
+ * rows per batch): the feature rows go straight from HBM to LDS with gfx950's
+ * global_load_lds_dwordx4 (no registers, no wait until the batch is needed), into one of two
+ * buffers that are separate __shared__ arrays so the compiler's wait insertion can tell the buffer
+ * being filled from the one being read. Rows are stored as raw fp32, S floats per row, and split
+ * into bf16 hi/lo MFMA operands when they are read.
+ */
+#ifndef HDS_STAGE_H
+#define HDS_STAGE_H
+
+#include "hds_internal.h"
+
+typedef __attribute__((address_space(3))) void hds_lds_void;
+
+/* Waits for this wave's outstanding vector-memory operations, including LDS DMA. Before a barrier it
+ * makes every wave's staged rows visible to the whole work-group. */
+__device__ static inline void hds_wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+/* Physical 16-byte chunk of logical chunk c in staged row r. With kSwizzle the chunks of a row are
+ * XOR-permuted by the row's low three bits, so 8 lanes reading the same logical chunk of 8
+ * consecutive rows with ds_read_b128 hit 8 different bank groups. */
+template <bool kSwizzle>
+__device__ static inline int hds_stage_chunk(int c, int r) {
+	return kSwizzle ? (c ^ (r & 7)) : c;
+}
+
+/* Issues the copy of rows 0..cnt-1 (S channels from c0 of features[gids[row]]) into buf, one
+ * 1 KB block of rows per wave instruction; cnt <= 64, the work-group has 256 threads. The caller
+ * waits with hds_wait_vmem() and a barrier before reading. */
+template <int S, bool kSwizzle>
+__device__ inline void hds_stage_rows_async(float* buf, const float* __restrict__ features, int channels, int c0,
+											const int* gids, int cnt, int tid) {
+	constexpr int kChunks = S / 4;              // 16-byte chunks per row
+	constexpr int kRowsPerOp = 64 / kChunks;    // rows per 1 KB wave instruction
+	constexpr int kOps = 64 / kRowsPerOp;       // instructions per 64-row batch
+	const int lane = tid & 63, wave = tid >> 6;
+	const int chunk = lane % kChunks;
+#pragma unroll
+	for (int op = wave; op < kOps; op += 4) {
+		const int row = op * kRowsPerOp + lane / kChunks;
+		if (row < cnt) {
+			const float* src = features + (size_t)gids[row] * channels + c0 + 4 * hds_stage_chunk<kSwizzle>(chunk, row);
+			__builtin_amdgcn_global_load_lds(src, (hds_lds_void*)(buf + op * 256), 16, 0, 0);
+		}
+	}
+}
+
+/* Eight fp32 values -> the split-bf16 hi and lo operands of one MFMA. */
+__device__ static inline void hds_split8(const float (&v)[8], hds_bf16x8& hi, hds_bf16x8& lo) {
+	uint32_t h[4], l[4];
+#pragma unroll
+	for (int i = 0; i < 4; i++) hds_split_pair(v[2 * i], v[2 * i + 1], h[i], l[i]);
+	hi = __builtin_bit_cast(hds_bf16x8, hds_u32x4{h[0], h[1], h[2], h[3]});
+	lo = __builtin_bit_cast(hds_bf16x8, hds_u32x4{l[0], l[1], l[2], l[3]});
+}
+
+#endif /* HDS_STAGE_H */
