@@ -74,8 +74,15 @@ __device__ static inline int hds_rank_below(uint64_t mask) {
 
 __device__ static inline uint64_t hds_ballot(bool pred) { return (uint64_t)__ballot(pred); }
 
-/* Keeps the compiler from moving LDS accesses of one wave across this point. */
-__device__ static inline void hds_wave_fence() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront"); __builtin_amdgcn_wave_barrier(); __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront"); }
+/* Keeps the compiler from moving the LDS accesses of one wave across this point. A wave's LDS
+ * instructions execute in order, so lanes then see each other's earlier LDS writes. It is not a
+ * memory fence: a fence would also wait for the wave's outstanding global loads, including the
+ * asynchronous LDS DMA of the next batch. */
+__device__ static inline void hds_wave_fence() {
+	asm volatile("" ::: "memory");
+	__builtin_amdgcn_wave_barrier();
+	asm volatile("" ::: "memory");
+}
 
 __device__ static inline float hds_shfl_xor(float v, int mask) { return __shfl_xor(v, mask, HDS_WAVE); }
 

@@ -28,6 +28,7 @@
 // gaussian's gradient row sees one atomic per 8x8 block it touches.
 #include "hds_internal.h"
 #include "hds_rasterizer.h"
+#include "hds_stage.h"
 
 namespace {
 
@@ -76,19 +77,24 @@ __device__ inline int tile_max_last(int last, int* s_max_last) {
 template <int S, bool RGB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void backward_geometry_kernel(const BackwardArgs a) {
 	constexpr int kKc = S > 0 ? S / 32 : 1;       // K steps of the dot over channels
-	constexpr int kStride = S > 0 ? S + 4 : 1;    // words per staged feature row
+	// Gaussians per batch: 32 at S = 128 so that two work-groups fit a CU's LDS; positions whose
+	// alphas are evaluated together: 2 at S = 128, where dL/dF takes half the registers.
+	constexpr int kGB = S >= 128 ? 32 : kBatch;
+	constexpr int kGeoIlp = S >= 128 ? 2 : kIlp;
+	constexpr int kRows = S > 0 ? (kGB + 1) * S : 1;
 
-	__shared__ int s_gid[kBatch];
-	__shared__ float2 s_mean[kBatch];
-	__shared__ float4 s_conic[kBatch];
-	__shared__ float4 s_color[RGB ? kBatch : 1];
-	__shared__ float4 s_box[kBatch];
-	// Row kBatch stays zero: positions past the end of a partial group point at it.
-	__shared__ __attribute__((aligned(16))) uint32_t s_feat[S > 0 ? (kBatch + 1) * kStride : 1];
-	// Per wave: s and w of the group as rows per position (the B operands of the moment MFMAs).
-	__shared__ __attribute__((aligned(16))) uint32_t s_tr[4][2][kGeoGroup * kRowStride];
+	// Gaussian ids of batches b, b+1, b+2 (slot b % 3); records and feature rows of the batch being
+	// walked and of the next one (the pipeline of render_forward_kernel). Feature rows are raw fp32
+	// with their 16-byte chunks XOR-swizzled by row; row kGB stays zero (positions past the end of a
+	// partial group point at it).
+	__shared__ int s_gid[3][kGB];
+	__shared__ HdsHeaderSlot<kGB, RGB> s_hdr0, s_hdr1;
+	__shared__ __attribute__((aligned(16))) float s_feat0[kRows];
+	__shared__ __attribute__((aligned(16))) float s_feat1[kRows];
 	__shared__ int s_slot[4][kGeoGroup];
 	__shared__ int s_max_last;
+	// Per wave: s and w of the group as rows per position (the B operands of the moment MFMAs).
+	__shared__ __attribute__((aligned(16))) uint32_t s_tr[4][2][kGeoGroup * kRowStride];
 
 	const int tile = hds_xcd_tile(blockIdx.x, a.num_tiles);
 	if (tile < 0) return;
@@ -125,27 +131,35 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void b
 	hds_bf16x8 pt_hi[2], pt_lo[2];
 	{
 		const int row = lane & 15;
+		// The 16 dL/dRGB values this lane contributes, loaded together (index 0 where unused).
+		float g[2][8];
+#pragma unroll
+		for (int kk = 0; kk < 2; kk++)
+#pragma unroll
+			for (int j = 0; j < 8; j++) g[kk][j] = 0.0f;
+		if (do_rgb) {
+#pragma unroll
+			for (int kk = 0; kk < 2; kk++)
+#pragma unroll
+				for (int j = 0; j < 8; j++) {
+					const int p = 32 * kk + 8 * (lane >> 4) + j;
+					const int x = wx0 + (p & 7), y = wy0 + (p >> 3);
+					const bool use = row >= 8 && row < 11 && x < a.width && y < a.height;
+					const float v = a.grad_image[use ? ((int64_t)y * a.width + x) * 3 + (row - 8) : 0];
+					g[kk][j] = use ? v : 0.0f;
+				}
+		}
 #pragma unroll
 		for (int kk = 0; kk < 2; kk++) {
-			uint32_t d[8];
+			float v[8];
 #pragma unroll
 			for (int j = 0; j < 8; j++) {
 				const int p = 32 * kk + 8 * (lane >> 4) + j;
 				const float xl = (float)(p & 7) - 3.5f, yl = (float)(p >> 3) - 3.5f;
-				float v = 0.0f;
-				if (row == 0) v = 1.0f;
-				else if (row == 1) v = xl;
-				else if (row == 2) v = yl;
-				else if (row == 3) v = xl * xl;
-				else if (row == 4) v = xl * yl;
-				else if (row == 5) v = yl * yl;
-				else if (row >= 8 && row < 11 && do_rgb) {
-					const int x = wx0 + (p & 7), y = wy0 + (p >> 3);
-					if (x < a.width && y < a.height) v = a.grad_image[((int64_t)y * a.width + x) * 3 + (row - 8)];
-				}
-				d[j] = hds_split_pack(v);
+				v[j] = row == 0 ? 1.0f : row == 1 ? xl : row == 2 ? yl : row == 3 ? xl * xl : row == 4 ? xl * yl
+					 : row == 5 ? yl * yl : g[kk][j];
 			}
-			hds_unpack8(d, pt_hi[kk], pt_lo[kk]);
+			hds_split8(v, pt_hi[kk], pt_lo[kk]);
 		}
 	}
 
@@ -175,7 +189,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void b
 				gb_lo[n][kk] = __builtin_bit_cast(hds_bf16x8, hds_u32x4{l[0], l[1], l[2], l[3]});
 			}
 		}
-		for (int i = tid; i < kStride; i += blockDim.x) s_feat[kBatch * kStride + i] = 0u;
+		for (int i = tid; i < S; i += blockDim.x) s_feat0[kGB * S + i] = s_feat1[kGB * S + i] = 0.0f;
 	}
 
 	const int2 range = a.ranges[tile];
@@ -185,217 +199,237 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void b
 	uint32_t* tr_w = s_tr[wave][1];
 	int* slots = s_slot[wave];
 
-	for (int batch_end = num; batch_end > 0; batch_end -= kBatch) {
-		const int cnt = min(kBatch, batch_end);
-		const int batch_start = batch_end - cnt;
+	// Batches run back to front: batch b holds list entries [start(b), start(b) + count(b)).
+	const int num_batches = (num + kGB - 1) / kGB;
+	auto batch_count = [&](int b) { return b < num_batches ? min(kGB, num - b * kGB) : 0; };
+	auto batch_start_of = [&](int b) { return num - b * kGB - batch_count(b); };
+	if (num_batches == 0) return;
+	{
+		// Prologue: gids of batches 0 and 1, then batch 0 staged synchronously.
+		const int cnt0 = batch_count(0), cnt1 = batch_count(1);
+		if (tid < cnt0) s_gid[0][tid] = a.values[range.x + batch_start_of(0) + tid];
+		if (tid < cnt1) s_gid[1][tid] = a.values[range.x + batch_start_of(1) + tid];
 		__syncthreads();
-		if (tid < cnt) {
-			const int gid = a.values[range.x + batch_start + tid];
-			const float2 m = a.means2D[gid];
-			const float4 co = a.conic4[gid];
-			s_gid[tid] = gid;
-			s_mean[tid] = m;
-			s_conic[tid] = co;
-			if constexpr (RGB) s_color[tid] = a.color_op4[gid];
-			s_box[tid] = hds_cull_box(m, co);
-		}
-		if constexpr (S > 0) {
-			// Feature rows of the batch, each read once for the whole tile; thread groups of S / 4 share
-			// a row, so the gaussian id is one broadcast load.
-			constexpr int kVec = S / 4;
-			for (int i = tid; i < cnt * kVec; i += blockDim.x) {
-				const int row = i / kVec, q = i - row * kVec;
-				const int gid = a.values[range.x + batch_start + row];
-				const float4 f = *reinterpret_cast<const float4*>(a.features + (size_t)gid * a.channels + c0 + 4 * q);
-				*reinterpret_cast<uint4*>(&s_feat[row * kStride + 4 * q]) =
-					make_uint4(hds_split_pack(f.x), hds_split_pack(f.y), hds_split_pack(f.z), hds_split_pack(f.w));
-			}
-		}
+		hds_stage_headers_async<kGB, RGB>(s_hdr0, a.means2D, a.conic4, a.color_op4, s_gid[0], cnt0, tid);
+		if constexpr (S > 0) hds_stage_rows_async<S, true, kGB>(s_feat0, a.features, a.channels, c0, s_gid[0], cnt0, tid);
+		hds_wait_vmem();
 		__syncthreads();
-		if (batch_start >= wave_last) continue;
+	}
 
-		uint64_t hits = hds_ballot(lane < cnt && batch_start + lane < wave_last &&
-								   hds_box_hits(s_box[lane < cnt ? lane : 0], rx0, rx1, ry0, ry1));
-		while (hits) {
-			// Next group: the (up to) 16 deepest hits. Hit bit b is position (number of hits above b).
-			const int count = min(kGeoGroup, __builtin_popcountll(hits));
-			{
-				const bool set = (hits >> lane) & 1ull;
-				const int rank = __builtin_popcountll((hits >> lane) >> 1);
-				const bool take = set && rank < kGeoGroup;
-				if (take) slots[rank] = lane;
-				if (lane >= count && lane < kGeoGroup) slots[lane] = kBatch;
-				hits &= ~hds_ballot(take);
-			}
-			hds_wave_fence();
+	// One batch: stage b+1, read the gids of b+2, walk b.
+	auto step = [&](int b, const HdsHeaderSlot<kGB, RGB>& h, const float* feat, HdsHeaderSlot<kGB, RGB>& h_next,
+					float* feat_next) {
+		const int cnt = batch_count(b), cnt1 = batch_count(b + 1), cnt2 = batch_count(b + 2);
+		const int batch_start = batch_start_of(b);
+		const int* gids = s_gid[b % 3];
+		int g2 = 0;
+		if (tid < cnt2) g2 = a.values[range.x + batch_start_of(b + 2) + tid];
+		const int* gid_next = s_gid[(b + 1) % 3];
+		if (cnt1 > 0) {
+			hds_stage_headers_async<kGB, RGB>(h_next, a.means2D, a.conic4, a.color_op4, gid_next, cnt1, tid);
+			if constexpr (S > 0)
+				hds_stage_rows_async<S, true, kGB>(feat_next, a.features, a.channels, c0, gid_next, cnt1, tid);
+		}
 
-			// dot[position 4h + i][own pixel] = dot[h][i] (zero without features).
-			float dot[4][4];
-#pragma unroll
-			for (int h = 0; h < 4; h++)
-#pragma unroll
-				for (int i = 0; i < 4; i++) dot[h][i] = 0.0f;
-			if constexpr (S > 0) {
-				// A = F: row lane % 16 = position, k = channels 32kk + 8(lane / 16) + 0..7.
-				const uint32_t* frow = s_feat + slots[lane & 15] * kStride + 8 * (lane >> 4);
-				hds_f32x4 X[4];
-#pragma unroll
-				for (int n = 0; n < 4; n++) X[n] = hds_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-				for (int kk = 0; kk < kKc; kk++) {
-					const uint4 d0 = *reinterpret_cast<const uint4*>(frow + 32 * kk);
-					const uint4 d1 = *reinterpret_cast<const uint4*>(frow + 32 * kk + 4);
-					const uint32_t d[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
-					hds_bf16x8 f_hi, f_lo;
-					hds_unpack8(d, f_hi, f_lo);
-#pragma unroll
-					for (int n = 0; n < 4; n++) X[n] = hds_mfma_split(f_hi, f_lo, gb_hi[n][kk], gb_lo[n][kk], X[n]);
-				}
-				// X[n] of lane group h holds positions 4h + 0..3 of pixel 16n + lane % 16: transpose the
-				// 4x4 (group, block) arrangement, first across halves, then across neighbouring rows.
-				uint32_t t[4][4];
-#pragma unroll
-				for (int n = 0; n < 4; n++)
-#pragma unroll
-					for (int i = 0; i < 4; i++) t[n][i] = hds_swap_operand(X[n][i]);
-#pragma unroll
-				for (int i = 0; i < 4; i++) {
-#pragma unroll
-					for (int n = 0; n < 2; n++) {
-						const auto r = __builtin_amdgcn_permlane32_swap(t[n][i], t[n + 2][i], false, false);
-						t[n][i] = r[0];
-						t[n + 2][i] = r[1];
-					}
-#pragma unroll
-					for (int n = 0; n < 4; n += 2) {
-						const auto r = __builtin_amdgcn_permlane16_swap(t[n][i], t[n + 1][i], false, false);
-						t[n][i] = r[0];
-						t[n + 1][i] = r[1];
-					}
-				}
-#pragma unroll
-				for (int h = 0; h < 4; h++)
-#pragma unroll
-					for (int i = 0; i < 4; i++) dot[h][i] = __builtin_bit_cast(float, t[h][i]);
+		if (batch_start < wave_last) {
+			bool box_hit = false;
+			if (lane < cnt && batch_start + lane < wave_last) {
+				const float4 box = hds_cull_box(make_float2(h.mx[lane], h.my[lane]), h.conic[lane]);
+				box_hit = hds_box_hits(box, rx0, rx1, ry0, ry1);
 			}
-
-			// Back-to-front replay of the group, kIlp positions at a time: their alphas are
-			// independent, only T and the behind-sums chain through them.
-			uint32_t active = 0;
-#pragma unroll
-			for (int q0 = 0; q0 < kGeoGroup; q0 += kIlp) {
-				// Unrolled with no early exit, so every dot[][] index stays static.
-				if (q0 < count) {
-					int slot[kIlp];
-					float raw[kIlp], G[kIlp];
-	#pragma unroll
-					for (int u = 0; u < kIlp; u++) {
-						slot[u] = slots[q0 + u];
-						const int sl = min(slot[u], kBatch - 1);
-						float dx, dy;
-						raw[u] = hds_raw_alpha(fx, fy, s_mean[sl], s_conic[sl], G[u], dx, dy);
-					}
-	#pragma unroll
-					for (int u = 0; u < kIlp; u++) {
-						const int q = q0 + u;
-						const float alpha = fminf(HDS_MAX_ALPHA, raw[u]);
-						const bool contributes = q < count && batch_start + slot[u] < last && alpha >= HDS_MIN_ALPHA;
-						float dL_dalpha = 0.0f, w = 0.0f;
-						if (contributes) {
-							const float inv_1ma = __builtin_amdgcn_rcpf(1.0f - alpha);
-							T *= inv_1ma;
-							w = alpha * T;
-							if (do_rgb) {
-								const float4 col = s_color[slot[u]];
-								rec_r = last_alpha * last_r + (1.0f - last_alpha) * rec_r;
-								rec_g = last_alpha * last_g + (1.0f - last_alpha) * rec_g;
-								rec_b = last_alpha * last_b + (1.0f - last_alpha) * rec_b;
-								last_r = col.x;
-								last_g = col.y;
-								last_b = col.z;
-								last_alpha = alpha;
-								dL_dalpha = ((col.x - rec_r) * gr + (col.y - rec_g) * gg + (col.z - rec_b) * gb) * T -
-											T_final * inv_1ma * dL_dTf;
-							}
-							if constexpr (S > 0) {
-								dL_dalpha += T * (dot[q >> 2][q & 3] - behind_dot);
-								behind_dot = alpha * dot[q >> 2][q & 3] + (1.0f - alpha) * behind_dot;
-							}
-						}
-						// A clamped alpha no longer depends on the gaussian (backward.cu:126-135).
-						const float sg = (contributes && raw[u] <= HDS_MAX_ALPHA) ? G[u] * dL_dalpha : 0.0f;
-						tr_s[q * kRowStride + lane] = hds_split_pack(sg);
-						if (do_rgb) tr_w[q * kRowStride + lane] = hds_split_pack(w);
-						if (hds_ballot(contributes)) active |= 1u << q;
-					}
-				}
-			}
-			if (!active) continue;
-#pragma unroll
-			for (int q = 0; q < kGeoGroup; q++) {
-				if (q >= count) {
-					tr_s[q * kRowStride + lane] = 0u;
-					if (do_rgb) tr_w[q * kRowStride + lane] = 0u;
-				}
-			}
-			hds_wave_fence();
-
-			// mom[j][position] = sum_px P^T[j][px] s[px][position]; B lane = (pixels 32kk + 8(lane / 16)
-			// + 0..7, position lane % 16). D: row 4(lane / 16) + i = j, column lane % 16 = position.
-			hds_f32x4 ms = {0.0f, 0.0f, 0.0f, 0.0f}, mw = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-			for (int kk = 0; kk < 2; kk++) {
-				const int off = (lane & 15) * kRowStride + 32 * kk + 8 * (lane >> 4);
+			uint64_t hits = hds_ballot(box_hit);
+			while (hits) {
+				// Next group: the (up to) 16 deepest hits. Hit bit b is position (number of hits above b).
+				const int count = min(kGeoGroup, __builtin_popcountll(hits));
 				{
-					const uint4 d0 = *reinterpret_cast<const uint4*>(tr_s + off);
-					const uint4 d1 = *reinterpret_cast<const uint4*>(tr_s + off + 4);
-					const uint32_t d[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
-					hds_bf16x8 b_hi, b_lo;
-					hds_unpack8(d, b_hi, b_lo);
-					ms = hds_mfma_split(pt_hi[kk], pt_lo[kk], b_hi, b_lo, ms);
+					const bool set = (hits >> lane) & 1ull;
+					const int rank = __builtin_popcountll((hits >> lane) >> 1);
+					const bool take = set && rank < kGeoGroup;
+					if (take) slots[rank] = lane;
+					if (lane >= count && lane < kGeoGroup) slots[lane] = kGB;
+					hits &= ~hds_ballot(take);
 				}
-				if (do_rgb) {
-					const uint4 d0 = *reinterpret_cast<const uint4*>(tr_w + off);
-					const uint4 d1 = *reinterpret_cast<const uint4*>(tr_w + off + 4);
-					const uint32_t d[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
-					hds_bf16x8 b_hi, b_lo;
-					hds_unpack8(d, b_hi, b_lo);
-					mw = hds_mfma_split(pt_hi[kk], pt_lo[kk], b_hi, b_lo, mw);
+				hds_wave_fence();
+
+				// dot[position 4h + i][own pixel] = dot[h][i] (zero without features).
+				float dot[4][4];
+	#pragma unroll
+				for (int h = 0; h < 4; h++)
+	#pragma unroll
+					for (int i = 0; i < 4; i++) dot[h][i] = 0.0f;
+				if constexpr (S > 0) {
+					// A = F: row lane % 16 = position, k = channels 32kk + 8(lane / 16) + 0..7.
+					const int frow_idx = slots[lane & 15];
+					const float* frow = feat + frow_idx * S;
+					hds_f32x4 X[4];
+	#pragma unroll
+					for (int n = 0; n < 4; n++) X[n] = hds_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+	#pragma unroll
+					for (int kk = 0; kk < kKc; kk++) {
+						// Logical chunks 8kk + 2(lane / 16) and the next one of the (swizzled) row.
+						const int lc = 8 * kk + 2 * (lane >> 4);
+						const float4 f0 = *reinterpret_cast<const float4*>(frow + 4 * hds_stage_chunk<true>(lc, frow_idx));
+						const float4 f1 = *reinterpret_cast<const float4*>(frow + 4 * hds_stage_chunk<true>(lc + 1, frow_idx));
+						const float v[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
+						hds_bf16x8 f_hi, f_lo;
+						hds_split8(v, f_hi, f_lo);
+	#pragma unroll
+						for (int n = 0; n < 4; n++) X[n] = hds_mfma_split(f_hi, f_lo, gb_hi[n][kk], gb_lo[n][kk], X[n]);
+					}
+					// X[n] of lane group h holds positions 4h + 0..3 of pixel 16n + lane % 16: transpose the
+					// 4x4 (group, block) arrangement, first across halves, then across neighbouring rows.
+					uint32_t t[4][4];
+	#pragma unroll
+					for (int n = 0; n < 4; n++)
+	#pragma unroll
+						for (int i = 0; i < 4; i++) t[n][i] = hds_swap_operand(X[n][i]);
+	#pragma unroll
+					for (int i = 0; i < 4; i++) {
+	#pragma unroll
+						for (int n = 0; n < 2; n++) {
+							const auto r = __builtin_amdgcn_permlane32_swap(t[n][i], t[n + 2][i], false, false);
+							t[n][i] = r[0];
+							t[n + 2][i] = r[1];
+						}
+	#pragma unroll
+						for (int n = 0; n < 4; n += 2) {
+							const auto r = __builtin_amdgcn_permlane16_swap(t[n][i], t[n + 1][i], false, false);
+							t[n][i] = r[0];
+							t[n + 1][i] = r[1];
+						}
+					}
+	#pragma unroll
+					for (int h = 0; h < 4; h++)
+	#pragma unroll
+						for (int i = 0; i < 4; i++) dot[h][i] = __builtin_bit_cast(float, t[h][i]);
 				}
+
+				// Back-to-front replay of the group, kIlp positions at a time: their alphas are
+				// independent, only T and the behind-sums chain through them.
+				uint32_t active = 0;
+	#pragma unroll
+				for (int q0 = 0; q0 < kGeoGroup; q0 += kGeoIlp) {
+					// Unrolled with no early exit, so every dot[][] index stays static.
+					if (q0 < count) {
+						int slot[kGeoIlp];
+						float raw[kGeoIlp], G[kGeoIlp];
+		#pragma unroll
+						for (int u = 0; u < kGeoIlp; u++) {
+							slot[u] = slots[q0 + u];
+							const int sl = min(slot[u], kGB - 1);
+							float dx, dy;
+							raw[u] = hds_raw_alpha(fx, fy, make_float2(h.mx[sl], h.my[sl]), h.conic[sl], G[u], dx, dy);
+						}
+		#pragma unroll
+						for (int u = 0; u < kGeoIlp; u++) {
+							const int q = q0 + u;
+							const float alpha = fminf(HDS_MAX_ALPHA, raw[u]);
+							const bool contributes = q < count && batch_start + slot[u] < last && alpha >= HDS_MIN_ALPHA;
+							float dL_dalpha = 0.0f, w = 0.0f;
+							if (contributes) {
+								const float inv_1ma = __builtin_amdgcn_rcpf(1.0f - alpha);
+								T *= inv_1ma;
+								w = alpha * T;
+								if (do_rgb) {
+									const float4 col = h.color[slot[u]];
+									rec_r = last_alpha * last_r + (1.0f - last_alpha) * rec_r;
+									rec_g = last_alpha * last_g + (1.0f - last_alpha) * rec_g;
+									rec_b = last_alpha * last_b + (1.0f - last_alpha) * rec_b;
+									last_r = col.x;
+									last_g = col.y;
+									last_b = col.z;
+									last_alpha = alpha;
+									dL_dalpha = ((col.x - rec_r) * gr + (col.y - rec_g) * gg + (col.z - rec_b) * gb) * T -
+												T_final * inv_1ma * dL_dTf;
+								}
+								if constexpr (S > 0) {
+									dL_dalpha += T * (dot[q >> 2][q & 3] - behind_dot);
+									behind_dot = alpha * dot[q >> 2][q & 3] + (1.0f - alpha) * behind_dot;
+								}
+							}
+							// A clamped alpha no longer depends on the gaussian (backward.cu:126-135).
+							const float sg = (contributes && raw[u] <= HDS_MAX_ALPHA) ? G[u] * dL_dalpha : 0.0f;
+							tr_s[q * kRowStride + lane] = hds_split_pack(sg);
+							if (do_rgb) tr_w[q * kRowStride + lane] = hds_split_pack(w);
+							if (hds_ballot(contributes)) active |= 1u << q;
+						}
+					}
+				}
+				if (!active) continue;
+	#pragma unroll
+				for (int q = 0; q < kGeoGroup; q++) {
+					if (q >= count) {
+						tr_s[q * kRowStride + lane] = 0u;
+						if (do_rgb) tr_w[q * kRowStride + lane] = 0u;
+					}
+				}
+				hds_wave_fence();
+
+				// mom[j][position] = sum_px P^T[j][px] s[px][position]; B lane = (pixels 32kk + 8(lane / 16)
+				// + 0..7, position lane % 16). D: row 4(lane / 16) + i = j, column lane % 16 = position.
+				hds_f32x4 ms = {0.0f, 0.0f, 0.0f, 0.0f}, mw = {0.0f, 0.0f, 0.0f, 0.0f};
+	#pragma unroll
+				for (int kk = 0; kk < 2; kk++) {
+					const int off = (lane & 15) * kRowStride + 32 * kk + 8 * (lane >> 4);
+					{
+						const hds_u32x4 d0 = hds_lds_read128(tr_s + off);
+						const hds_u32x4 d1 = hds_lds_read128(tr_s + off + 4);
+						const uint32_t d[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+						hds_bf16x8 b_hi, b_lo;
+						hds_unpack8(d, b_hi, b_lo);
+						ms = hds_mfma_split(pt_hi[kk], pt_lo[kk], b_hi, b_lo, ms);
+					}
+					if (do_rgb) {
+						const hds_u32x4 d0 = hds_lds_read128(tr_w + off);
+						const hds_u32x4 d1 = hds_lds_read128(tr_w + off + 4);
+						const uint32_t d[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+						hds_bf16x8 b_hi, b_lo;
+						hds_unpack8(d, b_hi, b_lo);
+						mw = hds_mfma_split(pt_hi[kk], pt_lo[kk], b_hi, b_lo, mw);
+					}
+				}
+				// Rows 4, 5 (xy, y^2) live in lane group 1; bring them to group 0 beside rows 0-3.
+				const float m11 = hds_swap16_from_odd(ms[0]);
+				const float m02 = hds_swap16_from_odd(ms[1]);
+				const int q = lane & 15;
+				const bool mine = q < count && ((active >> q) & 1u);
+				if (lane < 16 && mine) {
+					// Moments about the block centre -> gradients (backward.cu:136-160, in moment form).
+					const int sl = slots[q];
+					const int gid = gids[sl];
+					const float2 mn = make_float2(h.mx[sl], h.my[sl]);
+					const float4 co = h.conic[sl];
+					const float m00 = ms[0], m10 = ms[1], m01 = ms[2], m20 = ms[3];
+					const float mx = mn.x - centre_x, my = mn.y - centre_y;
+					const float sx = m10 - mx * m00, sy = m01 - my * m00;
+					const float sxx = m20 - 2.0f * mx * m10 + mx * mx * m00;
+					const float sxy = m11 - mx * m01 - my * m10 + mx * my * m00;
+					const float syy = m02 - 2.0f * my * m01 + my * my * m00;
+					atomicAdd(&a.grad_opacities[gid], m00);
+					atomicAdd(&a.grad_means2D[gid * 2 + 0], co.w * (co.x * sx + co.y * sy));
+					atomicAdd(&a.grad_means2D[gid * 2 + 1], co.w * (co.y * sx + co.z * sy));
+					atomicAdd(&a.grad_conics[gid * 3 + 0], -0.5f * co.w * sxx);
+					atomicAdd(&a.grad_conics[gid * 3 + 1], -co.w * sxy);
+					atomicAdd(&a.grad_conics[gid * 3 + 2], -0.5f * co.w * syy);
+				}
+				if (do_rgb && lane >= 32 && lane < 48 && mine) {
+					// Rows 8-10: the colour gradients sum_px w dL/dRGB (backward.cu:112-118).
+					const int gid = gids[slots[q]];
+					atomicAdd(&a.grad_colors[gid * 3 + 0], mw[0]);
+					atomicAdd(&a.grad_colors[gid * 3 + 1], mw[1]);
+					atomicAdd(&a.grad_colors[gid * 3 + 2], mw[2]);
+				}
+				hds_wave_fence();
 			}
-			// Rows 4, 5 (xy, y^2) live in lane group 1; bring them to group 0 beside rows 0-3.
-			const float m11 = hds_swap16_from_odd(ms[0]);
-			const float m02 = hds_swap16_from_odd(ms[1]);
-			const int q = lane & 15;
-			const bool mine = q < count && ((active >> q) & 1u);
-			if (lane < 16 && mine) {
-				// Moments about the block centre -> gradients (backward.cu:136-160, in moment form).
-				const int sl = slots[q];
-				const int gid = s_gid[sl];
-				const float2 mn = s_mean[sl];
-				const float4 co = s_conic[sl];
-				const float m00 = ms[0], m10 = ms[1], m01 = ms[2], m20 = ms[3];
-				const float mx = mn.x - centre_x, my = mn.y - centre_y;
-				const float sx = m10 - mx * m00, sy = m01 - my * m00;
-				const float sxx = m20 - 2.0f * mx * m10 + mx * mx * m00;
-				const float sxy = m11 - mx * m01 - my * m10 + mx * my * m00;
-				const float syy = m02 - 2.0f * my * m01 + my * my * m00;
-				atomicAdd(&a.grad_opacities[gid], m00);
-				atomicAdd(&a.grad_means2D[gid * 2 + 0], co.w * (co.x * sx + co.y * sy));
-				atomicAdd(&a.grad_means2D[gid * 2 + 1], co.w * (co.y * sx + co.z * sy));
-				atomicAdd(&a.grad_conics[gid * 3 + 0], -0.5f * co.w * sxx);
-				atomicAdd(&a.grad_conics[gid * 3 + 1], -co.w * sxy);
-				atomicAdd(&a.grad_conics[gid * 3 + 2], -0.5f * co.w * syy);
-			}
-			if (do_rgb && lane >= 32 && lane < 48 && mine) {
-				// Rows 8-10: the colour gradients sum_px w dL/dRGB (backward.cu:112-118).
-				const int gid = s_gid[slots[q]];
-				atomicAdd(&a.grad_colors[gid * 3 + 0], mw[0]);
-				atomicAdd(&a.grad_colors[gid * 3 + 1], mw[1]);
-				atomicAdd(&a.grad_colors[gid * 3 + 2], mw[2]);
-			}
-			hds_wave_fence();
 		}
+
+		if (tid < cnt2) s_gid[(b + 2) % 3][tid] = g2;
+		hds_wait_vmem();
+		__syncthreads();
+	};
+	for (int b = 0; b < num_batches; b += 2) {
+		step(b, s_hdr0, s_feat0, s_hdr1, s_feat1);
+		if (b + 1 < num_batches) step(b + 1, s_hdr1, s_feat1, s_hdr0, s_feat0);
 	}
 }
 
@@ -412,8 +446,8 @@ __device__ inline void flush_features(const hds_bf16x8 (&gb_hi)[4][S / 32], cons
 #pragma unroll
 	for (int kp = 0; kp < 4; kp++) {
 		const uint32_t* r = rows + (lane & 31) * kRowStride + 16 * kp + 8 * (lane >> 5);
-		const uint4 d0 = *reinterpret_cast<const uint4*>(r);
-		const uint4 d1 = *reinterpret_cast<const uint4*>(r + 4);
+		const hds_u32x4 d0 = hds_lds_read128(r);
+		const hds_u32x4 d1 = hds_lds_read128(r + 4);
 		const uint32_t d[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
 		hds_unpack8(d, a_hi[kp], a_lo[kp]);
 	}

@@ -99,23 +99,20 @@ struct Pixel {
 
 // Occupancy: S accumulators per lane plus the walk's registers, two waves per SIMD with features.
 //
-// Pipeline per batch b (parity p): gids of b+1 are in s_gid[p^1] and its feature rows are already
-// on their way into the other buffer; while b is walked, the headers of b+1 come into registers and
-// the gids of b+2 are read; the headers of b+1 and the gids of b+2 go to LDS at the end, and one
-// barrier (after each wave has waited for its copies) hands the next batch over.
+// Pipeline per batch b: the records and feature rows of batch b+1 are copied into the other slot by
+// LDS DMA while b is walked, and the gids of b+2 are read; one barrier, after each wave has waited
+// for its copies, hands the next batch over.
 template <int S, bool RGB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S > 0 ? 2 : 4))) void render_forward_kernel(
 	const RenderArgs a) {
 	constexpr int kNcb = S > 0 ? S / 32 : 1;
 	constexpr int kRows = S > 0 ? (kBatch + 1) * S : 1;
 
-	__shared__ int s_gid[2][kBatch];
-	__shared__ float2 s_mean[2][kBatch];
-	__shared__ float4 s_conic[2][kBatch];
-	__shared__ float4 s_color[2][RGB ? kBatch : 1];
-	__shared__ float4 s_box[2][kBatch];
-	// Feature rows of the batch being walked and of the next one; row kBatch stays zero (positions
-	// past the end of a partial group point at it).
+	// Gaussian ids of batches b, b+1, b+2 (slot b % 3).
+	__shared__ int s_gid[3][kBatch];
+	// Records and feature rows of the batch being walked and of the next one; feature row kBatch
+	// stays zero (positions past the end of a partial group point at it).
+	__shared__ HdsHeaderSlot<kBatch, RGB> s_hdr0, s_hdr1;
 	__shared__ __attribute__((aligned(16))) float s_feat0[kRows];
 	__shared__ __attribute__((aligned(16))) float s_feat1[kRows];
 
@@ -145,48 +142,42 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S > 0 ? 2 :
 
 	if (num_batches == 0) goto write_out;
 	{
-		// Prologue: batch 0 staged synchronously, the gids of batch 1 read.
+		// Prologue: gids of batches 0 and 1, then batch 0 staged synchronously.
 		if constexpr (S > 0)
 			for (int i = tid; i < S; i += blockDim.x) s_feat0[kBatch * S + i] = s_feat1[kBatch * S + i] = 0.0f;
 		const int cnt0 = batch_count(0), cnt1 = batch_count(1);
-		if (tid < cnt0) {
-			const int gid = a.values[range.x + tid];
-			const float2 m = a.means2D[gid];
-			const float4 co = a.conic4[gid];
-			s_gid[0][tid] = gid;
-			s_mean[0][tid] = m;
-			s_conic[0][tid] = co;
-			if constexpr (RGB) s_color[0][tid] = a.color_op4[gid];
-			s_box[0][tid] = hds_cull_box(m, co);
-		}
+		if (tid < cnt0) s_gid[0][tid] = a.values[range.x + tid];
 		if (tid < cnt1) s_gid[1][tid] = a.values[range.x + kBatch + tid];
 		__syncthreads();
-		if constexpr (S > 0) hds_stage_rows_async<S, false>(s_feat0, a.features, a.channels, c0, s_gid[0], cnt0, tid);
+		hds_stage_headers_async<kBatch, RGB>(s_hdr0, a.means2D, a.conic4, a.color_op4, s_gid[0], cnt0, tid);
+		if constexpr (S > 0)
+			hds_stage_rows_async<S, false, kBatch>(s_feat0, a.features, a.channels, c0, s_gid[0], cnt0, tid);
 		hds_wait_vmem();
 		__syncthreads();
 	}
 
 	{
-		// One batch: prefetch b+1 / b+2, walk b, publish b+1. Returns true when every pixel is done.
-		auto step = [&](int b, int p, const float* feat, float* feat_next) -> bool {
+		// One batch: stage b+1, read the gids of b+2, walk b. Returns true when every pixel is done.
+		auto step = [&](int b, const HdsHeaderSlot<kBatch, RGB>& h, const float* feat,
+						HdsHeaderSlot<kBatch, RGB>& h_next, float* feat_next) -> bool {
 			const int cnt = batch_count(b), cnt1 = batch_count(b + 1), cnt2 = batch_count(b + 2);
-			if constexpr (S > 0)
-				if (cnt1 > 0) hds_stage_rows_async<S, false>(feat_next, a.features, a.channels, c0, s_gid[p ^ 1], cnt1, tid);
-			float2 m1 = make_float2(0.0f, 0.0f);
-			float4 co1 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), col1 = co1;
 			int g2 = 0;
-			if (tid < cnt1) {
-				const int gid = s_gid[p ^ 1][tid];
-				m1 = a.means2D[gid];
-				co1 = a.conic4[gid];
-				if constexpr (RGB) col1 = a.color_op4[gid];
-			}
 			if (tid < cnt2) g2 = a.values[range.x + (b + 2) * kBatch + tid];
+			const int* gid_next = s_gid[(b + 1) % 3];
+			if (cnt1 > 0) {
+				hds_stage_headers_async<kBatch, RGB>(h_next, a.means2D, a.conic4, a.color_op4, gid_next, cnt1, tid);
+				if constexpr (S > 0)
+					hds_stage_rows_async<S, false, kBatch>(feat_next, a.features, a.channels, c0, gid_next, cnt1, tid);
+			}
 
 			if (hds_ballot(!st.done) != 0) {
 				const int batch = b * kBatch;
-				uint64_t hits =
-					hds_ballot(lane < cnt && hds_box_hits(s_box[p][lane < cnt ? lane : 0], rx0, rx1, ry0, ry1));
+				bool box_hit = false;
+				if (lane < cnt) {
+					const float4 box = hds_cull_box(make_float2(h.mx[lane], h.my[lane]), h.conic[lane]);
+					box_hit = hds_box_hits(box, rx0, rx1, ry0, ry1);
+				}
+				uint64_t hits = hds_ballot(box_hit);
 				while (hits) {
 					// The next group: up to 16 box-hits in list order; missing positions use the zero row.
 					int slot[kGroup];
@@ -208,7 +199,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S > 0 ? 2 :
 						for (int u = 0; u < kIlp; u++) {
 							const int sl = min(slot[q0 + u], kBatch - 1);
 							float G, dx, dy;
-							alpha[u] = fminf(HDS_MAX_ALPHA, hds_raw_alpha(fx, fy, s_mean[p][sl], s_conic[p][sl], G, dx, dy));
+							alpha[u] = fminf(HDS_MAX_ALPHA, hds_raw_alpha(fx, fy, make_float2(h.mx[sl], h.my[sl]),
+																		  h.conic[sl], G, dx, dy));
 						}
 #pragma unroll
 						for (int u = 0; u < kIlp; u++) {
@@ -221,7 +213,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S > 0 ? 2 :
 								} else {
 									w[q] = alpha[u] * st.T;
 									if constexpr (RGB) {
-										const float4 col = s_color[p][slot[q]];
+										const float4 col = h.color[slot[q]];
 										st.r += w[q] * col.x;
 										st.g += w[q] * col.y;
 										st.b += w[q] * col.z;
@@ -242,19 +234,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S > 0 ? 2 :
 				}
 			}
 
-			if (tid < cnt1) {
-				s_mean[p ^ 1][tid] = m1;
-				s_conic[p ^ 1][tid] = co1;
-				if constexpr (RGB) s_color[p ^ 1][tid] = col1;
-				s_box[p ^ 1][tid] = hds_cull_box(m1, co1);
-			}
-			if (tid < cnt2) s_gid[p][tid] = g2;
+			if (tid < cnt2) s_gid[(b + 2) % 3][tid] = g2;
 			hds_wait_vmem();
 			return __syncthreads_count(st.done) == (int)blockDim.x;
 		};
 		for (int b = 0; b < num_batches; b += 2) {
-			if (step(b, 0, s_feat0, s_feat1) || b + 1 >= num_batches) break;
-			if (step(b + 1, 1, s_feat1, s_feat0)) break;
+			if (step(b, s_hdr0, s_feat0, s_hdr1, s_feat1) || b + 1 >= num_batches) break;
+			if (step(b + 1, s_hdr1, s_feat1, s_hdr0, s_feat0)) break;
 		}
 	}
 

@@ -29,14 +29,15 @@ __device__ static inline int hds_stage_chunk(int c, int r) {
 }
 
 /* Issues the copy of rows 0..cnt-1 (S channels from c0 of features[gids[row]]) into buf, one
- * 1 KB block of rows per wave instruction; cnt <= 64, the work-group has 256 threads. The caller
- * waits with hds_wait_vmem() and a barrier before reading. */
-template <int S, bool kSwizzle>
-__device__ inline void hds_stage_rows_async(float* buf, const float* __restrict__ features, int channels, int c0,
+ * 1 KB block of rows per wave instruction; cnt <= kRowsMax, the work-group has 256 threads. The
+ * caller waits with hds_wait_vmem() and a barrier before reading. */
+template <int S, bool kSwizzle, int kRowsMax>
+__device__ inline void hds_stage_rows_async(float* buf, const float* features, int channels, int c0,
 											const int* gids, int cnt, int tid) {
 	constexpr int kChunks = S / 4;              // 16-byte chunks per row
 	constexpr int kRowsPerOp = 64 / kChunks;    // rows per 1 KB wave instruction
-	constexpr int kOps = 64 / kRowsPerOp;       // instructions per 64-row batch
+	constexpr int kOps = kRowsMax / kRowsPerOp; // instructions per batch
+	static_assert(kRowsMax % kRowsPerOp == 0, "batch must be whole 1 KB blocks");
 	const int lane = tid & 63, wave = tid >> 6;
 	const int chunk = lane % kChunks;
 #pragma unroll
@@ -47,6 +48,47 @@ __device__ inline void hds_stage_rows_async(float* buf, const float* __restrict_
 			__builtin_amdgcn_global_load_lds(src, (hds_lds_void*)(buf + op * 256), 16, 0, 0);
 		}
 	}
+}
+
+/* Gaussian records of one pipeline slot, filled by LDS DMA: mean x / y, conic4 = (a, b, c, opacity)
+ * and, for the RGB walks, color_opacity4. Each slot is its own __shared__ object. */
+template <int kB, bool kColor>
+struct HdsHeaderSlot {
+	float mx[kB];
+	float my[kB];
+	float4 conic[kB];
+	float4 color[kColor ? kB : 1];
+};
+
+/* Issues the copy of the records of rows 0..cnt-1 (gaussians gids[row]) into h: one DMA
+ * instruction per array, spread over the four waves. */
+template <int kB, bool kColor>
+__device__ inline void hds_stage_headers_async(HdsHeaderSlot<kB, kColor>& h, const float2* means2D,
+											   const float4* conic4, const float4* color4,
+											   const int* gids, int cnt, int tid) {
+	static_assert(kB <= 64, "one row per lane");
+	const int lane = tid & 63, wave = tid >> 6;
+	if (lane >= cnt) return;
+	const int gid = gids[lane];
+	if (wave == 0) {
+		__builtin_amdgcn_global_load_lds(conic4 + gid, (hds_lds_void*)h.conic, 16, 0, 0);
+	} else if (wave == 1) {
+		if constexpr (kColor) __builtin_amdgcn_global_load_lds(color4 + gid, (hds_lds_void*)h.color, 16, 0, 0);
+	} else if (wave == 2) {
+		__builtin_amdgcn_global_load_lds(&means2D[gid].x, (hds_lds_void*)h.mx, 4, 0, 0);
+	} else {
+		__builtin_amdgcn_global_load_lds(&means2D[gid].y, (hds_lds_void*)h.my, 4, 0, 0);
+	}
+}
+
+/* One 16-byte LDS read kept as a single vector load. Left alone, the compiler splits a vector
+ * load whose elements are used separately into scalar loads and merges them back into
+ * ds_read_b128 late, and the merged access has lost the alias information that tells it apart from
+ * the LDS DMA in flight: the wait-count pass then waits for all outstanding DMA before it. */
+__device__ static inline hds_u32x4 hds_lds_read128(const uint32_t* p) {
+	hds_u32x4 v = *reinterpret_cast<const hds_u32x4*>(p);
+	asm volatile("" : "+v"(v));
+	return v;
 }
 
 /* Eight fp32 values -> the split-bf16 hi and lo operands of one MFMA. */
