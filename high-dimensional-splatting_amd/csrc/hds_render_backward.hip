@@ -479,10 +479,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S >= 128 ? 
 	const BackwardArgs a) {
 	constexpr int kNcb = S / 32;
 
-	__shared__ int s_gid[kBatch];
-	__shared__ float2 s_mean[kBatch];
-	__shared__ float4 s_conic[kBatch];
-	__shared__ float4 s_box[kBatch];
+	// Gaussian ids of batches b, b+1, b+2 (slot b % 3) and the records of the batch being walked and of
+	// the next one (the pipeline of render_forward_kernel).
+	__shared__ int s_gid[3][kBatch];
+	__shared__ HdsHeaderSlot<kBatch, false> s_hdr0, s_hdr1;
 	__shared__ __attribute__((aligned(16))) uint32_t s_w[4][kFeatGroup * kRowStride];
 	__shared__ __attribute__((aligned(16))) int s_ggid[4][kFeatGroup];
 	__shared__ int s_max_last;
@@ -533,59 +533,80 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S >= 128 ? 
 
 	float T = 1.0f;
 	int q = 0;  // filled positions of the wave's current group
-	for (int batch = 0; batch < num; batch += kBatch) {
-		const int cnt = min(kBatch, num - batch);
+	const int num_batches = (num + kBatch - 1) / kBatch;
+	auto batch_count = [&](int b) { return b < num_batches ? min(kBatch, num - b * kBatch) : 0; };
+	if (num_batches > 0) {
+		// Prologue: gids of batches 0 and 1, then the records of batch 0.
+		const int cnt0 = batch_count(0), cnt1 = batch_count(1);
+		if (tid < cnt0) s_gid[0][tid] = a.values[range.x + tid];
+		if (tid < cnt1) s_gid[1][tid] = a.values[range.x + kBatch + tid];
 		__syncthreads();
-		if (tid < cnt) {
-			const int gid = a.values[range.x + batch + tid];
-			const float2 m = a.means2D[gid];
-			const float4 co = a.conic4[gid];
-			s_gid[tid] = gid;
-			s_mean[tid] = m;
-			s_conic[tid] = co;
-			s_box[tid] = hds_cull_box(m, co);
-		}
+		hds_stage_headers_async<kBatch, false>(s_hdr0, a.means2D, a.conic4, nullptr, s_gid[0], cnt0, tid);
+		hds_wait_vmem();
 		__syncthreads();
-		if (batch >= wave_last) continue;
+	}
+	// One batch: stage b+1, read the gids of b+2, walk b.
+	auto step = [&](int b, const HdsHeaderSlot<kBatch, false>& h, HdsHeaderSlot<kBatch, false>& h_next) {
+		const int cnt = batch_count(b), cnt1 = batch_count(b + 1), cnt2 = batch_count(b + 2);
+		const int batch = b * kBatch;
+		const int* bgid = s_gid[b % 3];
+		int g2 = 0;
+		if (tid < cnt2) g2 = a.values[range.x + (b + 2) * kBatch + tid];
+		if (cnt1 > 0) hds_stage_headers_async<kBatch, false>(h_next, a.means2D, a.conic4, nullptr, s_gid[(b + 1) % 3], cnt1, tid);
 
-		uint64_t hits = hds_ballot(lane < cnt && batch + lane < wave_last &&
-								   hds_box_hits(s_box[lane < cnt ? lane : 0], rx0, rx1, ry0, ry1));
-		while (hits) {
-			// The next (up to) kIlp hits in list order, as many as the group has room for.
-			const int take = min(min(kIlp, __builtin_popcountll(hits)), kFeatGroup - q);
-			int slot[kIlp];
-			float alpha[kIlp];
-#pragma unroll
-			for (int u = 0; u < kIlp; u++) {
-				slot[u] = kBatch - 1;
-				if (u < take) {
-					slot[u] = __builtin_ctzll(hits);
-					hits &= hits - 1;
-				}
-				float G, dx, dy;
-				alpha[u] = fminf(HDS_MAX_ALPHA, hds_raw_alpha(fx, fy, s_mean[slot[u]], s_conic[slot[u]], G, dx, dy));
+		if (batch < wave_last) {
+			bool box_hit = false;
+			if (lane < cnt && batch + lane < wave_last) {
+				const float4 box = hds_cull_box(make_float2(h.mx[lane], h.my[lane]), h.conic[lane]);
+				box_hit = hds_box_hits(box, rx0, rx1, ry0, ry1);
 			}
+			uint64_t hits = hds_ballot(box_hit);
+			while (hits) {
+				// The next (up to) kIlp hits in list order, as many as the group has room for.
+				const int take = min(min(kIlp, __builtin_popcountll(hits)), kFeatGroup - q);
+				int slot[kIlp];
+				float alpha[kIlp];
 #pragma unroll
-			for (int u = 0; u < kIlp; u++) {
-				if (u >= take) break;
-				// The forward's test, with its termination read from n_contrib.
-				const bool contributes = batch + slot[u] < last && alpha[u] >= HDS_MIN_ALPHA;
-				float w = 0.0f;
-				if (contributes) {
-					const float test_T = T * (1.0f - alpha[u]);
-					w = alpha[u] * T;
-					T = test_T;
+				for (int u = 0; u < kIlp; u++) {
+					slot[u] = kBatch - 1;
+					if (u < take) {
+						slot[u] = __builtin_ctzll(hits);
+						hits &= hits - 1;
+					}
+					float G, dx, dy;
+					alpha[u] = fminf(HDS_MAX_ALPHA, hds_raw_alpha(fx, fy, make_float2(h.mx[slot[u]], h.my[slot[u]]),
+																  h.conic[slot[u]], G, dx, dy));
 				}
-				rows[(q + u) * kRowStride + lane] = hds_split_pack(w);
-				const bool any = hds_ballot(contributes) != 0;
-				if (lane == 0) gids[q + u] = any ? s_gid[slot[u]] : -1;
-			}
-			q += take;
-			if (q == kFeatGroup) {
-				flush_features<S>(gb_hi, gb_lo, rows, gids, a.grad_features, a.channels, c0, lane);
-				q = 0;
+#pragma unroll
+				for (int u = 0; u < kIlp; u++) {
+					if (u >= take) break;
+					// The forward's test, with its termination read from n_contrib.
+					const bool contributes = batch + slot[u] < last && alpha[u] >= HDS_MIN_ALPHA;
+					float w = 0.0f;
+					if (contributes) {
+						const float test_T = T * (1.0f - alpha[u]);
+						w = alpha[u] * T;
+						T = test_T;
+					}
+					rows[(q + u) * kRowStride + lane] = hds_split_pack(w);
+					const bool any = hds_ballot(contributes) != 0;
+					if (lane == 0) gids[q + u] = any ? bgid[slot[u]] : -1;
+				}
+				q += take;
+				if (q == kFeatGroup) {
+					flush_features<S>(gb_hi, gb_lo, rows, gids, a.grad_features, a.channels, c0, lane);
+					q = 0;
+				}
 			}
 		}
+
+		if (tid < cnt2) s_gid[(b + 2) % 3][tid] = g2;
+		hds_wait_vmem();
+		__syncthreads();
+	};
+	for (int b = 0; b < num_batches; b += 2) {
+		step(b, s_hdr0, s_hdr1);
+		if (b + 1 < num_batches) step(b + 1, s_hdr1, s_hdr0);
 	}
 	if (q > 0) {
 		for (int r = q; r < kFeatGroup; r++) rows[r * kRowStride + lane] = 0u;
