@@ -255,7 +255,9 @@ __device__ static inline float hds_raw_alpha(float px, float py, float2 mean, fl
 	dx = px - mean.x;
 	dy = py - mean.y;
 	const float m = dx * (conic_op.x * dx + conic_op.y * dy) + dy * (conic_op.y * dx + conic_op.z * dy);
-	G = __expf(-0.5f * m);
+	// exp(-m / 2) as the hardware exp2 of m * (-log2(e) / 2): halving is exact, so the product is
+	// bit for bit the (-0.5 m) * log2(e) that __expf(-0.5 m) forms, with one multiply less.
+	G = __builtin_amdgcn_exp2f(m * (-0.5f * 1.44269502162933349609375f));
 	return conic_op.w * G;
 }
 

@@ -77,6 +77,7 @@ __device__ inline int tile_max_last(int last, int* s_max_last) {
 template <int S, bool RGB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void backward_geometry_kernel(const BackwardArgs a) {
 	constexpr int kKc = S > 0 ? S / 32 : 1;       // K steps of the dot over channels
+	constexpr int kAccStride = 9;
 	// Gaussians per batch: 32 at S = 128 so that two work-groups fit a CU's LDS; positions whose
 	// alphas are evaluated together: 2 at S = 128, where dL/dF takes half the registers.
 	constexpr int kGB = S >= 128 ? 32 : kBatch;
@@ -89,6 +90,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void b
 	// partial group point at it).
 	__shared__ int s_gid[3][kGB];
 	__shared__ HdsHeaderSlot<kGB, RGB> s_hdr0, s_hdr1;
+	// Gradients of batch b summed over the tile's waves (slot b & 1), 9 per gaussian: opacity,
+	// mean x / y, conic a / b / c, colour r / g / b. One lane per gaussian then adds them to HBM.
+	__shared__ float s_acc[2][kGB * kAccStride];
 	__shared__ __attribute__((aligned(16))) float s_feat0[kRows];
 	__shared__ __attribute__((aligned(16))) float s_feat1[kRows];
 	__shared__ int s_slot[4][kGeoGroup];
@@ -209,6 +213,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void b
 		const int cnt0 = batch_count(0), cnt1 = batch_count(1);
 		if (tid < cnt0) s_gid[0][tid] = a.values[range.x + batch_start_of(0) + tid];
 		if (tid < cnt1) s_gid[1][tid] = a.values[range.x + batch_start_of(1) + tid];
+		for (int i = tid; i < 2 * kGB * kAccStride; i += blockDim.x) (&s_acc[0][0])[i] = 0.0f;
 		__syncthreads();
 		hds_stage_headers_async<kGB, RGB>(s_hdr0, a.means2D, a.conic4, a.color_op4, s_gid[0], cnt0, tid);
 		if constexpr (S > 0) hds_stage_rows_async<S, true, kGB>(s_feat0, a.features, a.channels, c0, s_gid[0], cnt0, tid);
@@ -216,12 +221,41 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void b
 		__syncthreads();
 	}
 
+	// Adds batch b's summed gradients to HBM, one lane per gaussian, and clears its slot for b + 2.
+	// Runs at the end of the step that follows batch b (after the barrier that closed b, before the
+	// gids of b + 3 replace those of b in slot b % 3).
+	auto flush_gradients = [&](int b) {
+		const int cnt = batch_count(b);
+		if (tid >= cnt) return;
+		float* g = s_acc[b & 1] + tid * kAccStride;
+		const int gid = s_gid[b % 3][tid];
+		float v[kAccStride];
+#pragma unroll
+		for (int k = 0; k < kAccStride; k++) {
+			v[k] = g[k];
+			g[k] = 0.0f;
+		}
+		if (v[0] != 0.0f || v[1] != 0.0f || v[2] != 0.0f || v[3] != 0.0f || v[4] != 0.0f || v[5] != 0.0f) {
+			atomicAdd(&a.grad_opacities[gid], v[0]);
+			atomicAdd(&a.grad_means2D[gid * 2 + 0], v[1]);
+			atomicAdd(&a.grad_means2D[gid * 2 + 1], v[2]);
+			atomicAdd(&a.grad_conics[gid * 3 + 0], v[3]);
+			atomicAdd(&a.grad_conics[gid * 3 + 1], v[4]);
+			atomicAdd(&a.grad_conics[gid * 3 + 2], v[5]);
+		}
+		if (do_rgb && (v[6] != 0.0f || v[7] != 0.0f || v[8] != 0.0f)) {
+			atomicAdd(&a.grad_colors[gid * 3 + 0], v[6]);
+			atomicAdd(&a.grad_colors[gid * 3 + 1], v[7]);
+			atomicAdd(&a.grad_colors[gid * 3 + 2], v[8]);
+		}
+	};
+
 	// One batch: stage b+1, read the gids of b+2, walk b.
 	auto step = [&](int b, const HdsHeaderSlot<kGB, RGB>& h, const float* feat, HdsHeaderSlot<kGB, RGB>& h_next,
 					float* feat_next) {
 		const int cnt = batch_count(b), cnt1 = batch_count(b + 1), cnt2 = batch_count(b + 2);
 		const int batch_start = batch_start_of(b);
-		const int* gids = s_gid[b % 3];
+		float* acc = s_acc[b & 1];
 		int g2 = 0;
 		if (tid < cnt2) g2 = a.values[range.x + batch_start_of(b + 2) + tid];
 		const int* gid_next = s_gid[(b + 1) % 3];
@@ -313,12 +347,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void b
 					if (q0 < count) {
 						int slot[kGeoIlp];
 						float raw[kGeoIlp], G[kGeoIlp];
+						float4 col[kGeoIlp];
 		#pragma unroll
 						for (int u = 0; u < kGeoIlp; u++) {
 							slot[u] = slots[q0 + u];
 							const int sl = min(slot[u], kGB - 1);
 							float dx, dy;
 							raw[u] = hds_raw_alpha(fx, fy, make_float2(h.mx[sl], h.my[sl]), h.conic[sl], G[u], dx, dy);
+							// Read with the geometry: a read under the replay branch would stall on LDS latency.
+							if constexpr (RGB) col[u] = h.color[sl];
 						}
 		#pragma unroll
 						for (int u = 0; u < kGeoIlp; u++) {
@@ -331,15 +368,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void b
 								T *= inv_1ma;
 								w = alpha * T;
 								if (do_rgb) {
-									const float4 col = h.color[slot[u]];
 									rec_r = last_alpha * last_r + (1.0f - last_alpha) * rec_r;
 									rec_g = last_alpha * last_g + (1.0f - last_alpha) * rec_g;
 									rec_b = last_alpha * last_b + (1.0f - last_alpha) * rec_b;
-									last_r = col.x;
-									last_g = col.y;
-									last_b = col.z;
+									last_r = col[u].x;
+									last_g = col[u].y;
+									last_b = col[u].z;
 									last_alpha = alpha;
-									dL_dalpha = ((col.x - rec_r) * gr + (col.y - rec_g) * gg + (col.z - rec_b) * gb) * T -
+									dL_dalpha = ((col[u].x - rec_r) * gr + (col[u].y - rec_g) * gg + (col[u].z - rec_b) * gb) * T -
 												T_final * inv_1ma * dL_dTf;
 								}
 								if constexpr (S > 0) {
@@ -394,9 +430,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void b
 				const int q = lane & 15;
 				const bool mine = q < count && ((active >> q) & 1u);
 				if (lane < 16 && mine) {
-					// Moments about the block centre -> gradients (backward.cu:136-160, in moment form).
+					// Moments about the block centre -> gradients (backward.cu:136-160, in moment form),
+					// summed over the tile's waves in LDS.
 					const int sl = slots[q];
-					const int gid = gids[sl];
 					const float2 mn = make_float2(h.mx[sl], h.my[sl]);
 					const float4 co = h.conic[sl];
 					const float m00 = ms[0], m10 = ms[1], m01 = ms[2], m20 = ms[3];
@@ -405,24 +441,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void b
 					const float sxx = m20 - 2.0f * mx * m10 + mx * mx * m00;
 					const float sxy = m11 - mx * m01 - my * m10 + mx * my * m00;
 					const float syy = m02 - 2.0f * my * m01 + my * my * m00;
-					atomicAdd(&a.grad_opacities[gid], m00);
-					atomicAdd(&a.grad_means2D[gid * 2 + 0], co.w * (co.x * sx + co.y * sy));
-					atomicAdd(&a.grad_means2D[gid * 2 + 1], co.w * (co.y * sx + co.z * sy));
-					atomicAdd(&a.grad_conics[gid * 3 + 0], -0.5f * co.w * sxx);
-					atomicAdd(&a.grad_conics[gid * 3 + 1], -co.w * sxy);
-					atomicAdd(&a.grad_conics[gid * 3 + 2], -0.5f * co.w * syy);
+					float* g = acc + sl * kAccStride;
+					atomicAdd(&g[0], m00);
+					atomicAdd(&g[1], co.w * (co.x * sx + co.y * sy));
+					atomicAdd(&g[2], co.w * (co.y * sx + co.z * sy));
+					atomicAdd(&g[3], -0.5f * co.w * sxx);
+					atomicAdd(&g[4], -co.w * sxy);
+					atomicAdd(&g[5], -0.5f * co.w * syy);
 				}
 				if (do_rgb && lane >= 32 && lane < 48 && mine) {
 					// Rows 8-10: the colour gradients sum_px w dL/dRGB (backward.cu:112-118).
-					const int gid = gids[slots[q]];
-					atomicAdd(&a.grad_colors[gid * 3 + 0], mw[0]);
-					atomicAdd(&a.grad_colors[gid * 3 + 1], mw[1]);
-					atomicAdd(&a.grad_colors[gid * 3 + 2], mw[2]);
+					float* g = acc + slots[q] * kAccStride;
+					atomicAdd(&g[6], mw[0]);
+					atomicAdd(&g[7], mw[1]);
+					atomicAdd(&g[8], mw[2]);
 				}
 				hds_wave_fence();
 			}
 		}
 
+		if (b > 0) flush_gradients(b - 1);
 		if (tid < cnt2) s_gid[(b + 2) % 3][tid] = g2;
 		hds_wait_vmem();
 		__syncthreads();
@@ -431,6 +469,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void b
 		step(b, s_hdr0, s_feat0, s_hdr1, s_feat1);
 		if (b + 1 < num_batches) step(b + 1, s_hdr1, s_feat1, s_hdr0, s_feat0);
 	}
+	flush_gradients(num_batches - 1);
 }
 
 // dF[position][c] += sum_px W[position][px] dL/dF[px][c] for one group of 32 positions, then one
@@ -588,11 +627,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S >= 128 ? 
 						w = alpha[u] * T;
 						T = test_T;
 					}
-					rows[(q + u) * kRowStride + lane] = hds_split_pack(w);
-					const bool any = hds_ballot(contributes) != 0;
-					if (lane == 0) gids[q + u] = any ? bgid[slot[u]] : -1;
+					// A gaussian no pixel of the block takes gets no row (and no atomics).
+					if (hds_ballot(contributes) != 0) {
+						rows[q * kRowStride + lane] = hds_split_pack(w);
+						if (lane == 0) gids[q] = bgid[slot[u]];
+						q++;
+					}
 				}
-				q += take;
 				if (q == kFeatGroup) {
 					flush_features<S>(gb_hi, gb_lo, rows, gids, a.grad_features, a.channels, c0, lane);
 					q = 0;

@@ -103,7 +103,7 @@ struct Pixel {
 // LDS DMA while b is walked, and the gids of b+2 are read; one barrier, after each wave has waited
 // for its copies, hands the next batch over.
 template <int S, bool RGB>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S > 0 ? 2 : 4))) void render_forward_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S >= 128 ? 2 : S == 64 ? 3 : 4))) void render_forward_kernel(
 	const RenderArgs a) {
 	constexpr int kNcb = S > 0 ? S / 32 : 1;
 	constexpr int kRows = S > 0 ? (kBatch + 1) * S : 1;
@@ -195,12 +195,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S > 0 ? 2 :
 #pragma unroll
 					for (int q0 = 0; q0 < kGroup; q0 += kIlp) {
 						float alpha[kIlp];
+						float4 col[kIlp];
 #pragma unroll
 						for (int u = 0; u < kIlp; u++) {
 							const int sl = min(slot[q0 + u], kBatch - 1);
 							float G, dx, dy;
 							alpha[u] = fminf(HDS_MAX_ALPHA, hds_raw_alpha(fx, fy, make_float2(h.mx[sl], h.my[sl]),
 																		  h.conic[sl], G, dx, dy));
+							// Read with the geometry: a read under the blend branch would stall on LDS latency.
+							if constexpr (RGB) col[u] = h.color[sl];
 						}
 #pragma unroll
 						for (int u = 0; u < kIlp; u++) {
@@ -213,10 +216,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S > 0 ? 2 :
 								} else {
 									w[q] = alpha[u] * st.T;
 									if constexpr (RGB) {
-										const float4 col = h.color[slot[q]];
-										st.r += w[q] * col.x;
-										st.g += w[q] * col.y;
-										st.b += w[q] * col.z;
+										st.r += w[q] * col[u].x;
+										st.g += w[q] * col[u].y;
+										st.b += w[q] * col[u].z;
 									}
 									st.T = test_T;
 									st.last = batch + slot[q] + 1;

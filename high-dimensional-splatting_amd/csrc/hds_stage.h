@@ -40,7 +40,8 @@ __device__ inline void hds_stage_rows_async(float* buf, const float* features, i
 	static_assert(kRowsMax % kRowsPerOp == 0, "batch must be whole 1 KB blocks");
 	const int lane = tid & 63, wave = tid >> 6;
 	const int chunk = lane % kChunks;
-#pragma unroll
+	// Not unrolled: one row address live at a time keeps this off the walk's register budget.
+#pragma unroll 1
 	for (int op = wave; op < kOps; op += 4) {
 		const int row = op * kRowsPerOp + lane / kChunks;
 		if (row < cnt) {
