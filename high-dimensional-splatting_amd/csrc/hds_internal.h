@@ -203,18 +203,14 @@ __device__ static inline uint32_t hds_opaque(uint32_t v) {
 /* One MFMA result element as an independent 32-bit operand for a lane swap. */
 __device__ static inline uint32_t hds_swap_operand(float v) { return hds_opaque(__builtin_bit_cast(uint32_t, v)); }
 
-/* XCD-aware work-group order. Work-groups are dispatched round-robin over the 8 XCDs, each with its
- * own L2, so consecutive block ids land on different L2s. Remapping block b to tile
- * (b % 8) * ceil(T / 8) + b / 8 gives every XCD a contiguous band of tiles: neighbouring tiles, which
- * share most of their gaussians, then read them through the same L2. Returns -1 for the padding
- * blocks of a grid rounded up to a multiple of 8. */
+/* Tile of a work-group. Work-groups are dispatched round-robin over the 8 XCDs, so the identity
+ * order deals consecutive tiles to different XCDs: every XCD gets an even share of the dense centre
+ * of the image (mapping contiguous bands of tiles to one XCD left the busiest XCD with 1.33x the mean
+ * work at the headline scene). Neighbouring tiles then share gaussians through the memory-side cache
+ * rather than one XCD's L2. The grid is a multiple of 8; padding blocks get -1. */
 #define HDS_XCDS 8
 static inline unsigned hds_xcd_grid(int num_tiles) { return (unsigned)(((num_tiles + HDS_XCDS - 1) / HDS_XCDS) * HDS_XCDS); }
-__device__ static inline int hds_xcd_tile(int block, int num_tiles) {
-	const int per_xcd = (num_tiles + HDS_XCDS - 1) / HDS_XCDS;
-	const int tile = (block % HDS_XCDS) * per_xcd + block / HDS_XCDS;
-	return tile < num_tiles ? tile : -1;
-}
+__device__ static inline int hds_xcd_tile(int block, int num_tiles) { return block < num_tiles ? block : -1; }
 
 /* acc += A * B with A, B given as split-bf16 pairs (small terms first). */
 __device__ static inline hds_f32x4 hds_mfma_split(const hds_bf16x8& a_hi, const hds_bf16x8& a_lo,
