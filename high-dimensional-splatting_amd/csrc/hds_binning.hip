@@ -11,8 +11,14 @@
 // 8 B per pair and pass instead of 12. Everything is integer work; the only floating point is the
 // shared tile rectangle of hds_common.h.
 //
-// Scans and sorts are written for wave64: ranks inside a wave come from ballot-based digit
-// matching (no shuffles, no LDS atomics on a hot bin), and blocks own 4096 consecutive items.
+// Sorts and scans are single-pass: every radix pass is ONE launch in which each work-group ranks
+// its 4096-item partition in registers and LDS, publishes its per-digit counts, and reads the
+// counts of the partitions before it from a status array (decoupled look-back), so no separate
+// histogram / scan launches sit between passes. Partitions are handed out in launch order by an
+// atomic ticket, which is what makes the look-back safe: a work-group only ever waits for
+// partitions whose owners are already running and never wait themselves before publishing. The
+// digit histograms every pass needs up front come from the kernel that produces the keys
+// (prepare for depths, emit for tile ids). The whole binning is 11 launches.
 #include "hds_internal.h"
 #include "hds_rasterizer.h"
 
@@ -20,24 +26,75 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kItemsPerThread = 16;
-constexpr int kTileItems = kThreads * kItemsPerThread;  // items one block owns
+constexpr int kTileItems = kThreads * kItemsPerThread;  // items one partition / work-group owns
+constexpr int kWaves = kThreads / HDS_WAVE;
+constexpr int kWaveItems = kTileItems / kWaves;         // a wave ranks 16 rows of 64 consecutive items
 constexpr int kRadixBits = 8;
 constexpr int kRadix = 1 << kRadixBits;
-constexpr int kWaves = kThreads / HDS_WAVE;
+constexpr int kMaxPasses = 4;                           // 32-bit keys
+constexpr int kEmitCache = 4096;                        // depth-ordered offsets one emit work-group caches
+// Polls of a silent predecessor before a look-back gives up and raises the error flag (seconds of
+// waiting; reached only if a launch is broken, never by a slow but running predecessor).
+constexpr uint32_t kSpinLimit = 1u << 22;
 
 static_assert(kRadix == kThreads, "one thread per radix bin");
 
-inline int64_t tiles_of(int64_t n) { return (n + kTileItems - 1) / kTileItems; }
+inline int64_t parts_of(int64_t n) { return (n + kTileItems - 1) / kTileItems; }
 
 // ---------------------------------------------------------------------------------------------
-// Exclusive prefix sum of uint32 values, optionally gathered through an index array
-// (out[i] = sum_{j<i} in[idx[j]]), in three launches: block sums, one-block scan of the sums,
-// block-local scans plus the block offset. The grand total goes to *total as uint64.
+// Decoupled look-back. A status word is (flag << 56 | value): flag 2e+1 = the partition's own
+// count (aggregate) of epoch e, 2e+2 = inclusive prefix through that partition; anything lower is
+// "not yet". Epochs let one zeroed array serve all radix passes of a sort in turn.
 // ---------------------------------------------------------------------------------------------
 
-__device__ inline uint32_t scan_load(const uint32_t* __restrict__ in, const uint32_t* __restrict__ idx, int64_t i) {
-	return in[idx ? idx[i] : i];
+constexpr uint64_t kValueMask = (uint64_t(1) << 56) - 1;
+
+__device__ inline uint64_t status_word(uint32_t flag, uint64_t value) { return ((uint64_t)flag << 56) | value; }
+
+__device__ inline uint64_t status_load(uint64_t* p) {
+	return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+
+__device__ inline void status_store(uint64_t* p, uint64_t v) {
+	__hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Sum of the values that partitions [0, part) published in one column (status + p * stride):
+// walks back from part - 1 adding aggregates until an inclusive prefix ends the walk.
+__device__ inline uint64_t lookback(uint64_t* status, int64_t stride, int64_t part, uint32_t epoch,
+									uint32_t* error) {
+	const uint32_t agg = 2 * epoch + 1, inc = 2 * epoch + 2;
+	uint64_t sum = 0;
+	uint32_t spins = 0;
+	for (int64_t p = part - 1; p >= 0;) {
+		const uint64_t v = status_load(status + p * stride);
+		const uint32_t flag = (uint32_t)(v >> 56);
+		if (flag == inc) return sum + (v & kValueMask);
+		if (flag == agg) {
+			sum += v & kValueMask;
+			p--;
+			spins = 0;
+			continue;
+		}
+		if (++spins > kSpinLimit) {
+			atomicOr(error, 1u);
+			return sum;
+		}
+		__builtin_amdgcn_s_sleep(2);
+	}
+	return sum;
+}
+
+// Partition index in launch order (the look-back's progress guarantee), broadcast through LDS.
+__device__ inline int64_t take_ticket(uint32_t* ticket, int64_t* s_part) {
+	if (threadIdx.x == 0) *s_part = (int64_t)atomicAdd(ticket, 1u);
+	__syncthreads();
+	return *s_part;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Block primitives.
+// ---------------------------------------------------------------------------------------------
 
 // Exclusive scan across the block of one value per thread; also returns the block total.
 __device__ inline uint32_t block_exclusive_scan(uint32_t v, uint32_t* s_wave, uint32_t& total) {
@@ -62,115 +119,6 @@ __device__ inline uint32_t block_exclusive_scan(uint32_t v, uint32_t* s_wave, ui
 	return before + x - v;
 }
 
-__global__ __launch_bounds__(kThreads) void scan_reduce_kernel(const uint32_t* __restrict__ in,
-																const uint32_t* __restrict__ idx, int64_t n,
-																uint32_t* __restrict__ sums) {
-	__shared__ uint32_t s_wave[kWaves];
-	const int64_t base = (int64_t)blockIdx.x * kTileItems;
-	uint32_t v = 0;
-#pragma unroll 4
-	for (int r = 0; r < kItemsPerThread; r++) {
-		const int64_t i = base + r * kThreads + threadIdx.x;
-		if (i < n) v += scan_load(in, idx, i);
-	}
-	uint32_t total;
-	block_exclusive_scan(v, s_wave, total);
-	if (threadIdx.x == 0) sums[blockIdx.x] = total;
-}
-
-// Single work-group exclusive scan of the block sums, in place; total as uint64.
-__global__ __launch_bounds__(1024) void scan_top_kernel(uint32_t* __restrict__ sums, int64_t count,
-														uint64_t* __restrict__ total) {
-	__shared__ uint32_t s_wave[1024 / HDS_WAVE];
-	__shared__ uint64_t s_carry;
-	const int lane = threadIdx.x & (HDS_WAVE - 1), wave = threadIdx.x / HDS_WAVE;
-	if (threadIdx.x == 0) s_carry = 0;
-	__syncthreads();
-	for (int64_t base = 0; base < count; base += 1024) {
-		const int64_t i = base + threadIdx.x;
-		const uint32_t v = i < count ? sums[i] : 0u;
-		uint32_t x = v;
-#pragma unroll
-		for (int off = 1; off < HDS_WAVE; off <<= 1) {
-			const uint32_t y = __shfl_up(x, off, HDS_WAVE);
-			if (lane >= off) x += y;
-		}
-		if (lane == HDS_WAVE - 1) s_wave[wave] = x;
-		__syncthreads();
-		uint64_t before = 0, sum = 0;
-		for (int w = 0; w < 1024 / HDS_WAVE; w++) {
-			if (w < wave) before += s_wave[w];
-			sum += s_wave[w];
-		}
-		const uint64_t carry = s_carry;
-		if (i < count) sums[i] = (uint32_t)(carry + before + x - v);
-		__syncthreads();
-		if (threadIdx.x == 0) s_carry = carry + sum;
-		__syncthreads();
-	}
-	if (threadIdx.x == 0 && total) *total = s_carry;
-}
-
-__global__ __launch_bounds__(kThreads) void scan_apply_kernel(const uint32_t* __restrict__ in,
-															   const uint32_t* __restrict__ idx, int64_t n,
-															   const uint32_t* __restrict__ sums,
-															   uint32_t* __restrict__ out) {
-	// Items go through LDS so that global loads and stores stay coalesced while each thread
-	// scans 16 consecutive items; a pad word every 16 keeps the strided LDS reads conflict-free.
-	__shared__ uint32_t s_items[kTileItems + kTileItems / 16];
-	__shared__ uint32_t s_wave[kWaves];
-	const int64_t base = (int64_t)blockIdx.x * kTileItems;
-#pragma unroll 4
-	for (int r = 0; r < kItemsPerThread; r++) {
-		const int j = r * kThreads + threadIdx.x;
-		const int64_t i = base + j;
-		s_items[j + j / 16] = i < n ? scan_load(in, idx, i) : 0u;
-	}
-	__syncthreads();
-	uint32_t local[kItemsPerThread];
-	uint32_t sum = 0;
-	const int first = threadIdx.x * kItemsPerThread;
-#pragma unroll
-	for (int k = 0; k < kItemsPerThread; k++) {
-		local[k] = sum;
-		sum += s_items[first + k + (first + k) / 16];
-	}
-	uint32_t total;
-	const uint32_t before = block_exclusive_scan(sum, s_wave, total) + sums[blockIdx.x];
-#pragma unroll
-	for (int k = 0; k < kItemsPerThread; k++) s_items[first + k + (first + k) / 16] = local[k] + before;
-	__syncthreads();
-#pragma unroll 4
-	for (int r = 0; r < kItemsPerThread; r++) {
-		const int j = r * kThreads + threadIdx.x;
-		const int64_t i = base + j;
-		if (i < n) out[i] = s_items[j + j / 16];
-	}
-}
-
-int exclusive_scan(const uint32_t* in, const uint32_t* idx, int64_t n, uint32_t* out, uint32_t* sums,
-				   uint64_t* total, hipStream_t s) {
-	const int64_t blocks = tiles_of(n);
-	HdsKernelTimer timer1("scan_reduce_kernel", s);
-	scan_reduce_kernel<<<(unsigned)blocks, kThreads, 0, s>>>(in, idx, n, sums);
-	timer1.stop();
-	HDS_LAUNCH_CHECK("scan_reduce", s);
-	HdsKernelTimer timer2("scan_top_kernel", s);
-	scan_top_kernel<<<1, 1024, 0, s>>>(sums, blocks, total);
-	timer2.stop();
-	HDS_LAUNCH_CHECK("scan_top", s);
-	HdsKernelTimer timer3("scan_apply_kernel", s);
-	scan_apply_kernel<<<(unsigned)blocks, kThreads, 0, s>>>(in, idx, n, sums, out);
-	timer3.stop();
-	HDS_LAUNCH_CHECK("scan_apply", s);
-	return HDS_OK;
-}
-
-// ---------------------------------------------------------------------------------------------
-// Stable LSD radix sort of (uint32 key, uint32 value) pairs, 8 bits per pass.
-// Pass = per-block digit histograms (digit-major) -> exclusive scan -> stable scatter.
-// ---------------------------------------------------------------------------------------------
-
 // Lanes of this wave (among `active`) whose digit equals ours.
 __device__ inline uint64_t match_digit(uint32_t d, uint64_t active) {
 	uint64_t peers = active;
@@ -183,90 +131,147 @@ __device__ inline uint64_t match_digit(uint32_t d, uint64_t active) {
 	return peers;
 }
 
-__global__ __launch_bounds__(kThreads) void radix_hist_kernel(const uint32_t* __restrict__ keys, int64_t n, int shift,
-															   uint32_t num_blocks, uint32_t* __restrict__ hist) {
-	__shared__ uint32_t s_hist[kRadix];
-	s_hist[threadIdx.x] = 0;
-	__syncthreads();
-	const int64_t base = (int64_t)blockIdx.x * kTileItems;
-	for (int r = 0; r < kItemsPerThread; r++) {
-		const int64_t row = base + (int64_t)r * kThreads;
-		if (row >= n) break;
-		const int64_t i = row + threadIdx.x;
-		const bool valid = i < n;
-		const uint32_t d = valid ? (keys[i] >> shift) & (kRadix - 1) : 0u;
-		const uint64_t peers = match_digit(d, hds_ballot(valid));
-		if (valid && hds_rank_below(peers) == 0) atomicAdd(&s_hist[d], (uint32_t)__popcll(peers));
-	}
-	__syncthreads();
-	hist[(int64_t)threadIdx.x * num_blocks + blockIdx.x] = s_hist[threadIdx.x];
-}
-
-__global__ __launch_bounds__(kThreads) void radix_scatter_kernel(const uint32_t* __restrict__ keys_in,
-																  const uint32_t* __restrict__ vals_in,
-																  uint32_t* __restrict__ keys_out,
-																  uint32_t* __restrict__ vals_out, int64_t n,
-																  int shift, uint32_t num_blocks,
-																  const uint32_t* __restrict__ offsets) {
-	__shared__ uint32_t s_running[kRadix];
-	__shared__ uint32_t s_wave_count[kWaves][kRadix];
-	const int wave = threadIdx.x / HDS_WAVE;
-	s_running[threadIdx.x] = offsets[(int64_t)threadIdx.x * num_blocks + blockIdx.x];
-#pragma unroll
-	for (int w = 0; w < kWaves; w++) s_wave_count[w][threadIdx.x] = 0;
-	__syncthreads();
-	const int64_t base = (int64_t)blockIdx.x * kTileItems;
-	for (int r = 0; r < kItemsPerThread; r++) {
-		const int64_t row = base + (int64_t)r * kThreads;
-		if (row >= n) break;
-		const int64_t i = row + threadIdx.x;
-		const bool valid = i < n;
-		const uint32_t key = valid ? keys_in[i] : 0u;
-		const uint32_t val = valid ? vals_in[i] : 0u;
-		const uint32_t d = (key >> shift) & (kRadix - 1);
-		const uint64_t peers = match_digit(d, hds_ballot(valid));
-		const int rank = hds_rank_below(peers);
-		if (valid && rank == 0) s_wave_count[wave][d] = (uint32_t)__popcll(peers);
-		__syncthreads();
-		if (valid) {
-			uint32_t pos = s_running[d] + (uint32_t)rank;
-			for (int w = 0; w < wave; w++) pos += s_wave_count[w][d];
-			if (keys_out) keys_out[pos] = key;
-			vals_out[pos] = val;
-		}
-		__syncthreads();
-		uint32_t add = 0;
-#pragma unroll
-		for (int w = 0; w < kWaves; w++) {
-			add += s_wave_count[w][threadIdx.x];
-			s_wave_count[w][threadIdx.x] = 0;
-		}
-		s_running[threadIdx.x] += add;
-		__syncthreads();
+// Adds this row's keys (lanes in `active`) to the work-group's LDS digit histograms, one per pass.
+__device__ inline void count_digits(uint32_t key, bool valid, int passes, uint32_t (*s_hist)[kRadix]) {
+	const uint64_t active = hds_ballot(valid);
+	if (active == 0) return;
+	for (int p = 0; p < passes; p++) {
+		const uint32_t d = (key >> (p * kRadixBits)) & (kRadix - 1);
+		const uint64_t peers = match_digit(d, active);
+		if (valid && hds_rank_below(peers) == 0) atomicAdd(&s_hist[p][d], (uint32_t)__popcll(peers));
 	}
 }
 
-// Sorts (keys, vals) on bits [0, bits) through the buffers a (input) and b; returns in *out_a
-// whether the result ended in a (even pass count) or b. keys_final_needed=false lets the last
-// pass skip writing keys.
-int radix_sort(uint32_t* keys_a, uint32_t* vals_a, uint32_t* keys_b, uint32_t* vals_b, int64_t n, int bits,
-			   uint32_t* hist, uint32_t* sums, bool keys_final_needed, hipStream_t s) {
-	const int64_t blocks = tiles_of(n);
-	const int passes = (bits + kRadixBits - 1) / kRadixBits;
+__device__ inline void flush_digits(int passes, uint32_t (*s_hist)[kRadix], uint32_t* __restrict__ hist) {
+	__syncthreads();
+	for (int p = 0; p < passes; p++) {
+		const uint32_t c = s_hist[p][threadIdx.x];
+		if (c) atomicAdd(&hist[p * kRadix + threadIdx.x], c);
+	}
+}
+
+// ---------------------------------------------------------------------------------------------
+// One stable LSD radix pass over 8 bits, single launch.
+// ---------------------------------------------------------------------------------------------
+
+// digit_hist = this pass's global digit counts; status = [partitions][kRadix] look-back words.
+// Item order inside a partition is (wave, row, lane): wave w owns items [w*1024, w*1024 + 1024).
+template <bool kKeysOut>
+__global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __restrict__ keys_in,
+															 const uint32_t* __restrict__ vals_in,
+															 uint32_t* __restrict__ keys_out,
+															 uint32_t* __restrict__ vals_out, int64_t n, int pass,
+															 const uint32_t* __restrict__ digit_hist,
+															 uint64_t* status, uint32_t* ticket, uint32_t* error) {
+	__shared__ uint32_t s_keys[kTileItems];
+	__shared__ uint32_t s_vals[kTileItems];
+	__shared__ uint32_t s_cnt[kWaves][kRadix];  // per-wave running counts, then per-wave offsets
+	__shared__ uint32_t s_local[kRadix];        // first slot of each digit in the partition
+	__shared__ uint32_t s_adj[kRadix];          // output index of slot j of digit d = s_adj[d] + j
+	__shared__ uint32_t s_wave[kWaves];
+	__shared__ int64_t s_part;
+	const int t = threadIdx.x, lane = t & (HDS_WAVE - 1), wave = t / HDS_WAVE;
+	const int shift = pass * kRadixBits;
+#pragma unroll
+	for (int w = 0; w < kWaves; w++) s_cnt[w][t] = 0;
+	const int64_t part = take_ticket(ticket, &s_part);
+	const int64_t base = part * kTileItems;
+	const int64_t wbase = base + (int64_t)wave * kWaveItems;
+
+	uint32_t key[kItemsPerThread], val[kItemsPerThread];
+#pragma unroll
+	for (int r = 0; r < kItemsPerThread; r++) {
+		const int64_t i = wbase + r * HDS_WAVE + lane;
+		key[r] = i < n ? keys_in[i] : 0u;
+		val[r] = i < n ? vals_in[i] : 0u;
+	}
+	// Rank inside the wave: earlier rows' count of the digit (s_cnt, kept by each digit group's
+	// first lane) plus the lanes below with the same digit. A wave's LDS accesses run in order, so
+	// the read of row r + 1 sees the update of row r.
+	uint32_t rank[kItemsPerThread];
+#pragma unroll
+	for (int r = 0; r < kItemsPerThread; r++) {
+		const bool valid = wbase + r * HDS_WAVE + lane < n;
+		const uint32_t d = (key[r] >> shift) & (kRadix - 1);
+		const uint64_t peers = match_digit(d, hds_ballot(valid));
+		const uint32_t below = (uint32_t)hds_rank_below(peers);
+		const uint32_t before = s_cnt[wave][d];
+		rank[r] = before + below;
+		if (valid && below == 0) s_cnt[wave][d] = before + (uint32_t)__popcll(peers);
+	}
+	__syncthreads();
+
+	// Thread t owns digit t: per-wave offsets, the partition's count, publication and look-back.
+	uint32_t count = 0;
+#pragma unroll
+	for (int w = 0; w < kWaves; w++) {
+		const uint32_t c = s_cnt[w][t];
+		s_cnt[w][t] = count;
+		count += c;
+	}
+	uint64_t* mine = status + part * kRadix + t;
+	status_store(mine, status_word(part == 0 ? 2 * pass + 2 : 2 * pass + 1, count));
+	uint32_t unused;
+	const uint32_t digit_start = block_exclusive_scan(digit_hist[t], s_wave, unused);
+	const uint32_t local_start = block_exclusive_scan(count, s_wave, unused);
+	uint64_t before = 0;
+	if (part > 0) {
+		before = lookback(status + t, kRadix, part, (uint32_t)pass, error);
+		status_store(mine, status_word(2 * pass + 2, before + count));
+	}
+	s_local[t] = local_start;
+	s_adj[t] = digit_start + (uint32_t)before - local_start;
+	__syncthreads();
+
+	// Reorder the partition by digit in LDS, then write it out: consecutive threads write
+	// consecutive output positions inside each digit's run.
+#pragma unroll
+	for (int r = 0; r < kItemsPerThread; r++) {
+		if (wbase + r * HDS_WAVE + lane < n) {
+			const uint32_t d = (key[r] >> shift) & (kRadix - 1);
+			const uint32_t slot = s_local[d] + s_cnt[wave][d] + rank[r];
+			s_keys[slot] = key[r];
+			s_vals[slot] = val[r];
+		}
+	}
+	__syncthreads();
+	const int64_t items = n - base < kTileItems ? n - base : kTileItems;
+#pragma unroll
+	for (int r = 0; r < kItemsPerThread; r++) {
+		const int j = r * kThreads + t;
+		if (j < items) {
+			const uint32_t k = s_keys[j];
+			const uint32_t pos = s_adj[(k >> shift) & (kRadix - 1)] + (uint32_t)j;
+			// Always in range when the digit counts are right; the test keeps a failed look-back
+			// (error flag raised) from writing outside the buffers.
+			if (pos < n) {
+				if (kKeysOut) keys_out[pos] = k;
+				vals_out[pos] = s_vals[j];
+			}
+		}
+	}
+}
+
+// Sorts (keys, vals) on `passes` 8-bit digits through the buffers a (input) and b; the result
+// ends in a for an even pass count, else in b. hist holds every pass's digit counts (filled by
+// the producer of the keys); status/tickets are zeroed. Keys of the last pass are written only
+// if keys_final_needed.
+int onesweep_sort(uint32_t* keys_a, uint32_t* vals_a, uint32_t* keys_b, uint32_t* vals_b, int64_t n, int passes,
+				  const uint32_t* hist, uint64_t* status, uint32_t* tickets, uint32_t* error, bool keys_final_needed,
+				  hipStream_t s) {
+	const unsigned parts = (unsigned)parts_of(n);
 	uint32_t *kin = keys_a, *vin = vals_a, *kout = keys_b, *vout = vals_b;
 	for (int p = 0; p < passes; p++) {
-		HdsKernelTimer timer4("radix_hist_kernel", s);
-		radix_hist_kernel<<<(unsigned)blocks, kThreads, 0, s>>>(kin, n, p * kRadixBits, (uint32_t)blocks, hist);
-		timer4.stop();
-		HDS_LAUNCH_CHECK("radix_hist", s);
-		int st = exclusive_scan(hist, nullptr, (int64_t)kRadix * blocks, hist, sums, nullptr, s);
-		if (st != HDS_OK) return st;
-		const bool last = p == passes - 1;
-		HdsKernelTimer timer5("radix_scatter_kernel", s);
-		radix_scatter_kernel<<<(unsigned)blocks, kThreads, 0, s>>>(kin, vin, (last && !keys_final_needed) ? nullptr : kout,
-																   vout, n, p * kRadixBits, (uint32_t)blocks, hist);
-		timer5.stop();
-		HDS_LAUNCH_CHECK("radix_scatter", s);
+		const bool keys_out = p < passes - 1 || keys_final_needed;
+		HdsKernelTimer timer("onesweep_kernel", s);
+		if (keys_out)
+			onesweep_kernel<true><<<parts, kThreads, 0, s>>>(kin, vin, kout, vout, n, p, hist + p * kRadix, status,
+															 tickets + p, error);
+		else
+			onesweep_kernel<false><<<parts, kThreads, 0, s>>>(kin, vin, nullptr, vout, n, p, hist + p * kRadix,
+															  status, tickets + p, error);
+		timer.stop();
+		HDS_LAUNCH_CHECK("onesweep_radix_pass", s);
 		uint32_t* t;
 		t = kin; kin = kout; kout = t;
 		t = vin; vin = vout; vout = t;
@@ -275,44 +280,110 @@ int radix_sort(uint32_t* keys_a, uint32_t* vals_a, uint32_t* keys_b, uint32_t* v
 }
 
 // ---------------------------------------------------------------------------------------------
+// Single-pass exclusive scan: out[i] = sum_{j<i} in[idx[j]]; the grand total goes to *total.
+// ---------------------------------------------------------------------------------------------
+
+__global__ __launch_bounds__(kThreads) void scan_kernel(const uint32_t* __restrict__ in, const uint32_t* __restrict__ idx,
+														 int64_t n, uint32_t* __restrict__ out, uint64_t* status,
+														 uint32_t* ticket, uint32_t* error, uint64_t* __restrict__ total) {
+	// Items go through LDS so that global loads and stores stay coalesced while each thread
+	// scans 16 consecutive items; a pad word every 16 keeps the strided LDS reads conflict-free.
+	__shared__ uint32_t s_items[kTileItems + kTileItems / 16];
+	__shared__ uint32_t s_wave[kWaves];
+	__shared__ uint64_t s_before;
+	__shared__ int64_t s_part;
+	const int64_t part = take_ticket(ticket, &s_part);
+	const int64_t base = part * kTileItems;
+#pragma unroll 4
+	for (int r = 0; r < kItemsPerThread; r++) {
+		const int j = r * kThreads + threadIdx.x;
+		const int64_t i = base + j;
+		s_items[j + j / 16] = i < n ? in[idx ? idx[i] : i] : 0u;
+	}
+	__syncthreads();
+	uint32_t local[kItemsPerThread];
+	uint32_t sum = 0;
+	const int first = threadIdx.x * kItemsPerThread;
+#pragma unroll
+	for (int k = 0; k < kItemsPerThread; k++) {
+		local[k] = sum;
+		sum += s_items[first + k + (first + k) / 16];
+	}
+	uint32_t block_total;
+	const uint32_t before_thread = block_exclusive_scan(sum, s_wave, block_total);
+	if (threadIdx.x == 0) {
+		uint64_t before = 0;
+		if (part == 0) {
+			status_store(status, status_word(2, block_total));
+		} else {
+			status_store(status + part, status_word(1, block_total));
+			before = lookback(status, 1, part, 0, error);
+			status_store(status + part, status_word(2, before + block_total));
+		}
+		if (base + kTileItems >= n) *total = before + block_total;
+		s_before = before;
+	}
+	__syncthreads();
+	const uint32_t offset = (uint32_t)s_before + before_thread;
+#pragma unroll
+	for (int k = 0; k < kItemsPerThread; k++) s_items[first + k + (first + k) / 16] = local[k] + offset;
+	__syncthreads();
+#pragma unroll 4
+	for (int r = 0; r < kItemsPerThread; r++) {
+		const int j = r * kThreads + threadIdx.x;
+		const int64_t i = base + j;
+		if (i < n) out[i] = s_items[j + j / 16];
+	}
+}
+
+// ---------------------------------------------------------------------------------------------
 // Binning kernels.
 // ---------------------------------------------------------------------------------------------
 
-// Cull, tile rectangle, packed records, tile count and depth key per gaussian (forward.cu:13-61).
+// Cull, tile rectangle, packed records, tile count and depth key per gaussian (forward.cu:13-61),
+// plus the depth keys' four digit histograms for the sort.
 __global__ __launch_bounds__(kThreads) void prepare_kernel(
 	int64_t n, const float* __restrict__ means2D, const float* __restrict__ depths, const float* __restrict__ radii,
 	const float* __restrict__ conics, const float* __restrict__ colors, const float* __restrict__ opacities,
 	int tiles_x, int tiles_y, float4* __restrict__ conic4, float4* __restrict__ color_opacity4,
 	uint32_t* __restrict__ counts, uint2* __restrict__ rects, uint32_t* __restrict__ depth_keys,
-	uint32_t* __restrict__ order) {
-	const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-	if (i >= n) return;
-	const float radius = radii[i];
-	const float op = opacities[i];
-	const float a = conics[i * 3], b = conics[i * 3 + 1], c = conics[i * 3 + 2];
-	const float ux = means2D[i * 2], uy = means2D[i * 2 + 1];
-	conic4[i] = make_float4(a, b, c, op);
-	if (colors) color_opacity4[i] = make_float4(colors[i * 3], colors[i * 3 + 1], colors[i * 3 + 2], op);
-	int x0 = 0, y0 = 0, w = 0, h = 0;
-	// !(radius > 0) culls NaN radii too (forward.cu:31-37).
-	const bool ok = radius > 0.0f && hds_tile_rect(ux, uy, a, b, c, op, tiles_x, tiles_y, &x0, &y0, &w, &h);
-	counts[i] = ok ? (uint32_t)(w * h) : 0u;
-	rects[i] = ok ? make_uint2((uint32_t)x0 | ((uint32_t)y0 << 16), (uint32_t)w | ((uint32_t)h << 16)) : make_uint2(0u, 0u);
-	depth_keys[i] = hds_f2u(depths[i]);
-	order[i] = (uint32_t)i;
+	uint32_t* __restrict__ order, uint32_t* __restrict__ hist) {
+	__shared__ uint32_t s_hist[kMaxPasses][kRadix];
+#pragma unroll
+	for (int p = 0; p < kMaxPasses; p++) s_hist[p][threadIdx.x] = 0;
+	__syncthreads();
+	// 4 gaussians per thread keep the work-group count (and the histogram atomics) low while
+	// leaving several waves per SIMD to hide the gathers.
+	constexpr int kPer = 4;
+	for (int r = 0; r < kPer; r++) {
+		const int64_t i = ((int64_t)blockIdx.x * kPer + r) * kThreads + threadIdx.x;
+		const bool valid = i < n;
+		uint32_t key = 0;
+		if (valid) {
+			const float radius = radii[i];
+			const float op = opacities[i];
+			const float a = conics[i * 3], b = conics[i * 3 + 1], c = conics[i * 3 + 2];
+			const float ux = means2D[i * 2], uy = means2D[i * 2 + 1];
+			conic4[i] = make_float4(a, b, c, op);
+			if (colors) color_opacity4[i] = make_float4(colors[i * 3], colors[i * 3 + 1], colors[i * 3 + 2], op);
+			int x0 = 0, y0 = 0, w = 0, h = 0;
+			// !(radius > 0) culls NaN radii too (forward.cu:31-37).
+			const bool ok = radius > 0.0f && hds_tile_rect(ux, uy, a, b, c, op, tiles_x, tiles_y, &x0, &y0, &w, &h);
+			counts[i] = ok ? (uint32_t)(w * h) : 0u;
+			rects[i] = ok ? make_uint2((uint32_t)x0 | ((uint32_t)y0 << 16), (uint32_t)w | ((uint32_t)h << 16))
+						  : make_uint2(0u, 0u);
+			key = hds_f2u(depths[i]);
+			depth_keys[i] = key;
+			order[i] = (uint32_t)i;
+		}
+		count_digits(key, valid, kMaxPasses, s_hist);
+	}
+	flush_digits(kMaxPasses, s_hist, hist);
 }
 
-// One thread per output pair: the owning gaussian is the last depth-ordered entry whose offset is
-// <= the pair index (gaussians with no tiles share their successor's offset and are skipped);
-// tiles are enumerated row-major inside the rectangle (forward.cu:63-113).
-__global__ __launch_bounds__(kThreads) void emit_kernel(int64_t n, int64_t num_pairs, const uint32_t* __restrict__ offsets,
-														 const uint32_t* __restrict__ order,
-														 const uint2* __restrict__ rects, int tiles_x,
-														 uint32_t* __restrict__ tile_keys, uint32_t* __restrict__ gids) {
-	const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-	if (p >= num_pairs) return;
-	const uint32_t target = (uint32_t)p;
-	int64_t lo = 0, hi = n - 1;
+// Last depth-ordered entry in [lo, hi] whose offset is <= target (gaussians with no tiles share
+// their successor's offset, so the owner of a pair is never one of them).
+__device__ inline int64_t owner_of(const uint32_t* __restrict__ offsets, int64_t lo, int64_t hi, uint32_t target) {
 	while (lo < hi) {
 		const int64_t mid = (lo + hi + 1) >> 1;
 		if (offsets[mid] <= target)
@@ -320,45 +391,114 @@ __global__ __launch_bounds__(kThreads) void emit_kernel(int64_t n, int64_t num_p
 		else
 			hi = mid - 1;
 	}
-	const uint32_t gid = order[lo];
-	const uint2 r = rects[gid];
-	const uint32_t x0 = r.x & 0xffffu, y0 = r.x >> 16, w = r.y & 0xffffu;
-	const uint32_t local = target - offsets[lo];
-	const uint32_t ty = y0 + local / w, tx = x0 + local % w;
-	tile_keys[p] = ty * (uint32_t)tiles_x + tx;
-	gids[p] = gid;
+	return lo;
 }
 
-__global__ __launch_bounds__(kThreads) void fill_kernel(uint32_t* __restrict__ out, int64_t count, uint32_t value) {
+// Pairs [4096 b, 4096 b + 4096) per work-group, in depth order; tiles are enumerated row-major
+// inside each gaussian's rectangle (forward.cu:63-113). The owners of a work-group's pairs are a
+// contiguous run of the depth order, so their offsets are cached in LDS for the per-pair search.
+// Also counts the tile keys' digits for the pair sort.
+__global__ __launch_bounds__(kThreads) void emit_kernel(int64_t n, int64_t num_pairs, const uint32_t* __restrict__ offsets,
+														 const uint32_t* __restrict__ order,
+														 const uint2* __restrict__ rects, int tiles_x, int passes,
+														 uint32_t* __restrict__ tile_keys, uint32_t* __restrict__ gids,
+														 uint32_t* __restrict__ hist) {
+	__shared__ uint32_t s_off[kEmitCache];
+	__shared__ uint32_t s_hist[kMaxPasses][kRadix];
+	__shared__ int64_t s_range[2];
+	const int t = threadIdx.x;
+	const int64_t base = (int64_t)blockIdx.x * kTileItems;
+	const int64_t last = (base + kTileItems < num_pairs ? base + kTileItems : num_pairs) - 1;
+	if (t < 2) s_range[t] = owner_of(offsets, 0, n - 1, (uint32_t)(t == 0 ? base : last));
+#pragma unroll
+	for (int p = 0; p < kMaxPasses; p++) s_hist[p][t] = 0;
+	__syncthreads();
+	const int64_t g0 = s_range[0], g1 = s_range[1];
+	const bool cached = g1 - g0 < kEmitCache;
+	if (cached)
+		for (int64_t g = g0 + t; g <= g1; g += kThreads) s_off[g - g0] = offsets[g];
+	__syncthreads();
+	for (int r = 0; r < kItemsPerThread; r++) {
+		const int64_t p = base + r * kThreads + t;
+		const bool valid = p < num_pairs;
+		uint32_t key = 0;
+		if (valid) {
+			const uint32_t target = (uint32_t)p;
+			int64_t g;
+			uint32_t off;
+			if (cached) {
+				int lo = 0, hi = (int)(g1 - g0);
+				while (lo < hi) {
+					const int mid = (lo + hi + 1) >> 1;
+					if (s_off[mid] <= target)
+						lo = mid;
+					else
+						hi = mid - 1;
+				}
+				g = g0 + lo;
+				off = s_off[lo];
+			} else {
+				g = owner_of(offsets, g0, g1, target);
+				off = offsets[g];
+			}
+			const uint32_t gid = order[g];
+			const uint2 rc = rects[gid];
+			const uint32_t x0 = rc.x & 0xffffu, y0 = rc.x >> 16, w = rc.y & 0xffffu;
+			const uint32_t local = target - off;
+			key = (y0 + local / w) * (uint32_t)tiles_x + x0 + local % w;
+			tile_keys[p] = key;
+			gids[p] = gid;
+		}
+		count_digits(key, valid, passes, s_hist);
+	}
+	flush_digits(passes, s_hist, hist);
+}
+
+// Zeroes two word ranges (control words of the sorts, tile ranges) in one launch.
+__global__ __launch_bounds__(kThreads) void zero_kernel(uint32_t* __restrict__ a, int64_t na, uint32_t* __restrict__ b,
+														 int64_t nb) {
 	const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-	if (i < count) out[i] = value;
+	if (i < na)
+		a[i] = 0u;
+	else if (i < na + nb)
+		b[i - na] = 0u;
 }
 
 // [start, end) of each tile in the sorted pair list (forward.cu:115-139).
 __global__ __launch_bounds__(kThreads) void ranges_kernel(int64_t num_pairs, const uint32_t* __restrict__ tile_keys,
-														   int2* __restrict__ ranges) {
+														   int64_t num_tiles, int2* __restrict__ ranges) {
 	const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
 	if (p >= num_pairs) return;
 	const uint32_t t = tile_keys[p];
+	if (t >= num_tiles) return;
 	if (p == 0 || tile_keys[p - 1] != t) ranges[t].x = (int)p;
 	if (p == num_pairs - 1 || tile_keys[p + 1] != t) ranges[t].y = (int)(p + 1);
 }
 
 // ---------------------------------------------------------------------------------------------
-// Workspace layouts. Every region is 256-byte aligned.
+// Workspace layouts. Every region is 256-byte aligned; [ctrl, bytes) is zeroed before use.
 // ---------------------------------------------------------------------------------------------
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// Control block at the start of the zeroed region: the total of the counts scan and the error
+// flag sit together so that hds_bin_count reads both back in one 16-byte copy.
+struct Control {
+	uint64_t total;
+	uint32_t error;
+	uint32_t pad;
+	uint32_t tickets[kMaxPasses + 1];  // one per radix pass, then the scan's
+	uint32_t hist[kMaxPasses * kRadix];
+};
+
 struct GaussianSpace {
-	size_t counts, rects, keys_a, vals_a, keys_b, vals_b, offsets, hist, sums, total, bytes;
+	size_t counts, rects, keys_a, vals_a, keys_b, vals_b, offsets, ctrl, status, scan_status, bytes;
 };
 
 GaussianSpace gaussian_space(int64_t n) {
 	GaussianSpace g;
 	const size_t items = (size_t)(n > 0 ? n : 1);
-	const int64_t blocks = tiles_of(items);
-	const int64_t scan_items = std::max<int64_t>((int64_t)items, (int64_t)kRadix * blocks);
+	const size_t parts = (size_t)parts_of((int64_t)items);
 	size_t o = 0;
 	g.counts = o; o = align256(o + 4 * items);
 	g.rects = o; o = align256(o + 8 * items);
@@ -367,28 +507,27 @@ GaussianSpace gaussian_space(int64_t n) {
 	g.keys_b = o; o = align256(o + 4 * items);
 	g.vals_b = o; o = align256(o + 4 * items);
 	g.offsets = o; o = align256(o + 4 * items);
-	g.hist = o; o = align256(o + 4 * (size_t)kRadix * blocks);
-	g.sums = o; o = align256(o + 4 * (size_t)tiles_of(scan_items));
-	g.total = o; o = align256(o + 8);
+	g.ctrl = o; o = align256(o + sizeof(Control));
+	g.status = o; o = align256(o + 8 * parts * kRadix);
+	g.scan_status = o; o = align256(o + 8 * parts);
 	g.bytes = o;
 	return g;
 }
 
 struct PairSpace {
-	size_t keys_a, keys_b, vals_tmp, hist, sums, bytes;
+	size_t keys_a, keys_b, vals_tmp, ctrl, status, bytes;
 };
 
 PairSpace pair_space(int64_t num_pairs) {
 	PairSpace p;
 	const size_t items = (size_t)(num_pairs > 0 ? num_pairs : 1);
-	const int64_t blocks = tiles_of(items);
-	const int64_t scan_items = std::max<int64_t>((int64_t)items, (int64_t)kRadix * blocks);
+	const size_t parts = (size_t)parts_of((int64_t)items);
 	size_t o = 0;
 	p.keys_a = o; o = align256(o + 4 * items);
 	p.keys_b = o; o = align256(o + 4 * items);
 	p.vals_tmp = o; o = align256(o + 4 * items);
-	p.hist = o; o = align256(o + 4 * (size_t)kRadix * blocks);
-	p.sums = o; o = align256(o + 4 * (size_t)tiles_of(scan_items));
+	p.ctrl = o; o = align256(o + sizeof(Control));
+	p.status = o; o = align256(o + 8 * parts * kRadix);
 	p.bytes = o;
 	return p;
 }
@@ -447,27 +586,42 @@ extern "C" int hds_bin_count(int64_t n, const float* means2D, const float* depth
 	uint32_t* keys_b = at<uint32_t>(workspace, g.keys_b);
 	uint32_t* vals_b = at<uint32_t>(workspace, g.vals_b);
 	uint32_t* offsets = at<uint32_t>(workspace, g.offsets);
-	uint32_t* hist = at<uint32_t>(workspace, g.hist);
-	uint32_t* sums = at<uint32_t>(workspace, g.sums);
-	uint64_t* total = at<uint64_t>(workspace, g.total);
+	Control* ctrl = at<Control>(workspace, g.ctrl);
+	uint64_t* status = at<uint64_t>(workspace, g.status);
+	uint64_t* scan_status = at<uint64_t>(workspace, g.scan_status);
 
-	HdsKernelTimer timer6("prepare_kernel", s);
-	prepare_kernel<<<hds_blocks(n, kThreads), kThreads, 0, s>>>(
+	const int64_t zero_words = (int64_t)(g.bytes - g.ctrl) / 4;
+	HdsKernelTimer timer1("zero_kernel", s);
+	zero_kernel<<<hds_blocks(zero_words, kThreads), kThreads, 0, s>>>(at<uint32_t>(workspace, g.ctrl), zero_words,
+																	   nullptr, 0);
+	timer1.stop();
+	HDS_LAUNCH_CHECK("zero_sort_control", s);
+	HdsKernelTimer timer2("prepare_kernel", s);
+	prepare_kernel<<<hds_blocks(n, 4 * kThreads), kThreads, 0, s>>>(
 		n, means2D, depths, radii, conics, colors, opacities, tiles_x, tiles_y, reinterpret_cast<float4*>(conic4),
-		reinterpret_cast<float4*>(color_opacity4), counts, rects, keys_a, vals_a);
-	timer6.stop();
+		reinterpret_cast<float4*>(color_opacity4), counts, rects, keys_a, vals_a, ctrl->hist);
+	timer2.stop();
 	HDS_LAUNCH_CHECK("prepare_gaussians", s);
 	// 4 passes: the depth order ends back in (keys_a, vals_a).
-	int st = radix_sort(keys_a, vals_a, keys_b, vals_b, n, 32, hist, sums, false, s);
+	int st = onesweep_sort(keys_a, vals_a, keys_b, vals_b, n, kMaxPasses, ctrl->hist, status, ctrl->tickets,
+						   &ctrl->error, false, s);
 	if (st != HDS_OK) return st;
-	st = exclusive_scan(counts, vals_a, n, offsets, sums, total, s);
-	if (st != HDS_OK) return st;
-	uint64_t host_total = 0;
-	HDS_HIP(hipMemcpyAsync(&host_total, total, sizeof(host_total), hipMemcpyDeviceToHost, s));
+	HdsKernelTimer timer3("scan_kernel", s);
+	scan_kernel<<<(unsigned)parts_of(n), kThreads, 0, s>>>(counts, vals_a, n, offsets, scan_status,
+															ctrl->tickets + kMaxPasses, &ctrl->error, &ctrl->total);
+	timer3.stop();
+	HDS_LAUNCH_CHECK("scan_tile_counts", s);
+	struct {
+		uint64_t total;
+		uint32_t error, pad;
+	} host = {0, 0, 0};
+	HDS_HIP(hipMemcpyAsync(&host, ctrl, sizeof(host), hipMemcpyDeviceToHost, s));
 	HDS_HIP(hipStreamSynchronize(s));
-	HDS_REQUIRE(host_total < (uint64_t)INT32_MAX, "bin_count: %llu tile-gaussian pairs overflow int32 indices",
-				(unsigned long long)host_total);
-	*num_pairs = (int64_t)host_total;
+	if (host.error)
+		return hds_set_error(HDS_ERR_RUNTIME, "bin_count: a sort or scan look-back did not complete");
+	HDS_REQUIRE(host.total < (uint64_t)INT32_MAX, "bin_count: %llu tile-gaussian pairs overflow int32 indices",
+				(unsigned long long)host.total);
+	*num_pairs = (int64_t)host.total;
 	return HDS_OK;
 }
 
@@ -481,12 +635,14 @@ extern "C" int hds_bin_emit(int64_t n, int64_t num_pairs, int width, int height,
 	const int tiles_x = (width + HDS_TILE - 1) / HDS_TILE, tiles_y = (height + HDS_TILE - 1) / HDS_TILE;
 	const int64_t num_tiles = (int64_t)tiles_x * tiles_y;
 	hipStream_t s = (hipStream_t)stream;
-	HdsKernelTimer timer7("fill_kernel", s);
-	fill_kernel<<<hds_blocks(2 * num_tiles, kThreads), kThreads, 0, s>>>(reinterpret_cast<uint32_t*>(tile_ranges),
-																		  2 * num_tiles, 0u);
-	timer7.stop();
-	HDS_LAUNCH_CHECK("fill_tile_ranges", s);
-	if (num_pairs == 0) return HDS_OK;
+	uint32_t* ranges_words = reinterpret_cast<uint32_t*>(tile_ranges);
+	if (num_pairs == 0) {
+		HdsKernelTimer timer1("zero_kernel", s);
+		zero_kernel<<<hds_blocks(2 * num_tiles, kThreads), kThreads, 0, s>>>(ranges_words, 2 * num_tiles, nullptr, 0);
+		timer1.stop();
+		HDS_LAUNCH_CHECK("zero_tile_ranges", s);
+		return HDS_OK;
+	}
 	const PairSpace p = pair_space(num_pairs);
 	HDS_REQUIRE(pairs_workspace && pairs_workspace_bytes >= p.bytes, "bin_emit: pairs workspace of %zu bytes, need %zu",
 				pairs_workspace_bytes, p.bytes);
@@ -500,28 +656,34 @@ extern "C" int hds_bin_emit(int64_t n, int64_t num_pairs, int width, int height,
 	uint32_t* keys_a = at<uint32_t>(pairs_workspace, p.keys_a);
 	uint32_t* keys_b = at<uint32_t>(pairs_workspace, p.keys_b);
 	uint32_t* vals_tmp = at<uint32_t>(pairs_workspace, p.vals_tmp);
-	uint32_t* hist = at<uint32_t>(pairs_workspace, p.hist);
-	uint32_t* sums = at<uint32_t>(pairs_workspace, p.sums);
+	Control* ctrl = at<Control>(pairs_workspace, p.ctrl);
+	uint64_t* status = at<uint64_t>(pairs_workspace, p.status);
 	uint32_t* out = reinterpret_cast<uint32_t*>(values_sorted);
 
 	// Pick the ping-pong buffers so the last pass lands in values_sorted.
-	const int bits = tile_bits(num_tiles);
-	const int passes = (bits + kRadixBits - 1) / kRadixBits;
+	const int passes = (tile_bits(num_tiles) + kRadixBits - 1) / kRadixBits;
 	uint32_t* vals_a = (passes % 2 == 0) ? out : vals_tmp;
 	uint32_t* vals_b = (passes % 2 == 0) ? vals_tmp : out;
 
-	HdsKernelTimer timer8("emit_kernel", s);
-	emit_kernel<<<hds_blocks(num_pairs, kThreads), kThreads, 0, s>>>(n, num_pairs, offsets, order, rects, tiles_x,
-																	  keys_a, vals_a);
-	timer8.stop();
+	const int64_t ctrl_words = (int64_t)(p.bytes - p.ctrl) / 4;
+	HdsKernelTimer timer1("zero_kernel", s);
+	zero_kernel<<<hds_blocks(ctrl_words + 2 * num_tiles, kThreads), kThreads, 0, s>>>(
+		at<uint32_t>(pairs_workspace, p.ctrl), ctrl_words, ranges_words, 2 * num_tiles);
+	timer1.stop();
+	HDS_LAUNCH_CHECK("zero_sort_control", s);
+	HdsKernelTimer timer2("emit_kernel", s);
+	emit_kernel<<<(unsigned)parts_of(num_pairs), kThreads, 0, s>>>(n, num_pairs, offsets, order, rects, tiles_x,
+																	passes, keys_a, vals_a, ctrl->hist);
+	timer2.stop();
 	HDS_LAUNCH_CHECK("emit_pairs", s);
-	int st = radix_sort(keys_a, vals_a, keys_b, vals_b, num_pairs, bits, hist, sums, true, s);
+	int st = onesweep_sort(keys_a, vals_a, keys_b, vals_b, num_pairs, passes, ctrl->hist, status, ctrl->tickets,
+						   &ctrl->error, true, s);
 	if (st != HDS_OK) return st;
 	const uint32_t* keys_sorted = (passes % 2 == 0) ? keys_a : keys_b;
-	HdsKernelTimer timer9("ranges_kernel", s);
-	ranges_kernel<<<hds_blocks(num_pairs, kThreads), kThreads, 0, s>>>(num_pairs, keys_sorted,
+	HdsKernelTimer timer3("ranges_kernel", s);
+	ranges_kernel<<<hds_blocks(num_pairs, kThreads), kThreads, 0, s>>>(num_pairs, keys_sorted, num_tiles,
 																		reinterpret_cast<int2*>(tile_ranges));
-	timer9.stop();
+	timer3.stop();
 	HDS_LAUNCH_CHECK("identify_tile_ranges", s);
 	return HDS_OK;
 }
