@@ -33,6 +33,10 @@ constexpr int kRadixBits = 8;
 constexpr int kRadix = 1 << kRadixBits;
 constexpr int kMaxPasses = 4;                           // 32-bit keys
 constexpr int kEmitCache = 4096;                        // depth-ordered offsets one emit work-group caches
+// Copies of each global digit histogram: producers add into copy (block mod kHistCopies), so that
+// no histogram word takes more than ~1/16 of the producers' atomics; passes sum the copies.
+constexpr int kHistCopies = 16;
+constexpr int kHistWords = kHistCopies * kRadix;        // one pass's histogram copies
 // Polls of a silent predecessor before a look-back gives up and raises the error flag (seconds of
 // waiting; reached only if a launch is broken, never by a slow but running predecessor).
 constexpr uint32_t kSpinLimit = 1u << 22;
@@ -60,19 +64,28 @@ __device__ inline void status_store(uint64_t* p, uint64_t v) {
 }
 
 // Sum of the values that partitions [0, part) published in one column (status + p * stride):
-// walks back from part - 1 adding aggregates until an inclusive prefix ends the walk.
+// walks back from part - 1 adding aggregates until an inclusive prefix ends the walk. W words are
+// loaded at a time, so a walk over many aggregates costs one memory latency per W partitions.
+template <int W>
 __device__ inline uint64_t lookback(uint64_t* status, int64_t stride, int64_t part, uint32_t epoch,
 									uint32_t* error) {
 	const uint32_t agg = 2 * epoch + 1, inc = 2 * epoch + 2;
 	uint64_t sum = 0;
 	uint32_t spins = 0;
-	for (int64_t p = part - 1; p >= 0;) {
-		const uint64_t v = status_load(status + p * stride);
-		const uint32_t flag = (uint32_t)(v >> 56);
-		if (flag == inc) return sum + (v & kValueMask);
-		if (flag == agg) {
-			sum += v & kValueMask;
-			p--;
+	int64_t p = part - 1;
+	while (p >= 0) {
+		uint64_t v[W];
+#pragma unroll
+		for (int k = 0; k < W; k++) v[k] = p - k >= 0 ? status_load(status + (p - k) * stride) : status_word(inc, 0);
+		int k = 0;
+		for (; k < W; k++) {
+			const uint32_t flag = (uint32_t)(v[k] >> 56);
+			if (flag == inc) return sum + (v[k] & kValueMask);
+			if (flag != agg) break;
+			sum += v[k] & kValueMask;
+		}
+		p -= k;
+		if (k > 0) {
 			spins = 0;
 			continue;
 		}
@@ -142,11 +155,13 @@ __device__ inline void count_digits(uint32_t key, bool valid, int passes, uint32
 	}
 }
 
+// hist = [pass][kHistCopies][kRadix]; this work-group adds into copy blockIdx.x % kHistCopies.
 __device__ inline void flush_digits(int passes, uint32_t (*s_hist)[kRadix], uint32_t* __restrict__ hist) {
 	__syncthreads();
+	uint32_t* copy = hist + (blockIdx.x % kHistCopies) * kRadix + threadIdx.x;
 	for (int p = 0; p < passes; p++) {
 		const uint32_t c = s_hist[p][threadIdx.x];
-		if (c) atomicAdd(&hist[p * kRadix + threadIdx.x], c);
+		if (c) atomicAdd(copy + p * kHistWords, c);
 	}
 }
 
@@ -154,15 +169,19 @@ __device__ inline void flush_digits(int passes, uint32_t (*s_hist)[kRadix], uint
 // One stable LSD radix pass over 8 bits, single launch.
 // ---------------------------------------------------------------------------------------------
 
-// digit_hist = this pass's global digit counts; status = [partitions][kRadix] look-back words.
-// Item order inside a partition is (wave, row, lane): wave w owns items [w*1024, w*1024 + 1024).
-template <bool kKeysOut>
+// digit_hist = this pass's kHistCopies digit histograms; status = [partitions][kRadix] look-back
+// words. Item order inside a partition is (wave, row, lane): wave w owns items [w*1024, w*1024 +
+// 1024). With kGather, the value is an index and the pass also writes gathered[pos] = table[value]
+// (the depth sort's last pass carries each gaussian's tile rectangle into depth order this way).
+template <bool kKeysOut, bool kGather>
 __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __restrict__ keys_in,
 															 const uint32_t* __restrict__ vals_in,
 															 uint32_t* __restrict__ keys_out,
 															 uint32_t* __restrict__ vals_out, int64_t n, int pass,
 															 const uint32_t* __restrict__ digit_hist,
-															 uint64_t* status, uint32_t* ticket, uint32_t* error) {
+															 uint64_t* status, uint32_t* ticket, uint32_t* error,
+															 const uint2* __restrict__ table,
+															 uint2* __restrict__ gathered) {
 	__shared__ uint32_t s_keys[kTileItems];
 	__shared__ uint32_t s_vals[kTileItems];
 	__shared__ uint32_t s_cnt[kWaves][kRadix];  // per-wave running counts, then per-wave offsets
@@ -211,12 +230,15 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __re
 	}
 	uint64_t* mine = status + part * kRadix + t;
 	status_store(mine, status_word(part == 0 ? 2 * pass + 2 : 2 * pass + 1, count));
+	uint32_t digit_total = 0;
+#pragma unroll
+	for (int c = 0; c < kHistCopies; c++) digit_total += digit_hist[c * kRadix + t];
 	uint32_t unused;
-	const uint32_t digit_start = block_exclusive_scan(digit_hist[t], s_wave, unused);
+	const uint32_t digit_start = block_exclusive_scan(digit_total, s_wave, unused);
 	const uint32_t local_start = block_exclusive_scan(count, s_wave, unused);
 	uint64_t before = 0;
 	if (part > 0) {
-		before = lookback(status + t, kRadix, part, (uint32_t)pass, error);
+		before = lookback<8>(status + t, kRadix, part, (uint32_t)pass, error);
 		status_store(mine, status_word(2 * pass + 2, before + count));
 	}
 	s_local[t] = local_start;
@@ -245,31 +267,38 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __re
 			// Always in range when the digit counts are right; the test keeps a failed look-back
 			// (error flag raised) from writing outside the buffers.
 			if (pos < n) {
+				const uint32_t v = s_vals[j];
 				if (kKeysOut) keys_out[pos] = k;
-				vals_out[pos] = s_vals[j];
+				vals_out[pos] = v;
+				if (kGather) gathered[pos] = table[v];
 			}
 		}
 	}
 }
 
 // Sorts (keys, vals) on `passes` 8-bit digits through the buffers a (input) and b; the result
-// ends in a for an even pass count, else in b. hist holds every pass's digit counts (filled by
+// ends in a for an even pass count, else in b. hist holds every pass's digit histograms (filled by
 // the producer of the keys); status/tickets are zeroed. Keys of the last pass are written only
-// if keys_final_needed.
+// if keys_final_needed; with table, the last pass also writes gathered[i] = table[vals[i]].
 int onesweep_sort(uint32_t* keys_a, uint32_t* vals_a, uint32_t* keys_b, uint32_t* vals_b, int64_t n, int passes,
 				  const uint32_t* hist, uint64_t* status, uint32_t* tickets, uint32_t* error, bool keys_final_needed,
-				  hipStream_t s) {
+				  const uint2* table, uint2* gathered, hipStream_t s) {
 	const unsigned parts = (unsigned)parts_of(n);
 	uint32_t *kin = keys_a, *vin = vals_a, *kout = keys_b, *vout = vals_b;
 	for (int p = 0; p < passes; p++) {
-		const bool keys_out = p < passes - 1 || keys_final_needed;
+		const bool last = p == passes - 1;
+		const bool keys_out = !last || keys_final_needed;
+		const uint32_t* h = hist + p * kHistWords;
 		HdsKernelTimer timer("onesweep_kernel", s);
-		if (keys_out)
-			onesweep_kernel<true><<<parts, kThreads, 0, s>>>(kin, vin, kout, vout, n, p, hist + p * kRadix, status,
-															 tickets + p, error);
+		if (last && table)
+			onesweep_kernel<false, true><<<parts, kThreads, 0, s>>>(kin, vin, nullptr, vout, n, p, h, status,
+																	tickets + p, error, table, gathered);
+		else if (keys_out)
+			onesweep_kernel<true, false><<<parts, kThreads, 0, s>>>(kin, vin, kout, vout, n, p, h, status,
+																	tickets + p, error, nullptr, nullptr);
 		else
-			onesweep_kernel<false><<<parts, kThreads, 0, s>>>(kin, vin, nullptr, vout, n, p, hist + p * kRadix,
-															  status, tickets + p, error);
+			onesweep_kernel<false, false><<<parts, kThreads, 0, s>>>(kin, vin, nullptr, vout, n, p, h, status,
+																	 tickets + p, error, nullptr, nullptr);
 		timer.stop();
 		HDS_LAUNCH_CHECK("onesweep_radix_pass", s);
 		uint32_t* t;
@@ -280,11 +309,12 @@ int onesweep_sort(uint32_t* keys_a, uint32_t* vals_a, uint32_t* keys_b, uint32_t
 }
 
 // ---------------------------------------------------------------------------------------------
-// Single-pass exclusive scan: out[i] = sum_{j<i} in[idx[j]]; the grand total goes to *total.
+// Single-pass exclusive scan of the tile counts (w * h of each rectangle, in depth order):
+// out[i] = sum_{j<i} count[j]; the grand total goes to *total.
 // ---------------------------------------------------------------------------------------------
 
-__global__ __launch_bounds__(kThreads) void scan_kernel(const uint32_t* __restrict__ in, const uint32_t* __restrict__ idx,
-														 int64_t n, uint32_t* __restrict__ out, uint64_t* status,
+__global__ __launch_bounds__(kThreads) void scan_kernel(const uint2* __restrict__ rects, int64_t n,
+														 uint32_t* __restrict__ out, uint64_t* status,
 														 uint32_t* ticket, uint32_t* error, uint64_t* __restrict__ total) {
 	// Items go through LDS so that global loads and stores stay coalesced while each thread
 	// scans 16 consecutive items; a pad word every 16 keeps the strided LDS reads conflict-free.
@@ -298,7 +328,8 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const uint32_t* __restri
 	for (int r = 0; r < kItemsPerThread; r++) {
 		const int j = r * kThreads + threadIdx.x;
 		const int64_t i = base + j;
-		s_items[j + j / 16] = i < n ? in[idx ? idx[i] : i] : 0u;
+		const uint32_t wh = i < n ? rects[i].y : 0u;
+		s_items[j + j / 16] = (wh & 0xffffu) * (wh >> 16);
 	}
 	__syncthreads();
 	uint32_t local[kItemsPerThread];
@@ -317,7 +348,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const uint32_t* __restri
 			status_store(status, status_word(2, block_total));
 		} else {
 			status_store(status + part, status_word(1, block_total));
-			before = lookback(status, 1, part, 0, error);
+			before = lookback<16>(status, 1, part, 0, error);
 			status_store(status + part, status_word(2, before + block_total));
 		}
 		if (base + kTileItems >= n) *total = before + block_total;
@@ -340,13 +371,13 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const uint32_t* __restri
 // Binning kernels.
 // ---------------------------------------------------------------------------------------------
 
-// Cull, tile rectangle, packed records, tile count and depth key per gaussian (forward.cu:13-61),
-// plus the depth keys' four digit histograms for the sort.
+// Cull, tile rectangle (its w * h is the tile count), packed records and depth key per gaussian
+// (forward.cu:13-61), plus the depth keys' four digit histograms for the sort.
 __global__ __launch_bounds__(kThreads) void prepare_kernel(
 	int64_t n, const float* __restrict__ means2D, const float* __restrict__ depths, const float* __restrict__ radii,
 	const float* __restrict__ conics, const float* __restrict__ colors, const float* __restrict__ opacities,
 	int tiles_x, int tiles_y, float4* __restrict__ conic4, float4* __restrict__ color_opacity4,
-	uint32_t* __restrict__ counts, uint2* __restrict__ rects, uint32_t* __restrict__ depth_keys,
+	uint2* __restrict__ rects, uint32_t* __restrict__ depth_keys,
 	uint32_t* __restrict__ order, uint32_t* __restrict__ hist) {
 	__shared__ uint32_t s_hist[kMaxPasses][kRadix];
 #pragma unroll
@@ -355,6 +386,7 @@ __global__ __launch_bounds__(kThreads) void prepare_kernel(
 	// 4 gaussians per thread keep the work-group count (and the histogram atomics) low while
 	// leaving several waves per SIMD to hide the gathers.
 	constexpr int kPer = 4;
+#pragma unroll
 	for (int r = 0; r < kPer; r++) {
 		const int64_t i = ((int64_t)blockIdx.x * kPer + r) * kThreads + threadIdx.x;
 		const bool valid = i < n;
@@ -369,7 +401,6 @@ __global__ __launch_bounds__(kThreads) void prepare_kernel(
 			int x0 = 0, y0 = 0, w = 0, h = 0;
 			// !(radius > 0) culls NaN radii too (forward.cu:31-37).
 			const bool ok = radius > 0.0f && hds_tile_rect(ux, uy, a, b, c, op, tiles_x, tiles_y, &x0, &y0, &w, &h);
-			counts[i] = ok ? (uint32_t)(w * h) : 0u;
 			rects[i] = ok ? make_uint2((uint32_t)x0 | ((uint32_t)y0 << 16), (uint32_t)w | ((uint32_t)h << 16))
 						  : make_uint2(0u, 0u);
 			key = hds_f2u(depths[i]);
@@ -396,13 +427,15 @@ __device__ inline int64_t owner_of(const uint32_t* __restrict__ offsets, int64_t
 
 // Pairs [4096 b, 4096 b + 4096) per work-group, in depth order; tiles are enumerated row-major
 // inside each gaussian's rectangle (forward.cu:63-113). The owners of a work-group's pairs are a
-// contiguous run of the depth order, so their offsets are cached in LDS for the per-pair search.
-// Also counts the tile keys' digits for the pair sort.
+// contiguous run of the depth order, so their offsets are cached in LDS; the 16 rows of a thread
+// go through the owner search, the loads and the stores phase by phase, so each phase has 16
+// independent accesses in flight. Also counts the tile keys' digits for the pair sort.
+// order / rects_sorted: gaussian id and tile rectangle of each depth-ordered entry.
 __global__ __launch_bounds__(kThreads) void emit_kernel(int64_t n, int64_t num_pairs, const uint32_t* __restrict__ offsets,
 														 const uint32_t* __restrict__ order,
-														 const uint2* __restrict__ rects, int tiles_x, int passes,
-														 uint32_t* __restrict__ tile_keys, uint32_t* __restrict__ gids,
-														 uint32_t* __restrict__ hist) {
+														 const uint2* __restrict__ rects_sorted, int tiles_x,
+														 int passes, uint32_t* __restrict__ tile_keys,
+														 uint32_t* __restrict__ gids, uint32_t* __restrict__ hist) {
 	__shared__ uint32_t s_off[kEmitCache];
 	__shared__ uint32_t s_hist[kMaxPasses][kRadix];
 	__shared__ int64_t s_range[2];
@@ -418,36 +451,54 @@ __global__ __launch_bounds__(kThreads) void emit_kernel(int64_t n, int64_t num_p
 	if (cached)
 		for (int64_t g = g0 + t; g <= g1; g += kThreads) s_off[g - g0] = offsets[g];
 	__syncthreads();
+
+	int64_t owner[kItemsPerThread];
+	uint32_t off[kItemsPerThread];
+	if (cached) {
+		// Largest index in [0, g1 - g0] whose cached offset is <= the pair index, 12 fixed steps.
+		const int top = (int)(g1 - g0);
+		int lo[kItemsPerThread];
+#pragma unroll
+		for (int r = 0; r < kItemsPerThread; r++) lo[r] = 0;
+#pragma unroll
+		for (int step = kEmitCache / 2; step > 0; step >>= 1) {
+#pragma unroll
+			for (int r = 0; r < kItemsPerThread; r++) {
+				const uint32_t target = (uint32_t)(base + r * kThreads + t);
+				const int cand = lo[r] + step;
+				if (cand <= top && s_off[cand] <= target) lo[r] = cand;
+			}
+		}
+#pragma unroll
+		for (int r = 0; r < kItemsPerThread; r++) {
+			owner[r] = g0 + lo[r];
+			off[r] = s_off[lo[r]];
+		}
+	} else {
+		for (int r = 0; r < kItemsPerThread; r++) {
+			const int64_t p = base + r * kThreads + t;
+			owner[r] = p < num_pairs ? owner_of(offsets, g0, g1, (uint32_t)p) : g0;
+			off[r] = offsets[owner[r]];
+		}
+	}
+	uint32_t gid[kItemsPerThread];
+	uint2 rc[kItemsPerThread];
+#pragma unroll
+	for (int r = 0; r < kItemsPerThread; r++) {
+		gid[r] = order[owner[r]];
+		rc[r] = rects_sorted[owner[r]];
+	}
+#pragma unroll
 	for (int r = 0; r < kItemsPerThread; r++) {
 		const int64_t p = base + r * kThreads + t;
 		const bool valid = p < num_pairs;
 		uint32_t key = 0;
 		if (valid) {
-			const uint32_t target = (uint32_t)p;
-			int64_t g;
-			uint32_t off;
-			if (cached) {
-				int lo = 0, hi = (int)(g1 - g0);
-				while (lo < hi) {
-					const int mid = (lo + hi + 1) >> 1;
-					if (s_off[mid] <= target)
-						lo = mid;
-					else
-						hi = mid - 1;
-				}
-				g = g0 + lo;
-				off = s_off[lo];
-			} else {
-				g = owner_of(offsets, g0, g1, target);
-				off = offsets[g];
-			}
-			const uint32_t gid = order[g];
-			const uint2 rc = rects[gid];
-			const uint32_t x0 = rc.x & 0xffffu, y0 = rc.x >> 16, w = rc.y & 0xffffu;
-			const uint32_t local = target - off;
+			const uint32_t x0 = rc[r].x & 0xffffu, y0 = rc[r].x >> 16, w = rc[r].y & 0xffffu;
+			const uint32_t local = (uint32_t)p - off[r];
 			key = (y0 + local / w) * (uint32_t)tiles_x + x0 + local % w;
 			tile_keys[p] = key;
-			gids[p] = gid;
+			gids[p] = gid[r];
 		}
 		count_digits(key, valid, passes, s_hist);
 	}
@@ -488,11 +539,11 @@ struct Control {
 	uint32_t error;
 	uint32_t pad;
 	uint32_t tickets[kMaxPasses + 1];  // one per radix pass, then the scan's
-	uint32_t hist[kMaxPasses * kRadix];
+	uint32_t hist[kMaxPasses * kHistWords];
 };
 
 struct GaussianSpace {
-	size_t counts, rects, keys_a, vals_a, keys_b, vals_b, offsets, ctrl, status, scan_status, bytes;
+	size_t rects, rects_sorted, keys_a, vals_a, keys_b, vals_b, offsets, ctrl, status, scan_status, bytes;
 };
 
 GaussianSpace gaussian_space(int64_t n) {
@@ -500,8 +551,8 @@ GaussianSpace gaussian_space(int64_t n) {
 	const size_t items = (size_t)(n > 0 ? n : 1);
 	const size_t parts = (size_t)parts_of((int64_t)items);
 	size_t o = 0;
-	g.counts = o; o = align256(o + 4 * items);
 	g.rects = o; o = align256(o + 8 * items);
+	g.rects_sorted = o; o = align256(o + 8 * items);
 	g.keys_a = o; o = align256(o + 4 * items);
 	g.vals_a = o; o = align256(o + 4 * items);
 	g.keys_b = o; o = align256(o + 4 * items);
@@ -579,8 +630,8 @@ extern "C" int hds_bin_count(int64_t n, const float* means2D, const float* depth
 				"bin_count: conic4 / color_opacity4 must be 16-byte aligned");
 	hipStream_t s = (hipStream_t)stream;
 
-	uint32_t* counts = at<uint32_t>(workspace, g.counts);
 	uint2* rects = at<uint2>(workspace, g.rects);
+	uint2* rects_sorted = at<uint2>(workspace, g.rects_sorted);
 	uint32_t* keys_a = at<uint32_t>(workspace, g.keys_a);
 	uint32_t* vals_a = at<uint32_t>(workspace, g.vals_a);
 	uint32_t* keys_b = at<uint32_t>(workspace, g.keys_b);
@@ -599,15 +650,16 @@ extern "C" int hds_bin_count(int64_t n, const float* means2D, const float* depth
 	HdsKernelTimer timer2("prepare_kernel", s);
 	prepare_kernel<<<hds_blocks(n, 4 * kThreads), kThreads, 0, s>>>(
 		n, means2D, depths, radii, conics, colors, opacities, tiles_x, tiles_y, reinterpret_cast<float4*>(conic4),
-		reinterpret_cast<float4*>(color_opacity4), counts, rects, keys_a, vals_a, ctrl->hist);
+		reinterpret_cast<float4*>(color_opacity4), rects, keys_a, vals_a, ctrl->hist);
 	timer2.stop();
 	HDS_LAUNCH_CHECK("prepare_gaussians", s);
-	// 4 passes: the depth order ends back in (keys_a, vals_a).
+	// 4 passes: the depth order ends back in (keys_a, vals_a); the last one also writes each
+	// entry's tile rectangle to rects_sorted.
 	int st = onesweep_sort(keys_a, vals_a, keys_b, vals_b, n, kMaxPasses, ctrl->hist, status, ctrl->tickets,
-						   &ctrl->error, false, s);
+						   &ctrl->error, false, rects, rects_sorted, s);
 	if (st != HDS_OK) return st;
 	HdsKernelTimer timer3("scan_kernel", s);
-	scan_kernel<<<(unsigned)parts_of(n), kThreads, 0, s>>>(counts, vals_a, n, offsets, scan_status,
+	scan_kernel<<<(unsigned)parts_of(n), kThreads, 0, s>>>(rects_sorted, n, offsets, scan_status,
 															ctrl->tickets + kMaxPasses, &ctrl->error, &ctrl->total);
 	timer3.stop();
 	HDS_LAUNCH_CHECK("scan_tile_counts", s);
@@ -651,7 +703,7 @@ extern "C" int hds_bin_emit(int64_t n, int64_t num_pairs, int width, int height,
 	void* ws = const_cast<void*>(workspace);
 	const uint32_t* offsets = at<uint32_t>(ws, g.offsets);
 	const uint32_t* order = at<uint32_t>(ws, g.vals_a);
-	const uint2* rects = at<uint2>(ws, g.rects);
+	const uint2* rects_sorted = at<uint2>(ws, g.rects_sorted);
 
 	uint32_t* keys_a = at<uint32_t>(pairs_workspace, p.keys_a);
 	uint32_t* keys_b = at<uint32_t>(pairs_workspace, p.keys_b);
@@ -672,12 +724,12 @@ extern "C" int hds_bin_emit(int64_t n, int64_t num_pairs, int width, int height,
 	timer1.stop();
 	HDS_LAUNCH_CHECK("zero_sort_control", s);
 	HdsKernelTimer timer2("emit_kernel", s);
-	emit_kernel<<<(unsigned)parts_of(num_pairs), kThreads, 0, s>>>(n, num_pairs, offsets, order, rects, tiles_x,
+	emit_kernel<<<(unsigned)parts_of(num_pairs), kThreads, 0, s>>>(n, num_pairs, offsets, order, rects_sorted, tiles_x,
 																	passes, keys_a, vals_a, ctrl->hist);
 	timer2.stop();
 	HDS_LAUNCH_CHECK("emit_pairs", s);
 	int st = onesweep_sort(keys_a, vals_a, keys_b, vals_b, num_pairs, passes, ctrl->hist, status, ctrl->tickets,
-						   &ctrl->error, true, s);
+						   &ctrl->error, true, nullptr, nullptr, s);
 	if (st != HDS_OK) return st;
 	const uint32_t* keys_sorted = (passes % 2 == 0) ? keys_a : keys_b;
 	HdsKernelTimer timer3("ranges_kernel", s);

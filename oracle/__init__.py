@@ -155,6 +155,19 @@ def eval_sh_backward_adam(grad_rgb, sh_dc, sh_rest, dirs, degree, radii, m_dc, v
     return grad_dirs
 
 
+def tile_counts(means2D, radii, conics, opacities, width, height):
+    """Per-gaussian tile count and tile rectangle (x0, y0, w, h) of rasterize's binning
+    (forward.cu:13-61), without the pair list. Returns (counts [N] int32, rects [N, 4] int32)."""
+    means2D, radii, conics = _f32(means2D), _f32(radii), _f32(conics)
+    opacities = _f32(opacities).reshape(-1)
+    n = means2D.shape[0]
+    counts = np.zeros(n, np.int32)
+    rects = np.zeros((n, 4), np.int32)
+    _load().orc_bin_count(n, _p(means2D), _p(radii), _p(conics), _p(opacities), width, height, _p(counts),
+                          _p(rects))
+    return counts, rects
+
+
 def bin_gaussians(means2D, depths, radii, conics, opacities, width, height):
     """Binning of rasterize (forward.cu:13-139).
 

@@ -106,9 +106,10 @@ def test_projection_backward_matches_oracle():
 
 # ---- binning ----------------------------------------------------------------------------------
 
-@pytest.mark.parametrize("index,n", [(0, 10_000), (1, 200_000)])
+@pytest.mark.parametrize("index,n", [(0, 10_000), (1, 200_000), (2, None)])
 def test_binning_is_bitwise_equal_to_oracle(index, n):
-    wl = synthetic_config(index, n=n)
+    # (2, None) is the headline scene at full size: 1.18M gaussians, 1.92M pairs, 470 sort partitions.
+    wl = synthetic_config(index, n=n, channels=1)
     (m2, d, r, c), _ = project_both(wl.means, wl.scales, wl.quats, wl.opacities, wl.cam)
     colors = torch.rand(wl.n, 3, generator=torch.Generator().manual_seed(3)).to(DEV)
     values, ranges, conic4, color4 = _get_rasterizer().bin(m2, d, r, c, colors, wl.opacities.to(DEV), wl.width,
@@ -120,6 +121,56 @@ def test_binning_is_bitwise_equal_to_oracle(index, n):
     np.testing.assert_array_equal(np_(ranges), want_ranges)
     np.testing.assert_array_equal(np_(conic4[:, :3]), np_(c))
     np.testing.assert_array_equal(np_(color4), np.concatenate([np_(colors), np_(wl.opacities)], 1))
+
+
+def test_binning_of_the_stress_scene_restricted_to_a_subset_equals_the_oracle():
+    """Config 4 at full size (4M gaussians, 1920x1080, ~94M pairs; too many for the oracle's sort):
+    - every gaussian appears exactly as often as the oracle's tile count says;
+    - tile_ranges cut [0, P) into consecutive runs in tile order, empty tiles (0, 0);
+    - inside a tile, depth bits increase and equal depths keep index order;
+    - the (tile, gaussian) sequence restricted to 20k random gaussians equals the oracle's binning of
+      those gaussians alone: the sort order is a total order on (tile, depth bits, index), so
+      restricting the sorted list and sorting the restricted scene give the same sequence."""
+    wl = synthetic_config(4, channels=1)
+    cam = wl.cam
+    ext = _get_rasterizer()
+    m2, d, r, c = ext.project_gaussians(wl.means.to(DEV), wl.scales.to(DEV), wl.quats.to(DEV),
+                                        wl.opacities.to(DEV), torch.eye(4, device=DEV), cam["fx"], cam["fy"],
+                                        cam["cx"], cam["cy"], wl.width, wl.height, NEAR_PLANE, LOW_PASS,
+                                        JACOBIAN_FOV_SCALE)
+    opac = wl.opacities.to(DEV)
+    values, ranges, _, _ = ext.bin(m2, d, r, c, None, opac, wl.width, wl.height)
+    n, p, t = wl.n, values.numel(), ranges.shape[0]
+    assert p > 50_000_000, p
+    counts, _ = oracle.tile_counts(np_(m2), np_(r), np_(c), np_(opac), wl.width, wl.height)
+    vals = values.long()
+    np.testing.assert_array_equal(np_(torch.bincount(vals, minlength=n)), counts)
+
+    lens = (ranges[:, 1] - ranges[:, 0]).long()
+    full = lens > 0
+    assert (ranges[~full] == 0).all()
+    starts, ends = ranges[full, 0].long(), ranges[full, 1].long()
+    assert int(starts[0]) == 0 and int(ends[-1]) == p and torch.equal(starts[1:], ends[:-1])
+    tile_of = torch.repeat_interleave(torch.arange(t, device=DEV)[full], lens[full])
+    depth_bits = d.view(torch.int32).long()[vals] & 0xFFFFFFFF
+    key = tile_of * (1 << 32) + depth_bits
+    step = key[1:] - key[:-1]
+    assert bool((step >= 0).all())
+    tie = step == 0
+    assert bool((vals[1:][tie] > vals[:-1][tie]).all())
+    del key, step, tie, depth_bits
+
+    subset = np.sort(np.random.default_rng(7).choice(n, 20_000, replace=False))
+    mask = torch.zeros(n, dtype=torch.bool, device=DEV)
+    mask[torch.from_numpy(subset).to(DEV)] = True
+    keep = mask[vals]
+    got_tiles, got_ids = np_(tile_of[keep]), np_(vals[keep])
+    sub = torch.from_numpy(subset).to(DEV)
+    _, want_local, want_ranges = oracle.bin_gaussians(np_(m2[sub]), np_(d[sub]), np_(r[sub]), np_(c[sub]),
+                                                      np_(opac[sub]), wl.width, wl.height)
+    want_tiles = np.repeat(np.arange(t), want_ranges[:, 1] - want_ranges[:, 0])
+    np.testing.assert_array_equal(got_ids, subset[want_local])
+    np.testing.assert_array_equal(got_tiles, want_tiles)
 
 
 def test_binning_keeps_index_order_on_depth_ties():
