@@ -207,16 +207,18 @@ def main() -> int:
             bwd.append(s2.elapsed_time(e2))
         split = {"fwd_ms_median": round(statistics.median(fwd), 4), "bwd_ms_median": round(statistics.median(bwd), 4)}
 
-    # Roofline of the blend backward: its two kernels (back-to-front geometry/colour gradients and
-    # front-to-back feature gradients) are one hds_render_backward call; their HIP-event durations,
-    # recorded per launch inside the library over the timed region, are summed per step.
+    # Roofline of the blend backward: one hds_render_backward_accumulate call runs its two kernels
+    # (back-to-front geometry/colour gradients, front-to-back feature gradients) side by side on two
+    # streams. Its duration is the library stage timer's: HIP events recorded on the caller's stream
+    # right before the call and right after it, i.e. after the join of the second stream, over the
+    # timed region. The per-kernel means (each longer than when run alone) are reported beside it.
     bwd_names = [k for k in ("backward_geometry_kernel", "backward_features_kernel") if k in kernels]
-    bwd_ms = sum(kernels[k]["total_ms"] for k in bwd_names) / args.steps
+    bwd_ms = stages["render_backward"]["mean_ms"]
     achieved = alg["render_backward"] / (bwd_ms * 1e-3) / 1e9
-    roofline = {"kernel": " + ".join(bwd_names) + " (hds_render_backward_accumulate)", "bound": "hbm",
-                "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+    roofline = {"kernel": " + ".join(bwd_names) + " (concurrent, one hds_render_backward_accumulate call)",
+                "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_per_step(bwd_names),
-                "algorithmic_bytes": int(alg["render_backward"]), "ms_per_step": round(bwd_ms, 4),
+                "algorithmic_bytes": int(alg["render_backward"]), "ms_per_call": round(bwd_ms, 4),
                 "kernel_mean_ms": {k: round(kernels[k]["mean_ms"], 4) for k in bwd_names}}
     kernel_report = {k: {"launches_per_step": round(v["launches"] / args.steps, 2), "mean_ms": round(v["mean_ms"], 4)}
                      for k, v in sorted(kernels.items(), key=lambda kv: -kv[1]["total_ms"])}

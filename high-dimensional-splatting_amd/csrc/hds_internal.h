@@ -57,6 +57,9 @@ class HdsKernelTimer {
 	hipStream_t stream_;
 };
 
+/* Sets *out to this device's side stream (see hds_runtime.hip). */
+int hds_side_stream(hipStream_t* out);
+
 static inline unsigned hds_blocks(int64_t n, int threads) { return (unsigned)((n + threads - 1) / threads); }
 
 /* ------------------------------------------------------------------------------------------- */

@@ -26,6 +26,8 @@
 // are written once to LDS as rows per gaussian and read back as the A operand. The result of each
 // lane is 32 consecutive channels of one gaussian, so the atomics are whole cache lines and a
 // gaussian's gradient row sees one atomic per 8x8 block it touches.
+#include <algorithm>
+
 #include "hds_internal.h"
 #include "hds_rasterizer.h"
 #include "hds_stage.h"
@@ -674,20 +676,89 @@ int launch_features(const BackwardArgs& a, int slices, hipStream_t s) {
 	return hds_check_launch("backward_features", s);
 }
 
-__global__ __launch_bounds__(256) void zero_kernel(float* __restrict__ p, int64_t count) {
+// Zeroes up to four float ranges in one launch.
+struct ZeroList {
+	float* p[4];
+	int64_t end[4];  // running sums of the range lengths
+};
+
+__global__ __launch_bounds__(256) void zero_kernel(const ZeroList z) {
 	const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-	if (i < count) p[i] = 0.0f;
+	int64_t begin = 0;
+#pragma unroll
+	for (int k = 0; k < 4; k++) {
+		if (i >= begin && i < z.end[k]) z.p[k][i - begin] = 0.0f;
+		begin = z.end[k];
+	}
 }
 
-int zero(float* p, int64_t count, hipStream_t s) {
+int zero_small(hipStream_t s, float* p0, int64_t n0, float* p1 = nullptr, int64_t n1 = 0, float* p2 = nullptr,
+			   int64_t n2 = 0, float* p3 = nullptr, int64_t n3 = 0);
+
+// Zeroes a large 16-byte aligned range with one 16-byte store per thread and step.
+__global__ __launch_bounds__(256) void zero4_kernel(float4* __restrict__ p, int64_t count4) {
+	const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+	for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count4; i += (int64_t)gridDim.x * blockDim.x)
+		p[i] = z;
+}
+
+int zero_large(hipStream_t s, float* p, int64_t count) {
 	if (!p || count == 0) return HDS_OK;
+	if ((reinterpret_cast<uintptr_t>(p) & 15u) != 0 || count % 4 != 0) return zero_small(s, p, count);
+	const int64_t count4 = count / 4;
+	const int64_t blocks = std::min<int64_t>(hds_blocks(count4, 256), 8192);
+	HdsKernelTimer timer4("zero4_kernel", s);
+	zero4_kernel<<<(unsigned)blocks, 256, 0, s>>>(reinterpret_cast<float4*>(p), count4);
+	timer4.stop();
+	return hds_check_launch("zero_feature_gradients", s);
+}
+
+int zero_small(hipStream_t s, float* p0, int64_t n0, float* p1, int64_t n1, float* p2, int64_t n2, float* p3,
+			   int64_t n3) {
+	ZeroList z{};
+	float* ps[4] = {p0, p1, p2, p3};
+	const int64_t ns[4] = {p0 ? n0 : 0, p1 ? n1 : 0, p2 ? n2 : 0, p3 ? n3 : 0};
+	int64_t total = 0;
+	for (int k = 0; k < 4; k++) {
+		z.p[k] = ps[k];
+		total += ns[k];
+		z.end[k] = total;
+	}
+	if (total == 0) return HDS_OK;
 	HdsKernelTimer timer3("zero_kernel", s);
-	zero_kernel<<<hds_blocks(count, 256), 256, 0, s>>>(p, count);
+	zero_kernel<<<hds_blocks(total, 256), 256, 0, s>>>(z);
 	timer3.stop();
 	return hds_check_launch("zero_gradients", s);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Work on the device's side stream that starts after everything queued on `main` so far
+// (begin) and that `main` waits for before its later work (end). The events are released on
+// every path.
+struct Fork {
+	hipStream_t main = nullptr, side = nullptr;
+	hipEvent_t forked = nullptr, joined = nullptr;
+	int begin(hipStream_t s) {
+		main = s;
+		int st = hds_side_stream(&side);
+		if (st != HDS_OK) return st;
+		HDS_HIP(hipEventCreateWithFlags(&forked, hipEventDisableTiming));
+		HDS_HIP(hipEventCreateWithFlags(&joined, hipEventDisableTiming));
+		HDS_HIP(hipEventRecord(forked, main));
+		HDS_HIP(hipStreamWaitEvent(side, forked, 0));
+		return HDS_OK;
+	}
+	int end() {
+		HDS_HIP(hipEventRecord(joined, side));
+		HDS_HIP(hipStreamWaitEvent(main, joined, 0));
+		return HDS_OK;
+	}
+	~Fork() {
+		if (forked) (void)hipEventDestroy(forked);
+		if (joined) (void)hipEventDestroy(joined);
+	}
+};
 
 int render_backward(bool zero_outputs, int64_t n, int width, int height, int channels, int slice_width,
 								   const int32_t* tile_ranges, const int32_t* values_sorted, int64_t num_pairs,
@@ -715,15 +786,15 @@ int render_backward(bool zero_outputs, int64_t n, int width, int height, int cha
 	}
 	HDS_REQUIRE(aligned16(conic4) && (!color_opacity4 || aligned16(color_opacity4)), "render_backward: misaligned conic4");
 	hipStream_t s = (hipStream_t)stream;
+	// The gradients are accumulated with atomics; the zeroing variant clears them first.
+	const bool run = n > 0 && num_pairs > 0;
 	if (zero_outputs) {
-		int st;
-		if ((st = zero(grad_means2D, 2 * n, s)) != HDS_OK) return st;
-		if ((st = zero(grad_conics, 3 * n, s)) != HDS_OK) return st;
-		if ((st = zero(grad_opacities, n, s)) != HDS_OK) return st;
-		if (grad_colors && (st = zero(grad_colors, 3 * n, s)) != HDS_OK) return st;
-		if (feats && grad_features && (st = zero(grad_features, (int64_t)channels * n, s)) != HDS_OK) return st;
+		int st = zero_small(s, grad_means2D, 2 * n, grad_conics, 3 * n, grad_opacities, n, grad_colors, 3 * n);
+		if (st != HDS_OK) return st;
+		// Before the fork: zeroing beside the running geometry kernel starves the fill of CUs.
+		if (feats && grad_features && (st = zero_large(s, grad_features, (int64_t)channels * n)) != HDS_OK) return st;
 	}
-	if (n == 0 || num_pairs == 0) return HDS_OK;
+	if (!run) return HDS_OK;
 
 	const int tiles_x = (width + HDS_TILE - 1) / HDS_TILE, tiles_y = (height + HDS_TILE - 1) / HDS_TILE;
 	const int num_tiles = tiles_x * tiles_y;
@@ -750,18 +821,28 @@ int render_backward(bool zero_outputs, int64_t n, int width, int height, int cha
 				   feats ? grad_features : nullptr};
 	if (!feats) return launch_geometry<0, true>(a, 1, s);
 	const int slices = channels / slice_width;
+	// The feature-gradient kernel runs beside the geometry kernel, on a second stream forked from
+	// and joined back into the caller's: much of its time goes to HBM-bound gradient atomics, while
+	// the geometry kernel is bound by VALU issue and LDS latency, so the two overlap well.
+	Fork fork;
+	if (grad_features) {
+		int st = fork.begin(s);
+		if (st != HDS_OK) return st;
+		switch (slice_width) {
+			case 32: st = launch_features<32>(a, slices, fork.side); break;
+			case 64: st = launch_features<64>(a, slices, fork.side); break;
+			default: st = launch_features<128>(a, slices, fork.side); break;
+		}
+		if (st != HDS_OK) return st;
+	}
 	int st;
 	switch (slice_width) {
 		case 32: st = rgb ? launch_geometry<32, true>(a, slices, s) : launch_geometry<32, false>(a, slices, s); break;
 		case 64: st = rgb ? launch_geometry<64, true>(a, slices, s) : launch_geometry<64, false>(a, slices, s); break;
 		default: st = rgb ? launch_geometry<128, true>(a, slices, s) : launch_geometry<128, false>(a, slices, s); break;
 	}
-	if (st != HDS_OK || !grad_features) return st;
-	switch (slice_width) {
-		case 32: return launch_features<32>(a, slices, s);
-		case 64: return launch_features<64>(a, slices, s);
-		default: return launch_features<128>(a, slices, s);
-	}
+	const int joined = grad_features ? fork.end() : HDS_OK;
+	return st != HDS_OK ? st : joined;
 }
 
 }  // namespace

@@ -38,6 +38,20 @@ int hds_check_launch(const char* kernel, hipStream_t stream) {
 	return HDS_OK;
 }
 
+// A second stream per device for kernels that run beside the caller's stream (default priority,
+// non-blocking, created on first use and kept until the process ends).
+int hds_side_stream(hipStream_t* out) {
+	static std::mutex mutex;
+	static std::vector<hipStream_t> streams;
+	int device = 0;
+	HDS_HIP(hipGetDevice(&device));
+	std::lock_guard<std::mutex> lock(mutex);
+	if ((int)streams.size() <= device) streams.resize(device + 1, nullptr);
+	if (!streams[device]) HDS_HIP(hipStreamCreateWithFlags(&streams[device], hipStreamNonBlocking));
+	*out = streams[device];
+	return HDS_OK;
+}
+
 extern "C" const char* hds_last_error(void) { return g_last_error; }
 
 extern "C" int hds_abi_version(void) { return HDS_ABI_VERSION; }

@@ -326,15 +326,15 @@ class HipRasterizer:
             grad_image = _dev(grad_image, "grad_image")
             if background is None:
                 background = torch.zeros(3, device=dev, dtype=torch.float32)
-        # The walk accumulates with atomics into zeroed buffers.
+        # hds_render_backward zeroes the outputs itself before its atomics add into them.
         f32 = dict(device=dev, dtype=torch.float32)
-        g_means = torch.zeros((n, 2), **f32)
-        g_conics = torch.zeros((n, 3), **f32)
-        g_colors = torch.zeros((n, 3), **f32) if grad_image is not None else None
-        g_opac = torch.zeros((n, 1), **f32)
-        g_feat = torch.zeros((n, channels), **f32) if features is not None and want_feature_grad else None
+        g_means = torch.empty((n, 2), **f32)
+        g_conics = torch.empty((n, 3), **f32)
+        g_colors = torch.empty((n, 3), **f32) if grad_image is not None else None
+        g_opac = torch.empty((n, 1), **f32)
+        g_feat = torch.empty((n, channels), **f32) if features is not None and want_feature_grad else None
         with torch.cuda.device(dev):
-            self._run("render_backward", lambda: self.lib.hds_render_backward_accumulate(
+            self._run("render_backward", lambda: self.lib.hds_render_backward(
                 n, int(width), int(height), channels, slice_width or 0, _ptr(tile_ranges), _ptr(values_sorted),
                 values_sorted.numel(), _ptr(_dev(means2D, "means2D")), _ptr(conic4), _ptr(color_opacity4),
                 _ptr(background), _ptr(final_T), _ptr(n_contrib), _ptr(grad_image), _ptr(features),

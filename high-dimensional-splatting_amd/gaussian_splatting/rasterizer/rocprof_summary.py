@@ -34,7 +34,29 @@ def trace(directory: Path, top: int) -> str:
         out.append(f"| {short_name(r['Name'])} | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
                    f"{float(r['TotalDurationNs']) / 1e6:.3f} | {100 * float(r['TotalDurationNs']) / total:.2f} |")
     out.append(f"\nAll kernels: {total / 1e6:.3f} ms.")
+    spans = concurrent_spans(directory, "backward_geometry_kernel", "backward_features_kernel")
+    if spans:
+        out.append(f"\nbackward_geometry_kernel and backward_features_kernel run side by side: over {len(spans)} "
+                   f"calls, first start to last end averages {sum(spans) / len(spans) / 1e3:.1f} us.")
     return "\n".join(out)
+
+
+def concurrent_spans(directory: Path, first: str, second: str) -> list[int]:
+    """Per call, the time from the earlier start to the later end of two kernels launched together
+    (each dispatch of `first` paired with the `second` dispatch that starts nearest to it), in ns."""
+    files = list(directory.glob("*kernel_trace.csv"))
+    if not files:
+        return []
+    rows = list(csv.DictReader(open(files[0])))
+    a = [(int(r["Start_Timestamp"]), int(r["End_Timestamp"])) for r in rows if short_name(r["Kernel_Name"]) == first]
+    b = [(int(r["Start_Timestamp"]), int(r["End_Timestamp"])) for r in rows if short_name(r["Kernel_Name"]) == second]
+    spans = []
+    for s0, e0 in a:
+        if not b:
+            break
+        s1, e1 = min(b, key=lambda se: abs(se[0] - s0))
+        spans.append(max(e0, e1) - min(s0, s1))
+    return spans
 
 
 def _counter_values(directory: Path, counter: str) -> dict[str, list[float]]:
