@@ -425,6 +425,27 @@ __device__ inline int64_t owner_of(const uint32_t* __restrict__ offsets, int64_t
 	return lo;
 }
 
+// owner_of over the whole depth order, by one wave: each round the 64 lanes probe 64 evenly spaced
+// entries of the remaining range [lo, hi] and keep the last one whose offset is <= target, so the
+// range shrinks 64-fold per memory latency (4 rounds for a million gaussians instead of 21
+// dependent loads). offsets[0] = 0 <= target keeps lane 0's probe valid.
+__device__ inline int64_t wave_owner_of(const uint32_t* __restrict__ offsets, int64_t n, uint32_t target) {
+	const int lane = threadIdx.x & (HDS_WAVE - 1);
+	int64_t lo = 0, hi = n - 1;
+	while (hi - lo >= HDS_WAVE) {
+		const int64_t step = (hi - lo + HDS_WAVE) / HDS_WAVE;  // 64 probes cover [lo, hi]
+		const int64_t idx = lo + lane * step;
+		const uint64_t ok = hds_ballot(idx <= hi && offsets[idx <= hi ? idx : hi] <= target);
+		const int64_t found = lo + (int64_t)(63 - __builtin_clzll(ok)) * step;
+		// The owner lies before the next probe, which failed or lies past hi.
+		hi = found + step - 1 < hi ? found + step - 1 : hi;
+		lo = found;
+	}
+	const int64_t idx = lo + lane;
+	const uint64_t ok = hds_ballot(idx <= hi && offsets[idx <= hi ? idx : hi] <= target);
+	return lo + (63 - __builtin_clzll(ok));
+}
+
 // Pairs [4096 b, 4096 b + 4096) per work-group, in depth order; tiles are enumerated row-major
 // inside each gaussian's rectangle (forward.cu:63-113). The owners of a work-group's pairs are a
 // contiguous run of the depth order, so their offsets are cached in LDS; the 16 rows of a thread
@@ -442,7 +463,10 @@ __global__ __launch_bounds__(kThreads) void emit_kernel(int64_t n, int64_t num_p
 	const int t = threadIdx.x;
 	const int64_t base = (int64_t)blockIdx.x * kTileItems;
 	const int64_t last = (base + kTileItems < num_pairs ? base + kTileItems : num_pairs) - 1;
-	if (t < 2) s_range[t] = owner_of(offsets, 0, n - 1, (uint32_t)(t == 0 ? base : last));
+	if (t < 2 * HDS_WAVE) {
+		const int64_t g = wave_owner_of(offsets, n, (uint32_t)(t < HDS_WAVE ? base : last));
+		if ((t & (HDS_WAVE - 1)) == 0) s_range[t / HDS_WAVE] = g;
+	}
 #pragma unroll
 	for (int p = 0; p < kMaxPasses; p++) s_hist[p][t] = 0;
 	__syncthreads();

@@ -117,3 +117,13 @@ extern "C" int hds_profile_record(int64_t i, const char** name, float* ms) {
 	HDS_HIP(hipEventElapsedTime(ms, g_profile[i].start, g_profile[i].stop));
 	return HDS_OK;
 }
+
+extern "C" int hds_profile_timeline(int64_t i, const char** name, float* start_ms, float* end_ms) {
+	std::lock_guard<std::mutex> lock(g_profile_mutex);
+	HDS_REQUIRE(i >= 0 && i < g_profile_used && name && start_ms && end_ms, "hds_profile_timeline: no record %lld",
+				(long long)i);
+	*name = g_profile[i].name;
+	HDS_HIP(hipEventElapsedTime(start_ms, g_profile[0].start, g_profile[i].start));
+	HDS_HIP(hipEventElapsedTime(end_ms, g_profile[0].start, g_profile[i].stop));
+	return HDS_OK;
+}

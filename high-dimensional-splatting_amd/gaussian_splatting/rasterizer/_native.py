@@ -53,6 +53,8 @@ PROTOTYPES = {
     "hds_profile_begin": (_i32, []),
     "hds_profile_end": (_i64, []),
     "hds_profile_record": (_i32, [_i64, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_float)]),
+    "hds_profile_timeline": (_i32, [_i64, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_float),
+                                    ctypes.POINTER(ctypes.c_float)]),
 }
 
 _lib: ctypes.CDLL | None = None
@@ -90,6 +92,7 @@ class KernelProfile:
 
     def __init__(self):
         self.records: list[tuple[str, float]] = []
+        self.timeline: list[tuple[str, float, float]] = []  # (kernel, start ms, end ms) from the first start
 
     def __enter__(self):
         _check(load_library().hds_profile_begin())
@@ -100,10 +103,12 @@ class KernelProfile:
         count = lib.hds_profile_end()
         if count < 0:
             _check(-count)
-        name, ms = ctypes.c_char_p(), ctypes.c_float()
+        name, ms, t0, t1 = ctypes.c_char_p(), ctypes.c_float(), ctypes.c_float(), ctypes.c_float()
         for i in range(count):
             _check(lib.hds_profile_record(i, ctypes.byref(name), ctypes.byref(ms)))
             self.records.append((name.value.decode(), float(ms.value)))
+            _check(lib.hds_profile_timeline(i, ctypes.byref(name), ctypes.byref(t0), ctypes.byref(t1)))
+            self.timeline.append((name.value.decode(), float(t0.value), float(t1.value)))
         return False
 
     def summary(self) -> dict[str, dict[str, float]]:

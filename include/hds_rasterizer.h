@@ -171,6 +171,9 @@ HDS_API int64_t hds_profile_end(void);
 /* Kernel name and duration in ms of record i (0 <= i < the count hds_profile_end returned). */
 HDS_API int hds_profile_record(int64_t i, const char** name, float* ms);
 
+/* Kernel name, start and end in ms of record i, relative to the start of record 0. */
+HDS_API int hds_profile_timeline(int64_t i, const char** name, float* start_ms, float* end_ms);
+
 #ifdef __cplusplus
 }
 #endif

@@ -68,9 +68,11 @@ def test_kernel_profile_records_nothing_without_launches(lib):
 
     with KernelProfile() as prof:
         pass
-    assert prof.records == [] and prof.summary() == {}
-    name, ms = ctypes.c_char_p(), ctypes.c_float()
+    assert prof.records == [] and prof.timeline == [] and prof.summary() == {}
+    name, ms, end = ctypes.c_char_p(), ctypes.c_float(), ctypes.c_float()
     assert lib.hds_profile_record(0, ctypes.byref(name), ctypes.byref(ms)) != 0
+    assert b"no record 0" in lib.hds_last_error()
+    assert lib.hds_profile_timeline(0, ctypes.byref(name), ctypes.byref(ms), ctypes.byref(end)) != 0
     assert b"no record 0" in lib.hds_last_error()
 
 
