@@ -194,6 +194,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S >= 128 ? 
 					float w[kGroup];
 #pragma unroll
 					for (int q0 = 0; q0 < kGroup; q0 += kIlp) {
+						if (q0 >= count) {
+							// Past the group's last hit (wave-uniform): nothing to evaluate.
+#pragma unroll
+							for (int u = 0; u < kIlp; u++) w[q0 + u] = 0.0f;
+							continue;
+						}
 						float alpha[kIlp];
 						float4 col[kIlp];
 #pragma unroll
