@@ -43,7 +43,17 @@ constexpr uint32_t kSpinLimit = 1u << 22;
 
 static_assert(kRadix == kThreads, "one thread per radix bin");
 
-inline int64_t parts_of(int64_t n) { return (n + kTileItems - 1) / kTileItems; }
+__host__ __device__ inline int64_t parts_of(int64_t n) { return (n + kTileItems - 1) / kTileItems; }
+
+// Item count of a launch sized on the host for `cap` items whose actual count sits in device
+// memory: min(*total, cap), or 0 when the error word that follows *total is set (a failed
+// look-back upstream leaves nothing trustworthy to emit). A null total means cap is exact.
+__device__ inline int64_t device_count(const uint64_t* total, int64_t cap) {
+	if (!total) return cap;
+	if (reinterpret_cast<const uint32_t*>(total + 1)[0] != 0u) return 0;
+	const uint64_t t = *total;
+	return t < (uint64_t)cap ? (int64_t)t : cap;
+}
 
 // ---------------------------------------------------------------------------------------------
 // Decoupled look-back. A status word is (flag << 56 | value): flag 2e+1 = the partition's own
@@ -177,7 +187,8 @@ template <bool kKeysOut, bool kGather>
 __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __restrict__ keys_in,
 															 const uint32_t* __restrict__ vals_in,
 															 uint32_t* __restrict__ keys_out,
-															 uint32_t* __restrict__ vals_out, int64_t n, int pass,
+															 uint32_t* __restrict__ vals_out, int64_t n,
+															 const uint64_t* __restrict__ n_total, int pass,
 															 const uint32_t* __restrict__ digit_hist,
 															 uint64_t* status, uint32_t* ticket, uint32_t* error,
 															 const uint2* __restrict__ table,
@@ -194,6 +205,10 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __re
 #pragma unroll
 	for (int w = 0; w < kWaves; w++) s_cnt[w][t] = 0;
 	const int64_t part = take_ticket(ticket, &s_part);
+	// Launched for n items; with n_total the count is read here, and tickets past its last
+	// partition leave at once (every partition the look-back waits for has a lower ticket).
+	n = device_count(n_total, n);
+	if (part >= parts_of(n)) return;
 	const int64_t base = part * kTileItems;
 	const int64_t wbase = base + (int64_t)wave * kWaveItems;
 
@@ -277,11 +292,11 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __re
 }
 
 // Sorts (keys, vals) on `passes` 8-bit digits through the buffers a (input) and b; the result
-// ends in a for an even pass count, else in b. hist holds every pass's digit histograms (filled by
+// ends in a for an even pass count, else in b. n items, or device_count(n_total, n) with n_total. hist holds every pass's digit histograms (filled by
 // the producer of the keys); status/tickets are zeroed. Keys of the last pass are written only
 // if keys_final_needed; with table, the last pass also writes gathered[i] = table[vals[i]].
-int onesweep_sort(uint32_t* keys_a, uint32_t* vals_a, uint32_t* keys_b, uint32_t* vals_b, int64_t n, int passes,
-				  const uint32_t* hist, uint64_t* status, uint32_t* tickets, uint32_t* error, bool keys_final_needed,
+int onesweep_sort(uint32_t* keys_a, uint32_t* vals_a, uint32_t* keys_b, uint32_t* vals_b, int64_t n,
+				  const uint64_t* n_total, int passes, const uint32_t* hist, uint64_t* status, uint32_t* tickets, uint32_t* error, bool keys_final_needed,
 				  const uint2* table, uint2* gathered, hipStream_t s) {
 	const unsigned parts = (unsigned)parts_of(n);
 	uint32_t *kin = keys_a, *vin = vals_a, *kout = keys_b, *vout = vals_b;
@@ -291,13 +306,13 @@ int onesweep_sort(uint32_t* keys_a, uint32_t* vals_a, uint32_t* keys_b, uint32_t
 		const uint32_t* h = hist + p * kHistWords;
 		HdsKernelTimer timer("onesweep_kernel", s);
 		if (last && table)
-			onesweep_kernel<false, true><<<parts, kThreads, 0, s>>>(kin, vin, nullptr, vout, n, p, h, status,
+			onesweep_kernel<false, true><<<parts, kThreads, 0, s>>>(kin, vin, nullptr, vout, n, n_total, p, h, status,
 																	tickets + p, error, table, gathered);
 		else if (keys_out)
-			onesweep_kernel<true, false><<<parts, kThreads, 0, s>>>(kin, vin, kout, vout, n, p, h, status,
+			onesweep_kernel<true, false><<<parts, kThreads, 0, s>>>(kin, vin, kout, vout, n, n_total, p, h, status,
 																	tickets + p, error, nullptr, nullptr);
 		else
-			onesweep_kernel<false, false><<<parts, kThreads, 0, s>>>(kin, vin, nullptr, vout, n, p, h, status,
+			onesweep_kernel<false, false><<<parts, kThreads, 0, s>>>(kin, vin, nullptr, vout, n, n_total, p, h, status,
 																	 tickets + p, error, nullptr, nullptr);
 		timer.stop();
 		HDS_LAUNCH_CHECK("onesweep_radix_pass", s);
@@ -451,8 +466,10 @@ __device__ inline int64_t wave_owner_of(const uint32_t* __restrict__ offsets, in
 // contiguous run of the depth order, so their offsets are cached in LDS; the 16 rows of a thread
 // go through the owner search, the loads and the stores phase by phase, so each phase has 16
 // independent accesses in flight. Also counts the tile keys' digits for the pair sort.
-// order / rects_sorted: gaussian id and tile rectangle of each depth-ordered entry.
-__global__ __launch_bounds__(kThreads) void emit_kernel(int64_t n, int64_t num_pairs, const uint32_t* __restrict__ offsets,
+// order / rects_sorted: gaussian id and tile rectangle of each depth-ordered entry. With
+// pairs_total the grid covers num_pairs pairs and the count is read on the device.
+__global__ __launch_bounds__(kThreads) void emit_kernel(int64_t n, int64_t num_pairs, const uint64_t* __restrict__ pairs_total,
+														 const uint32_t* __restrict__ offsets,
 														 const uint32_t* __restrict__ order,
 														 const uint2* __restrict__ rects_sorted, int tiles_x,
 														 int passes, uint32_t* __restrict__ tile_keys,
@@ -462,6 +479,8 @@ __global__ __launch_bounds__(kThreads) void emit_kernel(int64_t n, int64_t num_p
 	__shared__ int64_t s_range[2];
 	const int t = threadIdx.x;
 	const int64_t base = (int64_t)blockIdx.x * kTileItems;
+	num_pairs = device_count(pairs_total, num_pairs);
+	if (base >= num_pairs) return;
 	const int64_t last = (base + kTileItems < num_pairs ? base + kTileItems : num_pairs) - 1;
 	if (t < 2 * HDS_WAVE) {
 		const int64_t g = wave_owner_of(offsets, n, (uint32_t)(t < HDS_WAVE ? base : last));
@@ -540,9 +559,11 @@ __global__ __launch_bounds__(kThreads) void zero_kernel(uint32_t* __restrict__ a
 }
 
 // [start, end) of each tile in the sorted pair list (forward.cu:115-139).
-__global__ __launch_bounds__(kThreads) void ranges_kernel(int64_t num_pairs, const uint32_t* __restrict__ tile_keys,
-														   int64_t num_tiles, int2* __restrict__ ranges) {
+__global__ __launch_bounds__(kThreads) void ranges_kernel(int64_t num_pairs, const uint64_t* __restrict__ pairs_total,
+														   const uint32_t* __restrict__ tile_keys, int64_t num_tiles,
+														   int2* __restrict__ ranges) {
 	const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+	num_pairs = device_count(pairs_total, num_pairs);
 	if (p >= num_pairs) return;
 	const uint32_t t = tile_keys[p];
 	if (t >= num_tiles) return;
@@ -634,12 +655,15 @@ extern "C" size_t hds_pairs_workspace_bytes(int64_t num_pairs, int width, int he
 	return pair_space(num_pairs).bytes;
 }
 
-extern "C" int hds_bin_count(int64_t n, const float* means2D, const float* depths, const float* radii,
-							 const float* conics, const float* colors, const float* opacities, int width, int height,
-							 float* conic4, float* color_opacity4, void* workspace, size_t workspace_bytes,
-							 int64_t* num_pairs, hds_stream_t stream) {
-	HDS_REQUIRE(num_pairs, "bin_count: num_pairs must not be NULL");
-	*num_pairs = 0;
+namespace {
+
+// Enqueues the counting half of the binning (cull, records, depth order, scan of the tile counts);
+// the pair count and the look-back error flag end in the workspace's control block. *launched is
+// false when there was nothing to enqueue (n == 0).
+int bin_count_launch(int64_t n, const float* means2D, const float* depths, const float* radii, const float* conics,
+					 const float* colors, const float* opacities, int width, int height, float* conic4,
+					 float* color_opacity4, void* workspace, size_t workspace_bytes, hipStream_t s, bool* launched) {
+	*launched = false;
 	HDS_REQUIRE(n >= 0 && n < INT32_MAX, "bin_count: gaussian count %lld outside [0, 2^31)", (long long)n);
 	HDS_REQUIRE(width > 0 && height > 0, "bin_count: image size %dx%d must be positive", width, height);
 	const int tiles_x = (width + HDS_TILE - 1) / HDS_TILE, tiles_y = (height + HDS_TILE - 1) / HDS_TILE;
@@ -652,7 +676,6 @@ extern "C" int hds_bin_count(int64_t n, const float* means2D, const float* depth
 	HDS_REQUIRE(colors == nullptr || color_opacity4 != nullptr, "bin_count: colors given without color_opacity4");
 	HDS_REQUIRE(aligned16(conic4) && (!color_opacity4 || aligned16(color_opacity4)),
 				"bin_count: conic4 / color_opacity4 must be 16-byte aligned");
-	hipStream_t s = (hipStream_t)stream;
 
 	uint2* rects = at<uint2>(workspace, g.rects);
 	uint2* rects_sorted = at<uint2>(workspace, g.rects_sorted);
@@ -679,7 +702,7 @@ extern "C" int hds_bin_count(int64_t n, const float* means2D, const float* depth
 	HDS_LAUNCH_CHECK("prepare_gaussians", s);
 	// 4 passes: the depth order ends back in (keys_a, vals_a); the last one also writes each
 	// entry's tile rectangle to rects_sorted.
-	int st = onesweep_sort(keys_a, vals_a, keys_b, vals_b, n, kMaxPasses, ctrl->hist, status, ctrl->tickets,
+	int st = onesweep_sort(keys_a, vals_a, keys_b, vals_b, n, nullptr, kMaxPasses, ctrl->hist, status, ctrl->tickets,
 						   &ctrl->error, false, rects, rects_sorted, s);
 	if (st != HDS_OK) return st;
 	HdsKernelTimer timer3("scan_kernel", s);
@@ -687,32 +710,33 @@ extern "C" int hds_bin_count(int64_t n, const float* means2D, const float* depth
 															ctrl->tickets + kMaxPasses, &ctrl->error, &ctrl->total);
 	timer3.stop();
 	HDS_LAUNCH_CHECK("scan_tile_counts", s);
-	struct {
-		uint64_t total;
-		uint32_t error, pad;
-	} host = {0, 0, 0};
-	HDS_HIP(hipMemcpyAsync(&host, ctrl, sizeof(host), hipMemcpyDeviceToHost, s));
-	HDS_HIP(hipStreamSynchronize(s));
-	if (host.error)
-		return hds_set_error(HDS_ERR_RUNTIME, "bin_count: a sort or scan look-back did not complete");
-	HDS_REQUIRE(host.total < (uint64_t)INT32_MAX, "bin_count: %llu tile-gaussian pairs overflow int32 indices",
-				(unsigned long long)host.total);
-	*num_pairs = (int64_t)host.total;
+	*launched = true;
 	return HDS_OK;
 }
 
-extern "C" int hds_bin_emit(int64_t n, int64_t num_pairs, int width, int height, const void* workspace,
-							void* pairs_workspace, size_t pairs_workspace_bytes, int32_t* values_sorted,
-							int32_t* tile_ranges, hds_stream_t stream) {
+// The (pair count, error flag) words hds_bin_count_async copies out.
+struct CountWords {
+	uint64_t total;
+	uint32_t error, pad;
+};
+
+const CountWords* count_words(const void* workspace, int64_t n) {
+	return at<CountWords>(const_cast<void*>(workspace), gaussian_space(n).ctrl);
+}
+
+// Enqueues the emitting half. With exact, num_pairs is the pair count; otherwise it is the
+// capacity the buffers were sized for and the kernels take min(count in the workspace, capacity).
+int bin_emit_launch(int64_t n, int64_t num_pairs, bool exact, int width, int height, const void* workspace,
+					void* pairs_workspace, size_t pairs_workspace_bytes, int32_t* values_sorted, int32_t* tile_ranges,
+					hipStream_t s) {
 	HDS_REQUIRE(width > 0 && height > 0, "bin_emit: image size %dx%d must be positive", width, height);
 	HDS_REQUIRE(num_pairs >= 0 && num_pairs < INT32_MAX, "bin_emit: pair count %lld outside [0, 2^31)",
 				(long long)num_pairs);
 	HDS_REQUIRE(tile_ranges, "bin_emit: tile_ranges must not be NULL");
 	const int tiles_x = (width + HDS_TILE - 1) / HDS_TILE, tiles_y = (height + HDS_TILE - 1) / HDS_TILE;
 	const int64_t num_tiles = (int64_t)tiles_x * tiles_y;
-	hipStream_t s = (hipStream_t)stream;
 	uint32_t* ranges_words = reinterpret_cast<uint32_t*>(tile_ranges);
-	if (num_pairs == 0) {
+	if (num_pairs == 0 || n == 0) {
 		HdsKernelTimer timer1("zero_kernel", s);
 		zero_kernel<<<hds_blocks(2 * num_tiles, kThreads), kThreads, 0, s>>>(ranges_words, 2 * num_tiles, nullptr, 0);
 		timer1.stop();
@@ -722,9 +746,10 @@ extern "C" int hds_bin_emit(int64_t n, int64_t num_pairs, int width, int height,
 	const PairSpace p = pair_space(num_pairs);
 	HDS_REQUIRE(pairs_workspace && pairs_workspace_bytes >= p.bytes, "bin_emit: pairs workspace of %zu bytes, need %zu",
 				pairs_workspace_bytes, p.bytes);
-	HDS_REQUIRE(workspace && values_sorted && n > 0, "bin_emit: null pointer argument");
+	HDS_REQUIRE(workspace && values_sorted, "bin_emit: null pointer argument");
 	const GaussianSpace g = gaussian_space(n);
 	void* ws = const_cast<void*>(workspace);
+	const uint64_t* total = exact ? nullptr : &count_words(workspace, n)->total;
 	const uint32_t* offsets = at<uint32_t>(ws, g.offsets);
 	const uint32_t* order = at<uint32_t>(ws, g.vals_a);
 	const uint2* rects_sorted = at<uint2>(ws, g.rects_sorted);
@@ -748,18 +773,75 @@ extern "C" int hds_bin_emit(int64_t n, int64_t num_pairs, int width, int height,
 	timer1.stop();
 	HDS_LAUNCH_CHECK("zero_sort_control", s);
 	HdsKernelTimer timer2("emit_kernel", s);
-	emit_kernel<<<(unsigned)parts_of(num_pairs), kThreads, 0, s>>>(n, num_pairs, offsets, order, rects_sorted, tiles_x,
-																	passes, keys_a, vals_a, ctrl->hist);
+	emit_kernel<<<(unsigned)parts_of(num_pairs), kThreads, 0, s>>>(n, num_pairs, total, offsets, order, rects_sorted,
+																	tiles_x, passes, keys_a, vals_a, ctrl->hist);
 	timer2.stop();
 	HDS_LAUNCH_CHECK("emit_pairs", s);
-	int st = onesweep_sort(keys_a, vals_a, keys_b, vals_b, num_pairs, passes, ctrl->hist, status, ctrl->tickets,
-						   &ctrl->error, true, nullptr, nullptr, s);
+	int st = onesweep_sort(keys_a, vals_a, keys_b, vals_b, num_pairs, total, passes, ctrl->hist, status,
+						   ctrl->tickets, &ctrl->error, true, nullptr, nullptr, s);
 	if (st != HDS_OK) return st;
 	const uint32_t* keys_sorted = (passes % 2 == 0) ? keys_a : keys_b;
 	HdsKernelTimer timer3("ranges_kernel", s);
-	ranges_kernel<<<hds_blocks(num_pairs, kThreads), kThreads, 0, s>>>(num_pairs, keys_sorted, num_tiles,
+	ranges_kernel<<<hds_blocks(num_pairs, kThreads), kThreads, 0, s>>>(num_pairs, total, keys_sorted, num_tiles,
 																		reinterpret_cast<int2*>(tile_ranges));
 	timer3.stop();
 	HDS_LAUNCH_CHECK("identify_tile_ranges", s);
 	return HDS_OK;
+}
+
+}  // namespace
+
+extern "C" int hds_bin_count(int64_t n, const float* means2D, const float* depths, const float* radii,
+							 const float* conics, const float* colors, const float* opacities, int width, int height,
+							 float* conic4, float* color_opacity4, void* workspace, size_t workspace_bytes,
+							 int64_t* num_pairs, hds_stream_t stream) {
+	HDS_REQUIRE(num_pairs, "bin_count: num_pairs must not be NULL");
+	*num_pairs = 0;
+	hipStream_t s = (hipStream_t)stream;
+	bool launched = false;
+	int st = bin_count_launch(n, means2D, depths, radii, conics, colors, opacities, width, height, conic4,
+							  color_opacity4, workspace, workspace_bytes, s, &launched);
+	if (st != HDS_OK || !launched) return st;
+	CountWords host = {0, 0, 0};
+	HDS_HIP(hipMemcpyAsync(&host, count_words(workspace, n), sizeof(host), hipMemcpyDeviceToHost, s));
+	HDS_HIP(hipStreamSynchronize(s));
+	if (host.error)
+		return hds_set_error(HDS_ERR_RUNTIME, "bin_count: a sort or scan look-back did not complete");
+	HDS_REQUIRE(host.total < (uint64_t)INT32_MAX, "bin_count: %llu tile-gaussian pairs overflow int32 indices",
+				(unsigned long long)host.total);
+	*num_pairs = (int64_t)host.total;
+	return HDS_OK;
+}
+
+extern "C" int hds_bin_count_async(int64_t n, const float* means2D, const float* depths, const float* radii,
+								   const float* conics, const float* colors, const float* opacities, int width,
+								   int height, float* conic4, float* color_opacity4, void* workspace,
+								   size_t workspace_bytes, void* count_host, hds_stream_t stream) {
+	HDS_REQUIRE(count_host, "bin_count_async: count_host must not be NULL");
+	hipStream_t s = (hipStream_t)stream;
+	bool launched = false;
+	int st = bin_count_launch(n, means2D, depths, radii, conics, colors, opacities, width, height, conic4,
+							  color_opacity4, workspace, workspace_bytes, s, &launched);
+	if (st != HDS_OK) return st;
+	if (!launched) {
+		// Nothing enqueued: the count is known now.
+		*static_cast<CountWords*>(count_host) = CountWords{0, 0, 0};
+		return HDS_OK;
+	}
+	HDS_HIP(hipMemcpyAsync(count_host, count_words(workspace, n), sizeof(CountWords), hipMemcpyDeviceToHost, s));
+	return HDS_OK;
+}
+
+extern "C" int hds_bin_emit(int64_t n, int64_t num_pairs, int width, int height, const void* workspace,
+							void* pairs_workspace, size_t pairs_workspace_bytes, int32_t* values_sorted,
+							int32_t* tile_ranges, hds_stream_t stream) {
+	return bin_emit_launch(n, num_pairs, true, width, height, workspace, pairs_workspace, pairs_workspace_bytes,
+						   values_sorted, tile_ranges, (hipStream_t)stream);
+}
+
+extern "C" int hds_bin_emit_capped(int64_t n, int64_t capacity, int width, int height, const void* workspace,
+								   void* pairs_workspace, size_t pairs_workspace_bytes, int32_t* values_sorted,
+								   int32_t* tile_ranges, hds_stream_t stream) {
+	return bin_emit_launch(n, capacity, false, width, height, workspace, pairs_workspace, pairs_workspace_bytes,
+						   values_sorted, tile_ranges, (hipStream_t)stream);
 }

@@ -51,14 +51,20 @@ class RasterizeGaussians(torch.autograd.Function):
         ext = _get_rasterizer()
         width, height = int(image_width), int(image_height)
         means2D = means2D.contiguous()
-        values_sorted, tile_ranges, conic, color_opacity = ext.bin(
-            means2D, depths.contiguous(), radii.contiguous(), conics.contiguous(), colors.contiguous(),
-            opacities.contiguous(), width, height)
+        # The render is enqueued before the host reads the pair count (the reference's one
+        # blocking read, forward.cu:321-325), so the GPU does not idle during that read.
+        bins = ext.bin_async(means2D, depths.contiguous(), radii.contiguous(), conics.contiguous(),
+                             colors.contiguous(), opacities.contiguous(), width, height)
         if features is not None:
             features = features.contiguous()
+        background = background.contiguous()
+        conic, color_opacity, tile_ranges = bins.conic4, bins.color_opacity4, bins.tile_ranges
         image, feature_image, final_T, n_contrib = ext.render(
-            means2D, conic, color_opacity, values_sorted, tile_ranges, width, height, background.contiguous(),
-            features)
+            means2D, conic, color_opacity, bins.values, tile_ranges, width, height, background, features)
+        if ext.resolve(bins):
+            image, feature_image, final_T, n_contrib = ext.render(
+                means2D, conic, color_opacity, bins.values, tile_ranges, width, height, background, features)
+        values_sorted = bins.values
         ctx.image_size = (width, height)
         ctx.save_for_backward(means2D, conic, color_opacity, values_sorted, tile_ranges, final_T, n_contrib,
                               background, features)

@@ -40,8 +40,10 @@ PROTOTYPES = {
     "hds_bin_workspace_bytes": (_sz, [_i64, _i32, _i32]),
     "hds_bin_count": (_i32, [_i64, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _vp, _vp, _vp, _sz,
                              ctypes.POINTER(ctypes.c_int64), _vp]),
+    "hds_bin_count_async": (_i32, [_i64, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _vp, _vp, _vp, _sz, _vp, _vp]),
     "hds_pairs_workspace_bytes": (_sz, [_i64, _i32, _i32]),
     "hds_bin_emit": (_i32, [_i64, _i64, _i32, _i32, _vp, _vp, _sz, _vp, _vp, _vp]),
+    "hds_bin_emit_capped": (_i32, [_i64, _i64, _i32, _i32, _vp, _vp, _sz, _vp, _vp, _vp]),
     "hds_render": (_i32, [_i64, _i32, _i32, _i32, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                           _vp]),
     "hds_render_backward": (_i32, [_i64, _i32, _i32, _i32, _i32, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp,
@@ -172,12 +174,35 @@ class StageTimer:
         return out
 
 
+class PendingBins:
+    """A binning enqueued by HipRasterizer.bin_async whose pair count the host has not read yet.
+
+    `values` is the capacity-sized pair buffer (exact once resolved), `tile_ranges`, `conic4` and
+    `color_opacity4` are final as soon as the stream has run the binning."""
+
+    def __init__(self, values, tile_ranges, conic4, color_opacity4, *, capacity=None, event=None, count=None,
+                 workspace=None, emit_args=None):
+        self.values = values
+        self.tile_ranges = tile_ranges
+        self.conic4 = conic4
+        self.color_opacity4 = color_opacity4
+        self.capacity = capacity        # None: already exact
+        self.event = event              # recorded after the count's copy to `count`
+        self.count = count              # pinned int64 [2]: pair count, look-back error flag
+        self.workspace = workspace      # per-gaussian workspace the exact re-emit reads
+        self.emit_args = emit_args      # (n, width, height, device)
+
+
 class HipRasterizer:
     """The reference extension's ten functions (bindings.cpp:4-42) on the HIP library, plus fused calls."""
+
+    # Pair buffers of bin_async are sized this much above the last pair count seen on the device.
+    PAIR_HEADROOM = 1.25
 
     def __init__(self) -> None:
         self.lib = load_library()
         self.timer: StageTimer | None = None
+        self._pair_capacity: dict[int, int] = {}
 
     def _run(self, stage: str, fn) -> None:
         """Runs one C call (raising on error), inside the stage timer when one is installed."""
@@ -279,6 +304,78 @@ class HipRasterizer:
             self._run("bin_emit", lambda: self.lib.hds_bin_emit(n, p, width, height, _ptr(ws), _ptr(pws), pws.numel(), _ptr(values_sorted),
                                          _ptr(tile_ranges), stream))
         return values_sorted, tile_ranges, conic4, color_opacity4
+
+    def bin_async(self, means2D, depths, radii, conics, colors, opacities, width, height) -> PendingBins:
+        """`bin` without the blocking read of P (forward.cu:311-326 deferred): the pair buffers are
+        sized from the last pair count seen on this device and the count reaches the host by an
+        asynchronous copy, so the render can be enqueued before the host knows P. `resolve` then
+        reads P, and rebins exactly when the capacity was too small. The first call on a device
+        has no history and bins synchronously."""
+        dev = means2D.device
+        if dev.index not in self._pair_capacity:
+            values, ranges, conic4, color_opacity4 = self.bin(means2D, depths, radii, conics, colors, opacities,
+                                                              width, height)
+            self._remember_pairs(dev, values.numel())
+            return PendingBins(values, ranges, conic4, color_opacity4)
+        means2D, depths, radii = _dev(means2D, "means2D"), _dev(depths, "depths"), _dev(radii, "radii")
+        conics, opacities = _dev(conics, "conics"), _dev(opacities, "opacities")
+        colors = None if colors is None else _dev(colors, "colors")
+        n = means2D.shape[0]
+        width, height = int(width), int(height)
+        tiles = ((width + TILE - 1) // TILE) * ((height + TILE - 1) // TILE)
+        cap = self._pair_capacity[dev.index]
+        conic4 = torch.empty((n, 4), device=dev, dtype=torch.float32)
+        color_opacity4 = torch.empty((n, 4), device=dev, dtype=torch.float32)
+        tile_ranges = torch.empty((tiles, 2), device=dev, dtype=torch.int32)
+        count = torch.zeros(2, dtype=torch.int64, pin_memory=True)
+        with torch.cuda.device(dev):
+            stream = _stream(dev)
+            ws = torch.empty(self.lib.hds_bin_workspace_bytes(n, width, height), device=dev, dtype=torch.uint8)
+            self._run("bin_count", lambda: self.lib.hds_bin_count_async(
+                n, _ptr(means2D), _ptr(depths), _ptr(radii), _ptr(conics), _ptr(colors), _ptr(opacities), width,
+                height, _ptr(conic4), _ptr(color_opacity4), _ptr(ws), ws.numel(), _ptr(count), stream))
+            event = torch.cuda.Event()
+            event.record()
+            values = torch.empty((cap,), device=dev, dtype=torch.int32)
+            pws = torch.empty(self.lib.hds_pairs_workspace_bytes(cap, width, height), device=dev, dtype=torch.uint8)
+            self._run("bin_emit", lambda: self.lib.hds_bin_emit_capped(
+                n, cap, width, height, _ptr(ws), _ptr(pws), pws.numel(), _ptr(values), _ptr(tile_ranges), stream))
+        return PendingBins(values, tile_ranges, conic4, color_opacity4, capacity=cap, event=event, count=count,
+                           workspace=ws, emit_args=(n, width, height, dev))
+
+    def resolve(self, pending: PendingBins) -> bool:
+        """Reads the pair count of a bin_async binning (waiting for its copy only, not for later
+        work on the stream) and trims `pending.values` to it. If the count exceeded the capacity,
+        bins again with exact buffers and returns True: whatever was rendered from the capped
+        binning must be rendered again."""
+        if pending.capacity is None:
+            return False
+        pending.event.synchronize()
+        total, error = int(pending.count[0]), int(pending.count[1]) & 0xFFFFFFFF
+        n, width, height, dev = pending.emit_args
+        cap = pending.capacity
+        pending.capacity = None
+        if error:
+            raise RuntimeError("bin_count: a sort or scan look-back did not complete")
+        if total >= 2**31 - 1:
+            raise RuntimeError(f"bin_count: {total} tile-gaussian pairs overflow int32 indices")
+        self._remember_pairs(dev, total)
+        if total <= cap:
+            pending.values = pending.values[:total]
+            return False
+        values = torch.empty((total,), device=dev, dtype=torch.int32)
+        with torch.cuda.device(dev):
+            pws = torch.empty(self.lib.hds_pairs_workspace_bytes(total, width, height), device=dev,
+                              dtype=torch.uint8)
+            self._run("bin_emit", lambda: self.lib.hds_bin_emit(
+                n, total, width, height, _ptr(pending.workspace), _ptr(pws), pws.numel(), _ptr(values),
+                _ptr(pending.tile_ranges), _stream(dev)))
+        pending.values = values
+        return True
+
+    def _remember_pairs(self, dev: torch.device, pairs: int) -> None:
+        chunk = 4096
+        self._pair_capacity[dev.index] = (int(pairs * self.PAIR_HEADROOM) + 2 * chunk) // chunk * chunk
 
     def render(self, means2D, conic4, color_opacity4, values_sorted, tile_ranges, width, height, background=None,
                features=None, rgb=True):

@@ -16,6 +16,8 @@
  *     the role of the reference's `conic` / `color_opacity` tuple members (forward.cu:274-276).
  *   - Work is enqueued on `stream` (a hipStream_t; NULL is the default stream). Only
  *     hds_bin_count blocks the host: it reads the pair count P back once, as forward.cu:321-325.
+ *     hds_bin_count_async + hds_bin_emit_capped are the same binning without that wait: the
+ *     count reaches the host by an asynchronous copy and the emit runs on capacity-sized buffers.
  *   - Returns HDS_OK (0) or an error status; hds_last_error() then holds a message for the
  *     calling thread. Invalid arguments are rejected before anything is enqueued.
  *   - The library never allocates device memory: scratch comes in as caller-owned workspaces
@@ -99,6 +101,16 @@ HDS_API int hds_bin_count(int64_t n, const float* means2D, const float* depths, 
 				  int height, float* conic4, float* color_opacity4, void* workspace,
 				  size_t workspace_bytes, int64_t* num_pairs, hds_stream_t stream);
 
+/* hds_bin_count without the blocking read (forward.cu:311-326 with the host read deferred):
+ * enqueues the same work, then an asynchronous copy of 16 bytes to count_host, which must be
+ * pinned host memory (hipHostMalloc): uint64 P, uint32 look-back error flag (nonzero = the
+ * counts are invalid), uint32 padding. The words are valid once the stream has passed this
+ * call; the caller checks them before trusting what hds_bin_emit_capped produced. */
+HDS_API int hds_bin_count_async(int64_t n, const float* means2D, const float* depths, const float* radii,
+						const float* conics, const float* colors, const float* opacities, int width,
+						int height, float* conic4, float* color_opacity4, void* workspace,
+						size_t workspace_bytes, void* count_host, hds_stream_t stream);
+
 /* Bytes of the per-pair workspace hds_bin_emit needs for P pairs. */
 HDS_API size_t hds_pairs_workspace_bytes(int64_t num_pairs, int width, int height);
 
@@ -108,6 +120,17 @@ HDS_API size_t hds_pairs_workspace_bytes(int64_t num_pairs, int width, int heigh
 HDS_API int hds_bin_emit(int64_t n, int64_t num_pairs, int width, int height, const void* workspace,
 				 void* pairs_workspace, size_t pairs_workspace_bytes, int32_t* values_sorted,
 				 int32_t* tile_ranges, hds_stream_t stream);
+
+/* hds_bin_emit (forward.cu:340-404) for a pair count the host has not read yet: values_sorted
+ * and the pairs workspace are sized for `capacity` pairs, and the kernels take P from the
+ * workspace hds_bin_count_async filled. When P <= capacity the result equals hds_bin_emit's for
+ * P (values_sorted[0, P) and tile_ranges). When P > capacity only the first `capacity` pairs of
+ * the depth order are sorted: tile_ranges stay consistent with what was written (every range
+ * lies in [0, capacity)) but the binning is incomplete, and the caller runs hds_bin_emit again
+ * with buffers for P. With the error flag set nothing is emitted (all ranges (0, 0)). */
+HDS_API int hds_bin_emit_capped(int64_t n, int64_t capacity, int width, int height, const void* workspace,
+						void* pairs_workspace, size_t pairs_workspace_bytes, int32_t* values_sorted,
+						int32_t* tile_ranges, hds_stream_t stream);
 
 /* ---- blend forward: replaces render_gaussians (forward.cu:406-434) and rasterize_features
  *      (features.cu:299-346) with one tile walk ------------------------------------------------ */

@@ -202,6 +202,69 @@ def test_empty_scene_renders_background():
     assert int(n_contrib.abs().sum()) == 0 and values.numel() == 0 and int(ranges.abs().sum()) == 0
 
 
+@pytest.mark.parametrize("capacity", ["exact", "short", "tiny", "roomy"])
+def test_async_binning_equals_the_oracle_whatever_the_capacity(capacity):
+    """bin_async + resolve (the autograd path: render enqueued before the host reads P) gives the
+    oracle's binning bit for bit when the pair buffers are exactly P, a partition short of P (the
+    capped sort runs, then resolve rebins exactly), far too small, or larger than P; the render
+    of a capped binning stays inside its buffers."""
+    from gaussian_splatting.rasterizer._native import HipRasterizer
+
+    wl = synthetic_config(1, n=60_000, channels=1)
+    (m2, d, r, c), _ = project_both(wl.means, wl.scales, wl.quats, wl.opacities, wl.cam)
+    opac = wl.opacities.to(DEV)
+    counts, want_values, want_ranges = oracle.bin_gaussians(np_(m2), np_(d), np_(r), np_(c), np_(opac), wl.width,
+                                                            wl.height)
+    p = int(counts.sum())
+    cap = {"exact": p, "short": p - 4096, "tiny": 1, "roomy": p + 10_000}[capacity]
+    ext = HipRasterizer()
+    ext._pair_capacity[m2.device.index] = cap
+    colors = torch.rand(wl.n, 3, generator=torch.Generator().manual_seed(3)).to(DEV)
+    bins = ext.bin_async(m2, d, r, c, colors, opac, wl.width, wl.height)
+    assert bins.values.numel() == cap
+    _, _, T, _ = ext.render(m2, bins.conic4, bins.color_opacity4, bins.values, bins.tile_ranges, wl.width,
+                            wl.height, torch.zeros(3, device=DEV))
+    torch.cuda.synchronize()
+    rebinned = ext.resolve(bins)
+    assert rebinned == (cap < p)
+    np.testing.assert_array_equal(np_(bins.values), want_values)
+    np.testing.assert_array_equal(np_(bins.tile_ranges), want_ranges)
+    assert ext._pair_capacity[m2.device.index] >= p
+    assert bool(torch.isfinite(T).all())
+
+
+def test_async_binning_of_a_scene_with_no_pairs():
+    from gaussian_splatting.rasterizer._native import HipRasterizer
+
+    ext = HipRasterizer()
+    ext._pair_capacity[0] = 8192
+    n = 500
+    means2D = torch.rand(n, 2, device=DEV) * 40
+    bins = ext.bin_async(means2D, torch.ones(n, device=DEV), torch.zeros(n, device=DEV),
+                         torch.full((n, 3), 0.1, device=DEV), None, torch.full((n, 1), 0.5, device=DEV), 40, 30)
+    assert not ext.resolve(bins)
+    assert bins.values.numel() == 0 and int(bins.tile_ranges.abs().sum()) == 0
+
+
+def test_rasterize_is_identical_with_and_without_the_pair_count_read():
+    # The first call on a fresh binding bins synchronously, later ones bin ahead of the count.
+    import gaussian_splatting.rasterizer as rasterizer_module
+    from gaussian_splatting.rasterizer._native import HipRasterizer
+
+    wl = synthetic_config(0, n=8000)
+    (m2, d, r, c), _ = project_both(wl.means, wl.scales, wl.quats, wl.opacities, wl.cam)
+    colors = torch.rand(wl.n, 3, generator=torch.Generator().manual_seed(3)).to(DEV)
+    feats, opac = wl.features.to(DEV), wl.opacities.to(DEV)
+    saved = rasterizer_module._rasterizer_module
+    rasterizer_module._rasterizer_module = HipRasterizer()
+    try:
+        outs = [rasterize(m2, d, r, c, colors, opac, wl.width, wl.height, features=feats) for _ in range(3)]
+    finally:
+        rasterizer_module._rasterizer_module = saved
+    for image, fimg in outs[1:]:
+        assert torch.equal(image, outs[0][0]) and torch.equal(fimg, outs[0][1])
+
+
 # ---- blend forward ----------------------------------------------------------------------------
 
 def oracle_render(inputs, width, height, background=None, features=None):
