@@ -100,7 +100,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void b
 	__shared__ int s_slot[4][kGeoGroup];
 	__shared__ int s_max_last;
 	// Per wave: s and w of the group as rows per position (the B operands of the moment MFMAs).
-	__shared__ __attribute__((aligned(16))) uint32_t s_tr[4][2][kGeoGroup * kRowStride];
+	__shared__ __attribute__((aligned(16))) float s_tr[4][2][kGeoGroup * kRowStride];
 
 	const int tile = hds_xcd_tile(blockIdx.x, a.num_tiles);
 	if (tile < 0) return;
@@ -128,8 +128,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void b
 		gb = a.grad_image[pix * 3 + 2];
 		dL_dTf = a.background[0] * gr + a.background[1] * gg + a.background[2] * gb;
 	}
-	float rec_r = 0.0f, rec_g = 0.0f, rec_b = 0.0f, last_alpha = 0.0f;
-	float last_r = 0.0f, last_g = 0.0f, last_b = 0.0f, behind_dot = 0.0f;
+	// One recurrence serves RGB and features: with dot = f . dL/dF + c . dL/dRGB, the reference's
+	// RGB term (c - rec) . g T (rec = colour blended behind, backward.cu:113-122) is
+	// T (c . g - rec . g), and rec . g obeys the same recurrence as the features' behind_dot.
+	float behind_dot = 0.0f;
 
 	// P^T, the A operand of the moment MFMAs: row lane % 16 = column j of P, k = pixels
 	// 32kk + 8(lane / 16) + 0..7. Rows 0-5: 1, x, y, x^2, xy, y^2 about the block centre (exact in
@@ -201,8 +203,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void b
 	const int2 range = a.ranges[tile];
 	const int num = min(range.y - range.x, tile_max_last(last, &s_max_last));
 	const int wave_last = hds_wave_max(last);
-	uint32_t* tr_s = s_tr[wave][0];
-	uint32_t* tr_w = s_tr[wave][1];
+	float* tr_s = s_tr[wave][0];
+	float* tr_w = s_tr[wave][1];
 	int* slots = s_slot[wave];
 
 	// Batches run back to front: batch b holds list entries [start(b), start(b) + count(b)).
@@ -366,29 +368,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void b
 							const bool contributes = q < count && batch_start + slot[u] < last && alpha >= HDS_MIN_ALPHA;
 							float dL_dalpha = 0.0f, w = 0.0f;
 							if (contributes) {
+								float d = 0.0f;
+								if constexpr (S > 0) d = dot[q >> 2][q & 3];
+								if (do_rgb) d += col[u].x * gr + col[u].y * gg + col[u].z * gb;
 								const float inv_1ma = __builtin_amdgcn_rcpf(1.0f - alpha);
 								T *= inv_1ma;
 								w = alpha * T;
-								if (do_rgb) {
-									rec_r = last_alpha * last_r + (1.0f - last_alpha) * rec_r;
-									rec_g = last_alpha * last_g + (1.0f - last_alpha) * rec_g;
-									rec_b = last_alpha * last_b + (1.0f - last_alpha) * rec_b;
-									last_r = col[u].x;
-									last_g = col[u].y;
-									last_b = col[u].z;
-									last_alpha = alpha;
-									dL_dalpha = ((col[u].x - rec_r) * gr + (col[u].y - rec_g) * gg + (col[u].z - rec_b) * gb) * T -
-												T_final * inv_1ma * dL_dTf;
-								}
-								if constexpr (S > 0) {
-									dL_dalpha += T * (dot[q >> 2][q & 3] - behind_dot);
-									behind_dot = alpha * dot[q >> 2][q & 3] + (1.0f - alpha) * behind_dot;
-								}
+								dL_dalpha = T * (d - behind_dot);
+								if (do_rgb) dL_dalpha -= T_final * inv_1ma * dL_dTf;
+								behind_dot = alpha * d + (1.0f - alpha) * behind_dot;
 							}
 							// A clamped alpha no longer depends on the gaussian (backward.cu:126-135).
-							const float sg = (contributes && raw[u] <= HDS_MAX_ALPHA) ? G[u] * dL_dalpha : 0.0f;
-							tr_s[q * kRowStride + lane] = hds_split_pack(sg);
-							if (do_rgb) tr_w[q * kRowStride + lane] = hds_split_pack(w);
+							tr_s[q * kRowStride + lane] = (contributes && raw[u] <= HDS_MAX_ALPHA) ? G[u] * dL_dalpha : 0.0f;
+							if (do_rgb) tr_w[q * kRowStride + lane] = w;
 							if (hds_ballot(contributes)) active |= 1u << q;
 						}
 					}
@@ -397,8 +389,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void b
 	#pragma unroll
 				for (int q = 0; q < kGeoGroup; q++) {
 					if (q >= count) {
-						tr_s[q * kRowStride + lane] = 0u;
-						if (do_rgb) tr_w[q * kRowStride + lane] = 0u;
+						tr_s[q * kRowStride + lane] = 0.0f;
+						if (do_rgb) tr_w[q * kRowStride + lane] = 0.0f;
 					}
 				}
 				hds_wave_fence();
@@ -410,19 +402,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void b
 				for (int kk = 0; kk < 2; kk++) {
 					const int off = (lane & 15) * kRowStride + 32 * kk + 8 * (lane >> 4);
 					{
-						const hds_u32x4 d0 = hds_lds_read128(tr_s + off);
-						const hds_u32x4 d1 = hds_lds_read128(tr_s + off + 4);
-						const uint32_t d[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+						const hds_u32x4 d0 = hds_lds_read128(reinterpret_cast<const uint32_t*>(tr_s + off));
+						const hds_u32x4 d1 = hds_lds_read128(reinterpret_cast<const uint32_t*>(tr_s + off + 4));
+						const float v[8] = {hds_u2f(d0.x), hds_u2f(d0.y), hds_u2f(d0.z), hds_u2f(d0.w),
+											hds_u2f(d1.x), hds_u2f(d1.y), hds_u2f(d1.z), hds_u2f(d1.w)};
 						hds_bf16x8 b_hi, b_lo;
-						hds_unpack8(d, b_hi, b_lo);
+						hds_split8(v, b_hi, b_lo);
 						ms = hds_mfma_split(pt_hi[kk], pt_lo[kk], b_hi, b_lo, ms);
 					}
 					if (do_rgb) {
-						const hds_u32x4 d0 = hds_lds_read128(tr_w + off);
-						const hds_u32x4 d1 = hds_lds_read128(tr_w + off + 4);
-						const uint32_t d[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+						const hds_u32x4 d0 = hds_lds_read128(reinterpret_cast<const uint32_t*>(tr_w + off));
+						const hds_u32x4 d1 = hds_lds_read128(reinterpret_cast<const uint32_t*>(tr_w + off + 4));
+						const float v[8] = {hds_u2f(d0.x), hds_u2f(d0.y), hds_u2f(d0.z), hds_u2f(d0.w),
+											hds_u2f(d1.x), hds_u2f(d1.y), hds_u2f(d1.z), hds_u2f(d1.w)};
 						hds_bf16x8 b_hi, b_lo;
-						hds_unpack8(d, b_hi, b_lo);
+						hds_split8(v, b_hi, b_lo);
 						mw = hds_mfma_split(pt_hi[kk], pt_lo[kk], b_hi, b_lo, mw);
 					}
 				}
