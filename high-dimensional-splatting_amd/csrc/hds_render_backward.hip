@@ -469,12 +469,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void b
 }
 
 // dF[position][c] += sum_px W[position][px] dL/dF[px][c] for one group of 32 positions, then one
-// atomic per (position, channel). rows: W as [position][pixel] split-packed; gids: -1 where no
-// pixel of the wave took the gaussian.
+// atomic per (position, channel). rows: W as [position][pixel] split-packed; gid_row: lane r < 32
+// holds the gaussian of row r (-1 for padding rows); gids: the wave's 32-int LDS scratch.
 template <int S>
 __device__ inline void flush_features(const hds_bf16x8 (&gb_hi)[4][S / 32], const hds_bf16x8 (&gb_lo)[4][S / 32],
-									  const uint32_t* rows, const int* gids, float* grad_features, int channels, int c0,
-									  int lane) {
+									  const uint32_t* rows, int gid_row, int* gids, float* grad_features, int channels,
+									  int c0, int lane) {
+	if (lane < kFeatGroup) gids[lane] = gid_row;
 	hds_wave_fence();
 	// A = W: row lane % 32 = position, k = pixels 16kp + 8(lane / 32) + 0..7.
 	hds_bf16x8 a_hi[4], a_lo[4];
@@ -567,7 +568,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S >= 128 ? 
 	int* gids = s_ggid[wave];
 
 	float T = 1.0f;
-	int q = 0;  // filled positions of the wave's current group
+	int q = 0;          // filled positions of the wave's current group (wave-uniform)
+	int gid_row = -1;   // lane r < 32: gaussian of group row r
 	const int num_batches = (num + kBatch - 1) / kBatch;
 	auto batch_count = [&](int b) { return b < num_batches ? min(kBatch, num - b * kBatch) : 0; };
 	if (num_batches > 0) {
@@ -580,6 +582,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S >= 128 ? 
 		hds_wait_vmem();
 		__syncthreads();
 	}
+	auto flush = [&]() {
+		flush_features<S>(gb_hi, gb_lo, rows, (lane & 31) < q ? gid_row : -1, gids, a.grad_features, a.channels, c0,
+						  lane);
+		q = 0;
+	};
 	// One batch: stage b+1, read the gids of b+2, walk b.
 	auto step = [&](int b, const HdsHeaderSlot<kBatch, false>& h, HdsHeaderSlot<kBatch, false>& h_next) {
 		const int cnt = batch_count(b), cnt1 = batch_count(b + 1), cnt2 = batch_count(b + 2);
@@ -595,18 +602,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S >= 128 ? 
 				const float4 box = hds_cull_box(make_float2(h.mx[lane], h.my[lane]), h.conic[lane]);
 				box_hit = hds_box_hits(box, rx0, rx1, ry0, ry1);
 			}
+			// Lane i holds the gaussian of batch slot i (read by the row bookkeeping below).
+			const int slot_gid = lane < cnt ? bgid[lane] : -1;
 			uint64_t hits = hds_ballot(box_hit);
 			while (hits) {
-				// The next (up to) kIlp hits in list order, as many as the group has room for.
-				const int take = min(min(kIlp, __builtin_popcountll(hits)), kFeatGroup - q);
+				// Room for kIlp more rows; the group is flushed a little early rather than split.
+				if (q > kFeatGroup - kIlp) flush();
+				// The next (up to) kIlp hits in list order. All bookkeeping here is wave-uniform.
 				int slot[kIlp];
 				float alpha[kIlp];
+				int take = 0;
 #pragma unroll
 				for (int u = 0; u < kIlp; u++) {
 					slot[u] = kBatch - 1;
-					if (u < take) {
-						slot[u] = __builtin_ctzll(hits);
+					if (hits) {
+						slot[u] = __builtin_amdgcn_readfirstlane(__builtin_ctzll(hits));
 						hits &= hits - 1;
+						take = u + 1;
 					}
 					float G, dx, dy;
 					alpha[u] = fminf(HDS_MAX_ALPHA, hds_raw_alpha(fx, fy, make_float2(h.mx[slot[u]], h.my[slot[u]]),
@@ -614,9 +626,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S >= 128 ? 
 				}
 #pragma unroll
 				for (int u = 0; u < kIlp; u++) {
-					if (u >= take) break;
 					// The forward's test, with its termination read from n_contrib.
-					const bool contributes = batch + slot[u] < last && alpha[u] >= HDS_MIN_ALPHA;
+					const bool contributes = u < take && batch + slot[u] < last && alpha[u] >= HDS_MIN_ALPHA;
 					float w = 0.0f;
 					if (contributes) {
 						const float test_T = T * (1.0f - alpha[u]);
@@ -626,13 +637,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S >= 128 ? 
 					// A gaussian no pixel of the block takes gets no row (and no atomics).
 					if (hds_ballot(contributes) != 0) {
 						rows[q * kRowStride + lane] = hds_split_pack(w);
-						if (lane == 0) gids[q] = bgid[slot[u]];
-						q++;
+						const int g = __builtin_amdgcn_readlane(slot_gid, slot[u]);
+						if ((lane & 31) == q) gid_row = g;
+						q = __builtin_amdgcn_readfirstlane(q + 1);
 					}
-				}
-				if (q == kFeatGroup) {
-					flush_features<S>(gb_hi, gb_lo, rows, gids, a.grad_features, a.channels, c0, lane);
-					q = 0;
 				}
 			}
 		}
@@ -647,8 +655,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S >= 128 ? 
 	}
 	if (q > 0) {
 		for (int r = q; r < kFeatGroup; r++) rows[r * kRowStride + lane] = 0u;
-		if (lane >= q && lane < kFeatGroup) gids[lane] = -1;
-		flush_features<S>(gb_hi, gb_lo, rows, gids, a.grad_features, a.channels, c0, lane);
+		flush();
 	}
 }
 

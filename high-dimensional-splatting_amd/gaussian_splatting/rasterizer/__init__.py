@@ -51,6 +51,10 @@ class RasterizeGaussians(torch.autograd.Function):
         ext = _get_rasterizer()
         width, height = int(image_width), int(image_height)
         means2D = means2D.contiguous()
+        # Training (features need a gradient): the gradient buffers are zeroed beside the binning.
+        ctx.prezeroed = None
+        if features is not None and ctx.needs_input_grad[7]:
+            ctx.prezeroed = ext.prezeroed_gradients(means2D.shape[0], int(features.shape[1]), means2D.device)
         # The render is enqueued before the host reads the pair count (the reference's one
         # blocking read, forward.cu:321-325), so the GPU does not idle during that read.
         bins = ext.bin_async(means2D, depths.contiguous(), radii.contiguous(), conics.contiguous(),
@@ -93,7 +97,8 @@ class RasterizeGaussians(torch.autograd.Function):
             features=features if feature_term else None,
             grad_feature_image=grad_features.contiguous() if feature_term else None,
             slice_width=(FEATURE_SLICE_WIDTH or default_slice_width(features.shape[1])) if feature_term else None,
-            want_feature_grad=feature_term and ctx.needs_input_grad[7])
+            want_feature_grad=feature_term and ctx.needs_input_grad[7], prezeroed=ctx.prezeroed)
+        ctx.prezeroed = None
         return g_means, None, None, g_conics, g_colors, g_opac, None, g_feat, None, None
 
 

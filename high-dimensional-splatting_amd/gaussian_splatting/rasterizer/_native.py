@@ -203,6 +203,29 @@ class HipRasterizer:
         self.lib = load_library()
         self.timer: StageTimer | None = None
         self._pair_capacity: dict[int, int] = {}
+        self._zero_streams: dict[int, torch.cuda.Stream] = {}
+
+    def prezeroed_gradients(self, n: int, channels: int, device: torch.device):
+        """Zeroed output buffers for a later render_backward (grad_means2D [N,2], grad_conics [N,3],
+        grad_colors [N,3], grad_opacities [N,1], grad_features [N,C]), cleared on a side stream
+        (default priority) that starts after the work queued so far, so the fill runs beside the
+        forward's binning instead of at the head of the backward. Returns (buffers, event); pass both
+        to render_backward."""
+        current = torch.cuda.current_stream(device)
+        side = self._zero_streams.get(device.index)
+        if side is None:
+            side = self._zero_streams[device.index] = torch.cuda.Stream(device=device)
+        f32 = dict(device=device, dtype=torch.float32)
+        buffers = (torch.empty((n, 2), **f32), torch.empty((n, 3), **f32), torch.empty((n, 3), **f32),
+                   torch.empty((n, 1), **f32), torch.empty((n, channels), **f32))
+        side.wait_stream(current)
+        with torch.cuda.stream(side):
+            torch._foreach_zero_(list(buffers))
+            for b in buffers:
+                b.record_stream(side)
+            event = torch.cuda.Event()
+            event.record(side)
+        return buffers, event
 
     def _run(self, stage: str, fn) -> None:
         """Runs one C call (raising on error), inside the stage timer when one is installed."""
@@ -411,8 +434,10 @@ class HipRasterizer:
 
     def render_backward(self, means2D, conic4, color_opacity4, values_sorted, tile_ranges, final_T, n_contrib,
                         width, height, grad_image=None, background=None, features=None, grad_feature_image=None,
-                        slice_width=None, want_feature_grad=True):
-        """One back-to-front walk (backward.cu:7-164 + features.cu:350-542).
+                        slice_width=None, want_feature_grad=True, prezeroed=None):
+        """One back-to-front walk (backward.cu:7-164 + features.cu:350-542). `prezeroed` is a
+        (buffers, event) pair from prezeroed_gradients: the gradients are then added into those
+        buffers once the event has passed, instead of into buffers zeroed here.
 
         Returns (grad_means2D [N,2], grad_conics [N,3], grad_colors [N,3] or None, grad_opacities [N,1],
         grad_features [N,C] or None).
@@ -428,15 +453,28 @@ class HipRasterizer:
             grad_image = _dev(grad_image, "grad_image")
             if background is None:
                 background = torch.zeros(3, device=dev, dtype=torch.float32)
-        # hds_render_backward zeroes the outputs itself before its atomics add into them.
-        f32 = dict(device=dev, dtype=torch.float32)
-        g_means = torch.empty((n, 2), **f32)
-        g_conics = torch.empty((n, 3), **f32)
-        g_colors = torch.empty((n, 3), **f32) if grad_image is not None else None
-        g_opac = torch.empty((n, 1), **f32)
-        g_feat = torch.empty((n, channels), **f32) if features is not None and want_feature_grad else None
+        want_feat = features is not None and want_feature_grad
+        if prezeroed is not None:
+            (g_means, g_conics, g_colors, g_opac, g_feat), event = prezeroed
+            if grad_image is None:
+                g_colors = None
+            if not want_feat:
+                g_feat = None
+            elif g_feat.shape != (n, channels):
+                raise RuntimeError(f"prezeroed grad_features {tuple(g_feat.shape)} != ({n}, {channels})")
+            torch.cuda.current_stream(dev).wait_event(event)
+            entry = self.lib.hds_render_backward_accumulate
+        else:
+            # hds_render_backward zeroes the outputs itself before its atomics add into them.
+            f32 = dict(device=dev, dtype=torch.float32)
+            g_means = torch.empty((n, 2), **f32)
+            g_conics = torch.empty((n, 3), **f32)
+            g_colors = torch.empty((n, 3), **f32) if grad_image is not None else None
+            g_opac = torch.empty((n, 1), **f32)
+            g_feat = torch.empty((n, channels), **f32) if want_feat else None
+            entry = self.lib.hds_render_backward
         with torch.cuda.device(dev):
-            self._run("render_backward", lambda: self.lib.hds_render_backward(
+            self._run("render_backward", lambda: entry(
                 n, int(width), int(height), channels, slice_width or 0, _ptr(tile_ranges), _ptr(values_sorted),
                 values_sorted.numel(), _ptr(_dev(means2D, "means2D")), _ptr(conic4), _ptr(color_opacity4),
                 _ptr(background), _ptr(final_T), _ptr(n_contrib), _ptr(grad_image), _ptr(features),
