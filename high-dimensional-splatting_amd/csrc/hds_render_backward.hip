@@ -79,10 +79,11 @@ __device__ inline int tile_max_last(int last, int* s_max_last) {
 template <int S, bool RGB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void backward_geometry_kernel(const BackwardArgs a) {
 	constexpr int kKc = S > 0 ? S / 32 : 1;       // K steps of the dot over channels
-	constexpr int kAccStride = 9;
-	// Gaussians per batch: 32 at S = 128 so that two work-groups fit a CU's LDS; positions whose
+	// Per gaussian slot: the six pixel moments of s of each wave's block, then the colour gradient.
+	constexpr int kAccStride = 4 * 6 + 3;
+	// Gaussians per batch: 32 at S >= 64 so that two work-groups fit a CU's LDS; positions whose
 	// alphas are evaluated together: 2 at S = 128, where dL/dF takes half the registers.
-	constexpr int kGB = S >= 128 ? 32 : kBatch;
+	constexpr int kGB = S >= 64 ? 32 : kBatch;
 	constexpr int kGeoIlp = S >= 128 ? 2 : kIlp;
 	constexpr int kRows = S > 0 ? (kGB + 1) * S : 1;
 
@@ -92,8 +93,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void b
 	// partial group point at it).
 	__shared__ int s_gid[3][kGB];
 	__shared__ HdsHeaderSlot<kGB, RGB> s_hdr0, s_hdr1;
-	// Gradients of batch b summed over the tile's waves (slot b & 1), 9 per gaussian: opacity,
-	// mean x / y, conic a / b / c, colour r / g / b. One lane per gaussian then adds them to HBM.
+	// Sums of batch b (slot b & 1) per gaussian: for each wave, the moments sum s {1, x, y, x^2, xy,
+	// y^2} about its block centre, then sum w dL/dRGB. One lane per gaussian turns them into
+	// gradients and adds those to HBM once per tile.
 	__shared__ float s_acc[2][kGB * kAccStride];
 	__shared__ __attribute__((aligned(16))) float s_feat0[kRows];
 	__shared__ __attribute__((aligned(16))) float s_feat1[kRows];
@@ -114,7 +116,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void b
 	const float fx = (float)px + 0.5f, fy = (float)py + 0.5f;
 	const float rx0 = (float)wx0 + 0.5f, rx1 = (float)wx0 + 7.5f;
 	const float ry0 = (float)wy0 + 0.5f, ry1 = (float)wy0 + 7.5f;
-	const float centre_x = (float)wx0 + 4.0f, centre_y = (float)wy0 + 4.0f;
 	const int c0 = slice * S;
 	const bool do_rgb = RGB && slice == 0;
 
@@ -225,33 +226,69 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void b
 		__syncthreads();
 	}
 
-	// Adds batch b's summed gradients to HBM, one lane per gaussian, and clears its slot for b + 2.
-	// Runs at the end of the step that follows batch b (after the barrier that closed b, before the
-	// gids of b + 3 replace those of b in slot b % 3).
+	// Turns batch b's sums into gradients and adds them to HBM, one lane per gaussian, and clears the
+	// slot for b + 2 (backward.cu:136-160 in moment form: with d = pixel - mean, dopacity = sum s,
+	// dmean = op Q sum s d, dconic = -op (sum s dx^2 / 2, sum s dx dy, sum s dy^2 / 2), each wave's
+	// moments shifted from its block centre to the mean). Runs at the end of the step that follows
+	// batch b (after the barrier that closed b, before the gids of b + 3 replace those of b in slot
+	// b % 3); mean and conic come from HBM, loaded at the start of that step (prefetch_geometry).
+	// The work is spread over the whole work-group: thread t takes gaussian slot t / 4 and the
+	// moments of wave t % 4, and the four partial gradients of a slot are summed across adjacent
+	// lanes. Mean and conic come from HBM, loaded at the start of that step (prefetch_geometry).
+	const int f_slot = tid >> 2, f_wave = tid & 3;
+	// The gaussian id is read here too: the flush runs beside the stores of the gids of b + 3
+	// into the same slot by other threads.
+	int pf_gid = 0;
+	float2 pf_mean = make_float2(0.0f, 0.0f);
+	float4 pf_conic = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+	auto prefetch_geometry = [&](int b) {
+		if (f_slot < batch_count(b)) {
+			pf_gid = s_gid[b % 3][f_slot];
+			pf_mean = a.means2D[pf_gid];
+			pf_conic = a.conic4[pf_gid];
+		}
+	};
 	auto flush_gradients = [&](int b) {
 		const int cnt = batch_count(b);
-		if (tid >= cnt) return;
-		float* g = s_acc[b & 1] + tid * kAccStride;
-		const int gid = s_gid[b % 3][tid];
-		float v[kAccStride];
+		if (f_slot >= ((cnt + 15) & ~15)) return;  // whole 16-slot (64-lane) groups stay converged
+		const bool valid = f_slot < cnt;
+		float* g = s_acc[b & 1] + f_slot * kAccStride;
+		float m[6];
 #pragma unroll
-		for (int k = 0; k < kAccStride; k++) {
-			v[k] = g[k];
-			g[k] = 0.0f;
+		for (int k = 0; k < 6; k++) {
+			m[k] = valid ? g[6 * f_wave + k] : 0.0f;
+			if (valid) g[6 * f_wave + k] = 0.0f;
 		}
-		if (v[0] != 0.0f || v[1] != 0.0f || v[2] != 0.0f || v[3] != 0.0f || v[4] != 0.0f || v[5] != 0.0f) {
-			atomicAdd(&a.grad_opacities[gid], v[0]);
-			atomicAdd(&a.grad_means2D[gid * 2 + 0], v[1]);
-			atomicAdd(&a.grad_means2D[gid * 2 + 1], v[2]);
-			atomicAdd(&a.grad_conics[gid * 3 + 0], v[3]);
-			atomicAdd(&a.grad_conics[gid * 3 + 1], v[4]);
-			atomicAdd(&a.grad_conics[gid * 3 + 2], v[5]);
+		float rgb = 0.0f;
+		if (valid && f_wave < 3) {
+			rgb = g[24 + f_wave];
+			g[24 + f_wave] = 0.0f;
 		}
-		if (do_rgb && (v[6] != 0.0f || v[7] != 0.0f || v[8] != 0.0f)) {
-			atomicAdd(&a.grad_colors[gid * 3 + 0], v[6]);
-			atomicAdd(&a.grad_colors[gid * 3 + 1], v[7]);
-			atomicAdd(&a.grad_colors[gid * 3 + 2], v[8]);
+		const float4 co = pf_conic;
+		const float mx = pf_mean.x - ((float)(tx0 + (f_wave & 1) * 8) + 4.0f);
+		const float my = pf_mean.y - ((float)(ty0 + (f_wave >> 1) * 8) + 4.0f);
+		const float sx = m[1] - mx * m[0], sy = m[2] - my * m[0];
+		const float sxx = m[3] - 2.0f * mx * m[1] + mx * mx * m[0];
+		const float sxy = m[4] - mx * m[2] - my * m[1] + mx * my * m[0];
+		const float syy = m[5] - 2.0f * my * m[2] + my * my * m[0];
+		float d[6] = {m[0], co.w * (co.x * sx + co.y * sy), co.w * (co.y * sx + co.z * sy), -0.5f * co.w * sxx,
+					  -co.w * sxy, -0.5f * co.w * syy};
+#pragma unroll
+		for (int k = 0; k < 6; k++) {
+			d[k] += hds_shfl_xor(d[k], 1);
+			d[k] += hds_shfl_xor(d[k], 2);
 		}
+		if (!valid) return;
+		const int gid = pf_gid;
+		if (f_wave == 0 && (d[0] != 0.0f || d[1] != 0.0f || d[2] != 0.0f || d[3] != 0.0f || d[4] != 0.0f || d[5] != 0.0f)) {
+			atomicAdd(&a.grad_opacities[gid], d[0]);
+			atomicAdd(&a.grad_means2D[gid * 2 + 0], d[1]);
+			atomicAdd(&a.grad_means2D[gid * 2 + 1], d[2]);
+			atomicAdd(&a.grad_conics[gid * 3 + 0], d[3]);
+			atomicAdd(&a.grad_conics[gid * 3 + 1], d[4]);
+			atomicAdd(&a.grad_conics[gid * 3 + 2], d[5]);
+		}
+		if (do_rgb && f_wave < 3 && rgb != 0.0f) atomicAdd(&a.grad_colors[gid * 3 + f_wave], rgb);
 	};
 
 	// One batch: stage b+1, read the gids of b+2, walk b.
@@ -260,6 +297,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void b
 		const int cnt = batch_count(b), cnt1 = batch_count(b + 1), cnt2 = batch_count(b + 2);
 		const int batch_start = batch_start_of(b);
 		float* acc = s_acc[b & 1];
+		if (b > 0) prefetch_geometry(b - 1);
 		int g2 = 0;
 		if (tid < cnt2) g2 = a.values[range.x + batch_start_of(b + 2) + tid];
 		const int* gid_next = s_gid[(b + 1) % 3];
@@ -426,31 +464,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void b
 				const int q = lane & 15;
 				const bool mine = q < count && ((active >> q) & 1u);
 				if (lane < 16 && mine) {
-					// Moments about the block centre -> gradients (backward.cu:136-160, in moment form),
-					// summed over the tile's waves in LDS.
-					const int sl = slots[q];
-					const float2 mn = make_float2(h.mx[sl], h.my[sl]);
-					const float4 co = h.conic[sl];
-					const float m00 = ms[0], m10 = ms[1], m01 = ms[2], m20 = ms[3];
-					const float mx = mn.x - centre_x, my = mn.y - centre_y;
-					const float sx = m10 - mx * m00, sy = m01 - my * m00;
-					const float sxx = m20 - 2.0f * mx * m10 + mx * mx * m00;
-					const float sxy = m11 - mx * m01 - my * m10 + mx * my * m00;
-					const float syy = m02 - 2.0f * my * m01 + my * my * m00;
-					float* g = acc + sl * kAccStride;
-					atomicAdd(&g[0], m00);
-					atomicAdd(&g[1], co.w * (co.x * sx + co.y * sy));
-					atomicAdd(&g[2], co.w * (co.y * sx + co.z * sy));
-					atomicAdd(&g[3], -0.5f * co.w * sxx);
-					atomicAdd(&g[4], -co.w * sxy);
-					atomicAdd(&g[5], -0.5f * co.w * syy);
+					// This wave's moments about its block centre, summed per gaussian in LDS (the
+					// flush turns them into gradients).
+					float* g = acc + slots[q] * kAccStride + 6 * wave;
+					atomicAdd(&g[0], ms[0]);
+					atomicAdd(&g[1], ms[1]);
+					atomicAdd(&g[2], ms[2]);
+					atomicAdd(&g[3], ms[3]);
+					atomicAdd(&g[4], m11);
+					atomicAdd(&g[5], m02);
 				}
 				if (do_rgb && lane >= 32 && lane < 48 && mine) {
 					// Rows 8-10: the colour gradients sum_px w dL/dRGB (backward.cu:112-118).
-					float* g = acc + slots[q] * kAccStride;
-					atomicAdd(&g[6], mw[0]);
-					atomicAdd(&g[7], mw[1]);
-					atomicAdd(&g[8], mw[2]);
+					float* g = acc + slots[q] * kAccStride + 24;
+					atomicAdd(&g[0], mw[0]);
+					atomicAdd(&g[1], mw[1]);
+					atomicAdd(&g[2], mw[2]);
 				}
 				hds_wave_fence();
 			}
@@ -465,6 +494,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void b
 		step(b, s_hdr0, s_feat0, s_hdr1, s_feat1);
 		if (b + 1 < num_batches) step(b + 1, s_hdr1, s_feat1, s_hdr0, s_feat0);
 	}
+	prefetch_geometry(num_batches - 1);
 	flush_gradients(num_batches - 1);
 }
 
