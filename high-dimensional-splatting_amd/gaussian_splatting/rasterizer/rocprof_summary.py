@@ -6,6 +6,10 @@
         HBM bytes per dispatch from a `--pmc FETCH_SIZE` and a `--pmc WRITE_SIZE` run. Each counter is
         scaled by what it reads for the run's plain device-to-device copy of B bytes (bench.py
         --calibrate-copy-mib), so the figures are in the bytes that copy is known to move.
+    python -m gaussian_splatting.rasterizer.rocprof_summary mfma <label>=<dir> ... [--kernels K ...]
+        matrix-core use per dispatch from `--pmc MfmaUtil MfmaFlopsBF16` runs: the share of cycles the
+        MFMA pipes are busy (rocprofv3's MfmaUtil, percent of SIMD cycles) and the bf16 MFMA rate
+        against MI355X's dense 2.5 PFLOP/s, one row per (label, kernel).
 
 Kernel names are shortened to the function name without template arguments.
 """
@@ -95,6 +99,31 @@ def traffic(fetch_dir: Path, write_dir: Path, copy_bytes: int, kernels: list[str
     return "\n".join(out)
 
 
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def mfma(runs: list[tuple[str, Path]], kernels: list[str]) -> str:
+    out = ["| run | kernel | dispatches | MFMA busy % | bf16 TFLOP/s | of 2.5 PFLOP/s |", "|---|---|---:|---:|---:|---:|"]
+    for label, directory in runs:
+        rows = list(csv.DictReader(open(next(directory.glob("*counter_collection.csv")))))
+        per = collections.defaultdict(lambda: collections.defaultdict(list))
+        for r in rows:
+            k = short_name(r["Kernel_Name"])
+            if kernels and k not in kernels:
+                continue
+            per[k][r["Counter_Name"]].append(float(r["Counter_Value"]))
+            per[k]["ns"].append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+        for k, c in per.items():
+            util, flops = c.get("MfmaUtil", []), c.get("MfmaFlopsBF16", [])
+            if not util or not flops:
+                continue
+            ns = sum(c["ns"]) / len(c["ns"])
+            rate = (sum(flops) / len(flops)) / ns / 1e3  # TFLOP/s
+            out.append(f"| {label} | {k} | {len(util)} | {sum(util) / len(util):.1f} | {rate:.1f} | "
+                       f"{rate / MFMA_BF16_PEAK_TFLOPS:.3f} |")
+    return "\n".join(out)
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -106,9 +135,15 @@ def main(argv=None) -> int:
     f.add_argument("write_dir", type=Path)
     f.add_argument("--copy-bytes", type=int, required=True)
     f.add_argument("--kernels", nargs="*", default=[])
+    m = sub.add_parser("mfma")
+    m.add_argument("runs", nargs="+", help="label=directory")
+    m.add_argument("--kernels", nargs="*", default=[])
     args = ap.parse_args(argv)
     if args.cmd == "trace":
         print(trace(args.dir, args.top))
+    elif args.cmd == "mfma":
+        runs = [(r.split("=", 1)[0], Path(r.split("=", 1)[1])) for r in args.runs]
+        print(mfma(runs, args.kernels))
     else:
         print(traffic(args.fetch_dir, args.write_dir, args.copy_bytes, args.kernels))
     return 0
