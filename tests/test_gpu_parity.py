@@ -332,6 +332,31 @@ def grads_oracle(inputs, width, height, features, grad_image, grad_feat, backgro
     return [dm, dc, dcol, dop, df]
 
 
+@pytest.mark.parametrize("channels", [64, 128])
+def test_reference_feature_entry_points_match_oracle(channels):
+    """The reference extension's rasterize / rasterize_features / rasterize_features_backward sequence
+    (rasterizer/__init__.py:130-165 there), through hds_render_backward with its own zeroing: the
+    feature-only gradients equal the oracle's with a zero image gradient."""
+    width, height = 128, 96
+    m2, d, r, c, col, op = scene(1, 3000, width, height)
+    g = torch.Generator().manual_seed(4)
+    features = torch.rand(3000, channels, generator=g).to(DEV)
+    grad_feat = torch.rand(height, width, channels, generator=g).to(DEV)
+    ext = _get_rasterizer()
+    bg = torch.zeros(3, device=DEV)
+    _, _, _, values, ranges, conic4, color4 = ext.rasterize(m2, d, r, c, col, op, bg, width, height)
+    fimg, fT, fnc = ext.rasterize_features(features, m2, conic4, color4, values, ranges, width, height)
+    got = ext.rasterize_features_backward(grad_feat, features, m2, conic4, color4, values, ranges, fT, fnc, width,
+                                          height, min(channels, 128))
+    want = grads_oracle((m2, d, r, c, col, op), width, height, features, torch.zeros(height, width, 3, device=DEV),
+                        grad_feat, bg)
+    _, want_f, _, _, _, _ = oracle_render((m2, d, r, c, col, op), width, height, features=features)
+    assert_image_close(np_(fimg), want_f, max_error=1e-3, max_perc_99=5e-4)
+    # got = (grad_features, dmeans2D, dconics, dopac); want = (dm, dc, dcol, dop, df)
+    assert_grads_close(("features", "means2D", "conics", "opacities"), [np_(t) for t in got],
+                       [want[4], want[0], want[1], want[3]])
+
+
 @pytest.mark.parametrize("channels,slice_width", [(32, 32), (64, 64), (64, 32), (128, 128), (128, 64), (128, 32),
                                                   (256, 128), (256, 64), (512, 128), (512, 64)])
 def test_backward_matches_oracle(channels, slice_width, monkeypatch):
