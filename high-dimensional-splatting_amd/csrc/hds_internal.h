@@ -206,14 +206,29 @@ __device__ static inline uint32_t hds_opaque(uint32_t v) {
 /* One MFMA result element as an independent 32-bit operand for a lane swap. */
 __device__ static inline uint32_t hds_swap_operand(float v) { return hds_opaque(__builtin_bit_cast(uint32_t, v)); }
 
-/* Tile of a work-group. Work-groups are dispatched round-robin over the 8 XCDs, so the identity
- * order deals consecutive tiles to different XCDs: every XCD gets an even share of the dense centre
- * of the image (mapping contiguous bands of tiles to one XCD left the busiest XCD with 1.33x the mean
- * work at the headline scene). Neighbouring tiles then share gaussians through the memory-side cache
- * rather than one XCD's L2. The grid is a multiple of 8; padding blocks get -1. */
+/* Tile of a work-group. Work-groups are dispatched round-robin over the 8 XCDs, so work-group b
+ * runs on XCD b % 8. The image is cut into 2x2 super-blocks of tiles, dealt to the XCDs round-robin,
+ * and an XCD's consecutive work-groups render the four tiles of one super-block: neighbouring tiles,
+ * which share gaussians, then stage those gaussians through the same L2, while every XCD still gets
+ * an even share of the dense centre (contiguous bands of tiles per XCD left the busiest XCD with 1.33x
+ * the mean work at the headline scene; 4x2 and 4x4 super-blocks were measured slower than 2x2, which
+ * took the blend forward from 0.62 to 0.58 ms). Padding work-groups get -1. */
 #define HDS_XCDS 8
-static inline unsigned hds_xcd_grid(int num_tiles) { return (unsigned)(((num_tiles + HDS_XCDS - 1) / HDS_XCDS) * HDS_XCDS); }
-__device__ static inline int hds_xcd_tile(int block, int num_tiles) { return block < num_tiles ? block : -1; }
+#define HDS_SUPER 2  // super-block edge in tiles
+static inline unsigned hds_xcd_grid(int tiles_x, int num_tiles) {
+	const int tiles_y = num_tiles / tiles_x;
+	const int supers = ((tiles_x + HDS_SUPER - 1) / HDS_SUPER) * ((tiles_y + HDS_SUPER - 1) / HDS_SUPER);
+	return (unsigned)(((supers + HDS_XCDS - 1) / HDS_XCDS) * HDS_XCDS * HDS_SUPER * HDS_SUPER);
+}
+__device__ static inline int hds_xcd_tile(int block, int tiles_x, int num_tiles) {
+	const int tiles_y = num_tiles / tiles_x;
+	const int sx = (tiles_x + HDS_SUPER - 1) / HDS_SUPER, sy = (tiles_y + HDS_SUPER - 1) / HDS_SUPER;
+	const int xcd = block % HDS_XCDS, r = block / HDS_XCDS;
+	const int k = r % (HDS_SUPER * HDS_SUPER), super = (r / (HDS_SUPER * HDS_SUPER)) * HDS_XCDS + xcd;
+	if (super >= sx * sy) return -1;
+	const int tx = (super % sx) * HDS_SUPER + k % HDS_SUPER, ty = (super / sx) * HDS_SUPER + k / HDS_SUPER;
+	return tx < tiles_x && ty < tiles_y ? ty * tiles_x + tx : -1;
+}
 
 /* acc += A * B with A, B given as split-bf16 pairs (small terms first). */
 __device__ static inline hds_f32x4 hds_mfma_split(const hds_bf16x8& a_hi, const hds_bf16x8& a_lo,

@@ -104,7 +104,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void b
 	// Per wave: s and w of the group as rows per position (the B operands of the moment MFMAs).
 	__shared__ __attribute__((aligned(16))) float s_tr[4][2][kGeoGroup * kRowStride];
 
-	const int tile = hds_xcd_tile(blockIdx.x, a.num_tiles);
+	const int tile = hds_xcd_tile(blockIdx.x, a.tiles_x, a.num_tiles);
 	if (tile < 0) return;
 	const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 	const int slice = blockIdx.y;
@@ -553,7 +553,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S >= 128 ? 
 	__shared__ __attribute__((aligned(16))) int s_ggid[4][kFeatGroup];
 	__shared__ int s_max_last;
 
-	const int tile = hds_xcd_tile(blockIdx.x, a.num_tiles);
+	const int tile = hds_xcd_tile(blockIdx.x, a.tiles_x, a.num_tiles);
 	if (tile < 0) return;
 	const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 	const int slice = blockIdx.y;
@@ -692,7 +692,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S >= 128 ? 
 template <int S, bool RGB>
 int launch_geometry(const BackwardArgs& a, int slices, hipStream_t s) {
 	HdsKernelTimer timer1("backward_geometry_kernel", s);
-	backward_geometry_kernel<S, RGB><<<dim3(hds_xcd_grid(a.num_tiles), (unsigned)slices), 256, 0, s>>>(a);
+	backward_geometry_kernel<S, RGB><<<dim3(hds_xcd_grid(a.tiles_x, a.num_tiles), (unsigned)slices), 256, 0, s>>>(a);
 	timer1.stop();
 	return hds_check_launch(RGB ? (S > 0 ? "backward_geometry_rgb_features" : "backward_geometry_rgb")
 								: "backward_geometry_features",
@@ -702,7 +702,7 @@ int launch_geometry(const BackwardArgs& a, int slices, hipStream_t s) {
 template <int S>
 int launch_features(const BackwardArgs& a, int slices, hipStream_t s) {
 	HdsKernelTimer timer2("backward_features_kernel", s);
-	backward_features_kernel<S><<<dim3(hds_xcd_grid(a.num_tiles), (unsigned)slices), 256, 0, s>>>(a);
+	backward_features_kernel<S><<<dim3(hds_xcd_grid(a.tiles_x, a.num_tiles), (unsigned)slices), 256, 0, s>>>(a);
 	timer2.stop();
 	return hds_check_launch("backward_features", s);
 }

@@ -116,7 +116,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S >= 128 ? 
 	__shared__ __attribute__((aligned(16))) float s_feat0[kRows];
 	__shared__ __attribute__((aligned(16))) float s_feat1[kRows];
 
-	const int tile = hds_xcd_tile(blockIdx.x, a.num_tiles);
+	const int tile = hds_xcd_tile(blockIdx.x, a.tiles_x, a.num_tiles);
 	if (tile < 0) return;
 	const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 	const int slice = blockIdx.y;
@@ -286,7 +286,7 @@ write_out:
 template <int S, bool RGB>
 int launch(const RenderArgs& a, int num_tiles, int slices, hipStream_t s) {
 	HdsKernelTimer timer1("render_forward_kernel", s);
-	render_forward_kernel<S, RGB><<<dim3(hds_xcd_grid(num_tiles), (unsigned)slices), 256, 0, s>>>(a);
+	render_forward_kernel<S, RGB><<<dim3(hds_xcd_grid(a.tiles_x, num_tiles), (unsigned)slices), 256, 0, s>>>(a);
 	timer1.stop();
 	return hds_check_launch(RGB ? (S > 0 ? "render_rgb_features" : "render_rgb") : "render_features", s);
 }
