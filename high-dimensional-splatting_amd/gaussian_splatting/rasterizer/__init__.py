@@ -42,7 +42,7 @@ class RasterizeGaussians(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, means2D, depths, radii, conics, colors, opacities, background, features, image_width,
-                image_height):
+                image_height, grad_enabled=False):
         """Bins, then renders the image (and the feature image when features are given) in one walk.
 
         Returns:
@@ -51,9 +51,11 @@ class RasterizeGaussians(torch.autograd.Function):
         ext = _get_rasterizer()
         width, height = int(image_width), int(image_height)
         means2D = means2D.contiguous()
-        # Training (features need a gradient): the gradient buffers are zeroed beside the binning.
+        # Training (features need a gradient and the caller records a graph): the gradient buffers are
+        # zeroed beside the binning. Inside forward grad mode is always off, so the caller's mode
+        # comes in as grad_enabled.
         ctx.prezeroed = None
-        if features is not None and ctx.needs_input_grad[7]:
+        if features is not None and ctx.needs_input_grad[7] and grad_enabled:
             ctx.prezeroed = ext.prezeroed_gradients(means2D.shape[0], int(features.shape[1]), means2D.device)
         # The render is enqueued before the host reads the pair count (the reference's one
         # blocking read, forward.cu:321-325), so the GPU does not idle during that read.
@@ -99,7 +101,7 @@ class RasterizeGaussians(torch.autograd.Function):
             slice_width=(FEATURE_SLICE_WIDTH or default_slice_width(features.shape[1])) if feature_term else None,
             want_feature_grad=feature_term and ctx.needs_input_grad[7], prezeroed=ctx.prezeroed)
         ctx.prezeroed = None
-        return g_means, None, None, g_conics, g_colors, g_opac, None, g_feat, None, None
+        return g_means, None, None, g_conics, g_colors, g_opac, None, g_feat, None, None, None
 
 
 def rasterize(
@@ -144,4 +146,4 @@ def rasterize(
     assert background.shape == (3,)
     assert features is None or (features.ndim == 2 and features.shape[0] == n)
     return RasterizeGaussians.apply(means2D, depths, radii, conics, colors, opacities, background, features,
-                                    image_width, image_height)
+                                    image_width, image_height, torch.is_grad_enabled())

@@ -246,6 +246,40 @@ def test_async_binning_of_a_scene_with_no_pairs():
     assert bins.values.numel() == 0 and int(bins.tile_ranges.abs().sum()) == 0
 
 
+def test_gradient_buffers_are_zeroed_ahead_only_when_a_graph_is_recorded(monkeypatch):
+    """The forward zeroes the backward's gradient buffers on a side stream only when the caller records
+    a graph (not under torch.no_grad(), where no backward can follow), and the backward then gives the
+    same gradients as one that zeroes its own buffers."""
+    wl = synthetic_config(0, n=6000)
+    (m2, d, r, c), _ = project_both(wl.means, wl.scales, wl.quats, wl.opacities, wl.cam)
+    colors = torch.rand(wl.n, 3, generator=torch.Generator().manual_seed(3)).to(DEV)
+    feats = wl.features.to(DEV).requires_grad_(True)
+    opac = wl.opacities.to(DEV)
+    ext = _get_rasterizer()
+    calls = []
+    original = ext.prezeroed_gradients
+    monkeypatch.setattr(ext, "prezeroed_gradients", lambda *args: calls.append(args) or original(*args))
+    with torch.no_grad():
+        rasterize(m2, d, r, c, colors, opac, wl.width, wl.height, features=feats)
+    assert not calls
+    image, fimg = rasterize(m2, d, r, c, colors, opac, wl.width, wl.height, features=feats)
+    assert len(calls) == 1
+    g = torch.Generator().manual_seed(6)
+    gi = torch.rand(image.shape, generator=g).to(DEV)
+    gf = torch.rand(fimg.shape, generator=g).to(DEV)
+    torch.autograd.backward((image, fimg), (gi, gf))
+    ahead = feats.grad.clone()
+    feats.grad = None
+    values, ranges, conic4, color4 = ext.bin(m2, d, r, c, colors, opac, wl.width, wl.height)
+    _, _, T, nc = ext.render(m2, conic4, color4, values, ranges, wl.width, wl.height, torch.zeros(3, device=DEV),
+                             feats.detach())
+    own = ext.render_backward(m2, conic4, color4, values, ranges, T, nc, wl.width, wl.height, grad_image=gi,
+                              background=torch.zeros(3, device=DEV), features=feats.detach(), grad_feature_image=gf,
+                              slice_width=32)[4]
+    scale = own.abs().max().item()
+    assert (ahead - own).abs().max().item() <= 1e-5 * scale
+
+
 def test_rasterize_is_identical_with_and_without_the_pair_count_read():
     # The first call on a fresh binding bins synchronously, later ones bin ahead of the count.
     import gaussian_splatting.rasterizer as rasterizer_module
