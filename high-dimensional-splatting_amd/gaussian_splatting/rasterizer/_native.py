@@ -52,6 +52,7 @@ PROTOTYPES = {
                                               _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "hds_ssim_forward": (_i32, [_i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "hds_ssim_backward": (_i32, [_i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "hds_densification_stats": (_i32, [_i64, _vp, _vp, _i32, _i32, _vp, _vp, _vp, _vp]),
     "hds_profile_begin": (_i32, []),
     "hds_profile_end": (_i64, []),
     "hds_profile_record": (_i32, [_i64, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_float)]),
@@ -517,6 +518,22 @@ class HipRasterizer:
                                                   features=features, grad_feature_image=grad_output,
                                                   slice_width=slice_width)
         return gf, gm, gc, gop
+
+    # -- densification statistics ----------------------------------------------------------------
+
+    def densification_stats(self, grad_means2D, radii, width, height, max_radii2D, grad_accum, denom):
+        """utils/gaussian.py:143-160, in place on max_radii2D [N], grad_accum [N, 1] and denom [N, 1]."""
+        for t, name in ((max_radii2D, "max_radii2D"), (grad_accum, "means2D_grad_accum"), (denom, "denom")):
+            if not (t.is_cuda and t.is_contiguous() and t.dtype == torch.float32):
+                raise RuntimeError(f"{name} must be a contiguous float32 CUDA tensor (updated in place)")
+        grad_means2D, radii = _dev(grad_means2D, "means2D_grad"), _dev(radii, "radii")
+        n = radii.shape[0]
+        if grad_means2D.shape != (n, 2) or max_radii2D.numel() != n or grad_accum.numel() != n or denom.numel() != n:
+            raise RuntimeError("densification statistics need means2D_grad [N,2], radii [N] and [N] / [N,1] buffers")
+        with torch.cuda.device(radii.device):
+            self._run("densification_stats", lambda: self.lib.hds_densification_stats(
+                n, _ptr(grad_means2D), _ptr(radii), int(width), int(height), _ptr(max_radii2D), _ptr(grad_accum),
+                _ptr(denom), _stream(radii.device)))
 
     # -- SSIM -------------------------------------------------------------------------------------
 

@@ -181,6 +181,17 @@ HDS_API int hds_ssim_backward(int height, int width, const float* grad_mean, con
 					  const float* gt, const float* d_mu, const float* d_aa, const float* d_ab,
 					  float* grad_rendered, hds_stream_t stream);
 
+/* ---- densification statistics: replaces GaussianModel.add_densification_stats -------------- */
+
+/* utils/gaussian.py:143-160 for one view, in place, without the host synchronisation of the
+ * reference's boolean indexing: for every gaussian with radii > 0, max_radii2D = max(max_radii2D,
+ * radius), grad_accum += |grad_means2D * (width / 2, height / 2)|, denom += 1. grad_means2D [N,2]
+ * (dL/dmeans2D, the gradient the rasterizer backward produced), radii [N], max_radii2D [N],
+ * grad_accum [N] (the reference's [N,1]), denom [N] ([N,1]). */
+HDS_API int hds_densification_stats(int64_t n, const float* grad_means2D, const float* radii, int width,
+							int height, float* max_radii2D, float* grad_accum, float* denom,
+							hds_stream_t stream);
+
 /* ---- kernel timing (no counterpart in the reference; for benchmarks) ------------------------ */
 
 /* Starts recording: from now on every hot-path kernel launch (projection, blend forward, the two

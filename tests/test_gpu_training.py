@@ -2,8 +2,9 @@
 
 One iteration: project the gaussians for a camera, colour them with eval_sh (whose backward steps
 sh_dc / sh_rest with Adam inside the kernel), rasterize, score with 0.8 L1 + 0.2 (1 - SSIM), backward,
-read means2D.grad for the densification statistics (utils/gaussian.py:143-160), then optimizer.step()
-on the other parameters. The targets are renders of a known scene from four cameras orbiting it; the
+accumulate the densification statistics from means2D.grad (utils/gaussian.py:143-160, on this
+library's fused kernel, checked against the reference's torch formula), then optimizer.step() on the
+other parameters. The targets are renders of a known scene from four cameras orbiting it; the
 trained model starts from a perturbed copy. What is checked is the integration, not a convergence
 rate: every gradient is finite, means2D.grad is non-zero on the visible gaussians and zero on the
 culled ones, the fused SH Adam and torch's Adam both move their parameters, and the loss falls well
@@ -16,6 +17,7 @@ import torch
 import torch.nn.functional as F
 
 from gaussian_splatting.rasterizer import project_gaussians, rasterize
+from gaussian_splatting.utils.densification import DensificationStats
 from gaussian_splatting.utils.loss import l1_loss, psnr, ssim
 from gaussian_splatting.utils.sh import eval_sh, rgb_to_sh
 
@@ -93,6 +95,8 @@ def test_training_iterations_reduce_the_loss(channels):
            "features": 5e-2}
     optimizer = torch.optim.Adam([{"params": [model[k]], "lr": lrs[k], "name": k} for k in model], eps=1e-15,
                                  fused=True)
+    stats = DensificationStats(1500, DEV)
+    ref_accum, ref_denom = torch.zeros(1500, 1, device=DEV), torch.zeros(1500, 1, device=DEV)
     sh_before = model["sh_dc"].detach().clone()
     means_before = model["means"].detach().clone()
 
@@ -118,8 +122,11 @@ def test_training_iterations_reduce_the_loss(channels):
             assert grad2d is not None and torch.isfinite(grad2d).all()
             visible = radii > 0
             # Densification statistics (utils/gaussian.py:143-160): norms of the screen-space gradient.
-            stats = torch.linalg.vector_norm(grad2d[visible], dim=-1)
-            assert torch.isfinite(stats).all() and float(stats.max()) > 0.0
+            stats.add(grad2d, radii, W, H)
+            scale = torch.tensor([0.5 * W, 0.5 * H], device=DEV)
+            ref_accum[visible] += (grad2d * scale)[visible].norm(dim=-1, keepdim=True)
+            ref_denom[visible] += 1
+            assert float(ref_accum.max()) > 0.0
             assert float(grad2d[~visible].abs().sum()) == 0.0
             for name, p in model.items():
                 if name.startswith("sh_"):
@@ -132,6 +139,8 @@ def test_training_iterations_reduce_the_loss(channels):
     with torch.no_grad():
         end = sum(float(loss_of(*render(model, cam, 3)[:2], t)) for cam, t in zip(cams, targets)) / len(cams)
         end_psnr = sum(float(psnr(render(model, cam, 3)[0], t[0])) for cam, t in zip(cams, targets)) / len(cams)
+    torch.testing.assert_close(stats.means2D_grad_accum, ref_accum, rtol=1e-5, atol=0.0)
+    assert torch.equal(stats.denom, ref_denom)
     assert not torch.equal(model["sh_dc"].detach(), sh_before), "the fused SH Adam did not step sh_dc"
     assert not torch.equal(model["means"].detach(), means_before), "torch's Adam did not step the means"
     print(f"loss {start:.4f} -> {end:.4f}, PSNR {start_psnr:.2f} -> {end_psnr:.2f} dB")
