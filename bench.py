@@ -9,16 +9,23 @@ autograd backward of dL/dimage and dL/dfeature_image (both U[0, 1]) through the 
 projection. Colours are a leaf, as in the harness, so SH is not in the timed region.
 
 Prints ONE JSON line: the metric (ms per fwd+bwd, lower is better), the fwd / bwd split measured the
-harness way (events, median), per-stage HIP-event timings taken inside the timed region, the roofline
-of the dominant kernel (render_backward) against MI355X HBM (8 TB/s) and a CPU baseline: the oracle
-(oracle/hds_oracle.c, OpenMP) running the same frame on this host.
+harness way (events around each sample, a pause after each, median; bench/harness.py:130-153), per-stage
+HIP-event timings taken inside the timed region, the roofline of the dominant kernel (render_backward)
+against MI355X HBM (8 TB/s), a CPU baseline: the oracle (oracle/hds_oracle.c, OpenMP) running the same
+frame on this host, and the environment (GPU, clocks and power from amd-smi, source digest).
+
+Like the reference harness, which times only what agrees with its comparison (harness.py:196-208), it
+first checks one fwd+bwd step of this frame against the oracle (images and every leaf gradient within
+the parity tests' bars) and refuses to time a build that disagrees (exit status 1, value null).
 """
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import os
 import statistics
+import subprocess
 import sys
 import time
 from pathlib import Path
@@ -39,7 +46,8 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", type=int, default=2, help="BASELINE.json config index (0-4)")
     ap.add_argument("--channels", type=int, default=None, help="override the config's feature width")
-    ap.add_argument("--no-cpu-baseline", action="store_true", help="skip timing the CPU oracle")
+    ap.add_argument("--no-cpu-baseline", action="store_true",
+                    help="skip the CPU oracle (its timing and the agreement check it provides)")
     ap.add_argument("--no-split", action="store_true", help="skip the separate fwd / bwd median timing")
     ap.add_argument("--frozen-features", action="store_true",
                     help="features without requires_grad: the backward keeps the feature term of the geometry "
@@ -144,6 +152,22 @@ def main() -> int:
     torch.cuda.synchronize()
     print("[bench] warmup done", file=sys.stderr, flush=True)
 
+    # Agreement gate and CPU baseline: the oracle runs the same frame; one GPU step must agree with it.
+    cpu, agreement = None, None
+    if not args.no_cpu_baseline and not args.rgb_only and not args.frozen_features:
+        step()
+        torch.cuda.synchronize()
+        gpu_out = {"image": state["out"][0], "feature_image": state["out"][1],
+                   **{name: leaf.grad for name, leaf in leaves.items()}}
+        gpu_out = {k: v.detach().cpu().numpy() for k, v in gpu_out.items()}
+        cpu, want = cpu_baseline(wl, colors, grad_image, grad_features)
+        agreement = agree(gpu_out, want)
+        print(f"[bench] agreement with the oracle: {agreement}", file=sys.stderr, flush=True)
+        if not agreement["passed"]:
+            print(json.dumps({"metric": METRIC, "value": None, "unit": "ms", "n_gpus": 1,
+                              "error": "disagrees with the oracle; not timed", "agreement": agreement}), flush=True)
+            return 1
+
     # Timed region: exactly `steps` fwd+bwd steps between two device synchronisations, with the
     # library's stage timer recording HIP events around every call on the compute stream.
     timer = StageTimer()
@@ -187,25 +211,32 @@ def main() -> int:
 
     split = {}
     if not args.no_split:
-        # The harness method (bench/harness.py:133-177): events around forward alone, and around
-        # backward alone with an untimed forward before each sample; medians.
-        fwd, bwd = [], []
-        for _ in range(min(args.steps, 20)):
-            reset()
-            torch.cuda.synchronize()
-            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            s.record()
-            forward()
-            e.record()
-            e.synchronize()
-            fwd.append(s.elapsed_time(e))
-            s2, e2 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            s2.record()
-            backward()
-            e2.record()
-            e2.synchronize()
-            bwd.append(s2.elapsed_time(e2))
-        split = {"fwd_ms_median": round(statistics.median(fwd), 4), "bwd_ms_median": round(statistics.median(bwd), 4)}
+        # The harness method (bench/harness.py:130-177): events around forward alone, and around
+        # backward alone with an untimed forward before each sample, a pause of 1.5x the sample after
+        # each, median / min / max, GPU clock and power read before and after.
+        def time_ms(fn, before=None):
+            time.sleep(0.5)
+            start_state = gpu_state()
+            times = []
+            for _ in range(min(args.steps, 20)):
+                if before:
+                    before()
+                torch.cuda.synchronize()
+                s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                s.record()
+                fn()
+                e.record()
+                e.synchronize()
+                times.append(s.elapsed_time(e))
+                time.sleep(max(0.01, 1.5 * times[-1] / 1000))
+            return times, start_state, gpu_state()
+
+        fwd, fwd_start, _ = time_ms(lambda: (reset(), forward()))
+        bwd, _, bwd_end = time_ms(backward, before=lambda: (reset(), forward()))
+        split = {"fwd_ms_median": round(statistics.median(fwd), 4), "bwd_ms_median": round(statistics.median(bwd), 4),
+                 "fwd_ms_min_max": [round(min(fwd), 4), round(max(fwd), 4)],
+                 "bwd_ms_min_max": [round(min(bwd), 4), round(max(bwd), 4)],
+                 "gpu_state_split_start": fwd_start, "gpu_state_split_end": bwd_end}
 
     # Roofline of the blend backward: one hds_render_backward call runs its two kernels (back-to-front
     # geometry/colour gradients, front-to-back feature gradients) side by side on two streams. The
@@ -225,10 +256,6 @@ def main() -> int:
     total_alg = sum(alg.values())
     step_frac = total_alg / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS
 
-    cpu = None
-    if not args.no_cpu_baseline and not args.rgb_only and not args.frozen_features:
-        cpu = cpu_baseline(wl, colors, grad_image, grad_features)
-
     line = {
         "metric": METRIC, "value": round(ms_per_step, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": False, "scaling": "weak",
@@ -240,6 +267,7 @@ def main() -> int:
         "step_ms_median": round(statistics.median(step_ms), 4), **split,
         "step_hbm_frac": round(step_frac, 4), "step_algorithmic_MB": round(total_alg / 1e6, 1),
         "roofline": roofline, "stages": stage_report, "kernels": kernel_report, "cpu_baseline": cpu,
+        "agreement": agreement, "environment": environment(),
     }
     print(json.dumps(line), flush=True)
     if args.calibrate_copy_mib > 0:
@@ -287,8 +315,10 @@ def traffic_per_step(kernel_names) -> int | None:
 
 def cpu_baseline(wl, colors, grad_image, grad_features):
     """The CPU oracle (OpenMP, all host threads) on the same frame: projection, binning, blend forward,
-    blend backward and projection backward, once. Sample = the full frame."""
+    blend backward and projection backward, once. Sample = the full frame. Returns the baseline record
+    and the oracle's outputs in the leaves' shapes (for the agreement gate)."""
     import numpy as np
+    import torch
 
     import oracle
 
@@ -303,18 +333,89 @@ def cpu_baseline(wl, colors, grad_image, grad_features):
     m2, d, r, c = oracle.project_forward(means, scales, quats, opac, np.eye(4), cam["fx"], cam["fy"], cam["cx"],
                                          cam["cy"], cam["width"], cam["height"])
     _, values, ranges = oracle.bin_gaussians(m2, d, r, c, opac, cam["width"], cam["height"])
-    _, T, nc, _ = oracle.render_forward(cam["width"], cam["height"], ranges, values, m2, c, opac, cols,
-                                        np.zeros(3, np.float32), feats)
+    image, T, nc, fimg = oracle.render_forward(cam["width"], cam["height"], ranges, values, m2, c, opac, cols,
+                                               np.zeros(3, np.float32), feats)
     t1 = time.perf_counter()
-    dm, dc, _, _, _ = oracle.render_backward(cam["width"], cam["height"], ranges, values, m2, c, opac, cols,
-                                            np.zeros(3, np.float32), T, nc, gi, feats, gf)
-    oracle.project_backward(dm, dc, means, scales, quats, np.eye(4), cam["fx"], cam["fy"], cam["cx"], cam["cy"],
-                            cam["width"], cam["height"])
+    dm, dc, dcol, dop, df = oracle.render_backward(cam["width"], cam["height"], ranges, values, m2, c, opac, cols,
+                                                   np.zeros(3, np.float32), T, nc, gi, feats, gf)
+    dmeans, dscales, dq = oracle.project_backward(dm, dc, means, scales, quats, np.eye(4), cam["fx"], cam["fy"],
+                                                  cam["cx"], cam["cy"], cam["width"], cam["height"])
     t2 = time.perf_counter()
-    return {"value": round((t2 - t0) * 1e3, 1), "unit": "ms", "cores": oracle.num_threads(), "kind": "port",
-            "fwd_ms": round((t1 - t0) * 1e3, 1), "bwd_ms": round((t2 - t1) * 1e3, 1),
-            "sample": f"one full fwd+bwd frame of {wl.name} (same inputs) on the C oracle, OpenMP",
-            "cpu": _cpu_model()}
+    # The quats leaf goes through F.normalize before the projection: chain its gradient on the CPU.
+    q = wl.quats.detach().clone().requires_grad_(True)
+    torch.nn.functional.normalize(q, dim=-1).backward(torch.from_numpy(np.ascontiguousarray(dq)))
+    want = {"image": image, "feature_image": fimg, "means": dmeans, "scales": dscales, "quats": q.grad.numpy(),
+            "opacities": np.asarray(dop).reshape(-1), "colors": dcol, "features": df}
+    return ({"value": round((t2 - t0) * 1e3, 1), "unit": "ms", "cores": oracle.num_threads(), "kind": "port",
+             "fwd_ms": round((t1 - t0) * 1e3, 1), "bwd_ms": round((t2 - t1) * 1e3, 1),
+             "sample": f"one full fwd+bwd frame of {wl.name} (same inputs) on the C oracle, OpenMP",
+             "cpu": _cpu_model()}, want)
+
+
+# Largest gradient error allowed by the gate, relative to max|want|. The parity tests' 2e-3 holds on
+# their scenes; over the 1.18M gaussians of a full frame a gaussian whose alpha sits exactly on the
+# 1/255 or 0.99 cut can blend on one side and not the other (the reference's assert_grads_close says
+# the same), and its few gradients then differ by up to a few 1e-3.
+GATE_MAX_REL = 1e-2
+
+
+def agree(got: dict, want: dict) -> dict:
+    """The parity tests' bars on this frame: images by max / 99th percentile error, gradients by the
+    share of values outside rtol 1e-3 (< 0.1%) and the largest error relative to max|want|
+    (GATE_MAX_REL)."""
+    from tests.tolerances import grad_error, image_error
+
+    report, passed = {}, True
+    for name, (max_error, max_p99) in (("image", (2e-3, 1e-4)), ("feature_image", (1e-3, 5e-4))):
+        worst, p99 = image_error(got[name], want[name])
+        report[name] = {"max": worst, "p99": p99}
+        passed &= worst < max_error and p99 < max_p99
+    for name in ("means", "scales", "quats", "opacities", "colors", "features"):
+        outside, rel = grad_error(got[name].reshape(want[name].shape), want[name])
+        report[name] = {"outside": outside, "max_rel": rel}
+        passed &= outside < 1e-3 and rel <= GATE_MAX_REL
+    report["passed"] = bool(passed)
+    return report
+
+
+def gpu_state() -> dict:
+    """Mean GFX clock (MHz) over the XCDs and socket power (W) of GPU 0 from amd-smi; {} if unavailable
+    (the reference harness reads clocks and power capping from nvidia-smi, harness.py:117-128)."""
+    try:
+        out = subprocess.run(["amd-smi", "metric", "-g", "0", "--clock", "--power", "--json"], capture_output=True,
+                             text=True, timeout=20, check=True).stdout
+        data = json.loads(out)
+        data = data["gpu_data"] if isinstance(data, dict) and "gpu_data" in data else data
+        data = data[0] if isinstance(data, list) else data
+        clocks = [v["clk"]["value"] for k, v in data.get("clock", {}).items()
+                  if k.startswith("gfx") and isinstance(v.get("clk"), dict)]
+        power = data.get("power", {}).get("socket_power", {})
+        return {"gfx_clock_mhz": round(sum(clocks) / len(clocks), 1) if clocks else None,
+                "socket_power_w": power.get("value") if isinstance(power, dict) else None}
+    except Exception:  # noqa: BLE001 - a missing or differently shaped amd-smi only drops the record
+        return {}
+
+
+def environment() -> dict:
+    """GPU, software and a digest of the HIP sources, like the reference's golden-test environment
+    record (tests/test_golden.py:34-35)."""
+    import torch
+
+    digest = hashlib.sha256()
+    for path in sorted((ROOT / "high-dimensional-splatting_amd" / "csrc").glob("*")) + [ROOT / "include" / "hds_rasterizer.h"]:
+        digest.update(path.read_bytes())
+    name = torch.cuda.get_device_name(0)
+    try:
+        out = subprocess.run(["amd-smi", "static", "-g", "0", "--asic", "--json"], capture_output=True, text=True,
+                             timeout=20, check=True).stdout
+        data = json.loads(out)
+        data = data["gpu_data"] if isinstance(data, dict) and "gpu_data" in data else data
+        data = data[0] if isinstance(data, list) else data
+        name = data["asic"]["market_name"]
+    except Exception:  # noqa: BLE001 - torch's device name stands in
+        pass
+    return {"gpu": name, "torch": torch.__version__, "hip": torch.version.hip, "source": digest.hexdigest()[:16],
+            **gpu_state()}
 
 
 def _cpu_model() -> str:

@@ -15,6 +15,7 @@ import oracle
 from gaussian_splatting.rasterizer import _get_rasterizer, rasterize
 from gaussian_splatting.rasterizer.projection import JACOBIAN_FOV_SCALE, LOW_PASS, NEAR_PLANE
 from tests.scenes import camera, flat_scene, gaussians, synthetic_config
+from tests.tolerances import assert_grads_close, assert_image_close
 
 pytestmark = pytest.mark.gpu
 
@@ -23,27 +24,6 @@ DEV = "cuda"
 
 def np_(t):
     return t.detach().cpu().numpy()
-
-
-def assert_image_close(got, want, max_error=2e-3, max_perc_99=1e-4):
-    diff = np.abs(np.asarray(got, np.float64) - np.asarray(want, np.float64)).ravel()
-    if diff.size == 0:
-        return
-    p99 = np.sort(diff)[max(0, math.ceil(0.99 * diff.size) - 1)]
-    assert diff.max() < max_error and p99 < max_perc_99, f"max {diff.max():.2e}, 99th {p99:.2e}"
-
-
-def assert_grads_close(names, grads, wants):
-    for name, got, want in zip(names, grads, wants):
-        got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
-        assert got.shape == want.shape, f"{name}: shape {got.shape} vs {want.shape}"
-        if want.size == 0:
-            continue
-        scale = np.abs(want).max()
-        bad = ~np.isclose(got, want, rtol=1e-3, atol=1e-4 * scale)
-        assert bad.mean() < 1e-3, f"{name}: {bad.sum()} of {bad.size} outside tolerance"
-        err = np.abs(got - want).max()
-        assert err <= 2e-3 * scale, f"{name}: max error {err:.2e} of max {scale:.2e}"
 
 
 def project_both(wl_means, wl_scales, wl_quats, wl_opac, cam, w2c=None):

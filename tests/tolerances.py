@@ -1,0 +1,45 @@
+"""Agreement bars shared by the GPU parity tests and bench.py's agreement gate.
+
+Images: the reference's assert_image_close (tests/test_render.py:33-38 there): max error and 99th
+percentile of the absolute difference. Gradients: assert_grads_close (test_render.py:45-58 there):
+rtol 1e-3 with an absolute floor of 1e-4 x max|want|, fewer than 0.1% of the values outside, and the
+largest error at most 2e-3 x max|want|.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+
+def image_error(got, want) -> tuple[float, float]:
+    """(max, 99th percentile) of |got - want|."""
+    diff = np.abs(np.asarray(got, np.float64) - np.asarray(want, np.float64)).ravel()
+    if diff.size == 0:
+        return 0.0, 0.0
+    p99 = np.partition(diff, max(0, math.ceil(0.99 * diff.size) - 1))[max(0, math.ceil(0.99 * diff.size) - 1)]
+    return float(diff.max()), float(p99)
+
+
+def assert_image_close(got, want, max_error=2e-3, max_perc_99=1e-4):
+    worst, p99 = image_error(got, want)
+    assert worst < max_error and p99 < max_perc_99, f"max {worst:.2e}, 99th {p99:.2e}"
+
+
+def grad_error(got, want) -> tuple[float, float]:
+    """(share of values outside rtol 1e-3 / atol 1e-4 max, max error / max|want|)."""
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    if want.size == 0:
+        return 0.0, 0.0
+    scale = np.abs(want).max()
+    bad = ~np.isclose(got, want, rtol=1e-3, atol=1e-4 * scale)
+    return float(bad.mean()), float(np.abs(got - want).max() / scale) if scale > 0 else 0.0
+
+
+def assert_grads_close(names, grads, wants):
+    for name, got, want in zip(names, grads, wants):
+        got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+        assert got.shape == want.shape, f"{name}: shape {got.shape} vs {want.shape}"
+        outside, rel = grad_error(got, want)
+        assert outside < 1e-3, f"{name}: {outside:.2%} outside tolerance"
+        assert rel <= 2e-3, f"{name}: max error {rel:.2e} of max |want|"
