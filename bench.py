@@ -56,9 +56,36 @@ def parse_args():
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="after the run, copy a buffer of this many MiB device to device once: the plain copy "
                          "kernel whose FETCH_SIZE / WRITE_SIZE calibrate the --pmc traffic figures")
+    ap.add_argument("--checkpoint", type=Path, default=None,
+                    help="model.pt in the reference's layout (main.py:86-94): render its gaussians instead of the "
+                         "synthetic config, with features U[0, 1] as bench/harness.py:46 does (needs --camera)")
+    ap.add_argument("--camera", type=Path, default=None,
+                    help="JSON camera for --checkpoint (gaussian_splatting.utils.checkpoint.load_camera)")
     ap.add_argument("--bwd-slice", type=int, default=None,
                     help="channels per backward work-group (gaussian_splatting.rasterizer.FEATURE_SLICE_WIDTH)")
-    return ap.parse_args()
+    args = ap.parse_args()
+    if (args.checkpoint is None) != (args.camera is None):
+        ap.error("--checkpoint and --camera go together")
+    return args
+
+
+def checkpoint_workload(checkpoint: Path, camera: Path, channels: int | None):
+    """The frame bench/harness.py:33-56 renders: a trained model's activated gaussians (exp scales,
+    sigmoid opacities, the raw quats as the leaf) seen from one camera, its SH at the checkpoint's
+    active degree, and `channels` (default 128) features U[0, 1] from a seeded generator."""
+    import torch
+
+    from gaussian_splatting.utils.checkpoint import load_camera, load_checkpoint
+    from tests.scenes import Workload
+
+    ckpt, view = load_checkpoint(checkpoint), load_camera(camera)
+    c = 128 if channels is None else channels
+    features = torch.rand(ckpt.n, c, generator=torch.Generator().manual_seed(0))
+    name = f"checkpoint-{checkpoint.stem}-{view.name or 'view'}-{ckpt.n}-{view.width}x{view.height}-c{c}"
+    return Workload(name, ckpt.n, view.width, view.height, view.fx, c, ckpt.means, ckpt.scales,
+                    ckpt.params["quats"], ckpt.opacities, ckpt.params["sh_dc"], ckpt.params["sh_rest"], features,
+                    w2c=view.world_to_camera, intrinsics=(view.fx, view.fy, view.cx, view.cy),
+                    sh_degree=ckpt.active_sh_degree)
 
 
 def algorithmic_bytes(n: int, n_vis: int, pairs: int, hw: int, c: int) -> dict[str, float]:
@@ -95,18 +122,22 @@ def main() -> int:
         return 2
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    wl = synthetic_config(args.config, channels=args.channels)
+    if args.checkpoint is not None:
+        wl = checkpoint_workload(args.checkpoint, args.camera, args.channels)
+    else:
+        wl = synthetic_config(args.config, channels=args.channels)
     cam = wl.cam
     W, H, C, N = wl.width, wl.height, wl.channels, wl.n
     print(f"[bench] {wl.name}: N={N} {W}x{H} C={C}", file=sys.stderr, flush=True)
     wl_dev = wl.to(dev)
-    w2c = torch.eye(4, device=dev)
+    w2c = wl_dev.world_to_camera.contiguous()
 
     # Colours are a leaf computed once under no_grad, as in bench/harness.py:33-56.
     with torch.no_grad():
         _, _, radii0, _ = project_gaussians(wl_dev.means, wl_dev.scales, wl_dev.quats, wl_dev.opacities, w2c,
                                             cam["fx"], cam["fy"], cam["cx"], cam["cy"], W, H)
-        colors = eval_sh(wl_dev.sh_dc, wl_dev.sh_rest, view_dirs(wl_dev.means), 3, radii0, None)
+        colors = eval_sh(wl_dev.sh_dc, wl_dev.sh_rest, view_dirs(wl_dev.means, wl_dev.center), wl.sh_degree,
+                         radii0, None)
     leaves = {
         "means": wl_dev.means.clone().requires_grad_(True),
         "scales": wl_dev.scales.clone().requires_grad_(True),
@@ -328,9 +359,10 @@ def cpu_baseline(wl, colors, grad_image, grad_features):
     quats = np_(wl.quats / wl.quats.norm(dim=-1, keepdim=True))
     opac, feats = np_(wl.opacities), np_(wl.features)
     cols, gi, gf = np_(colors), np_(grad_image), np_(grad_features)
+    w2c = np_(wl.world_to_camera).astype(np.float32)
     print("[bench] cpu baseline: oracle fwd+bwd of the full frame", file=sys.stderr, flush=True)
     t0 = time.perf_counter()
-    m2, d, r, c = oracle.project_forward(means, scales, quats, opac, np.eye(4), cam["fx"], cam["fy"], cam["cx"],
+    m2, d, r, c = oracle.project_forward(means, scales, quats, opac, w2c, cam["fx"], cam["fy"], cam["cx"],
                                          cam["cy"], cam["width"], cam["height"])
     _, values, ranges = oracle.bin_gaussians(m2, d, r, c, opac, cam["width"], cam["height"])
     image, T, nc, fimg = oracle.render_forward(cam["width"], cam["height"], ranges, values, m2, c, opac, cols,
@@ -338,7 +370,7 @@ def cpu_baseline(wl, colors, grad_image, grad_features):
     t1 = time.perf_counter()
     dm, dc, dcol, dop, df = oracle.render_backward(cam["width"], cam["height"], ranges, values, m2, c, opac, cols,
                                                    np.zeros(3, np.float32), T, nc, gi, feats, gf)
-    dmeans, dscales, dq = oracle.project_backward(dm, dc, means, scales, quats, np.eye(4), cam["fx"], cam["fy"],
+    dmeans, dscales, dq = oracle.project_backward(dm, dc, means, scales, quats, w2c, cam["fx"], cam["fy"],
                                                   cam["cx"], cam["cy"], cam["width"], cam["height"])
     t2 = time.perf_counter()
     # The quats leaf goes through F.normalize before the projection: chain its gradient on the CPU.

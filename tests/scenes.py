@@ -48,11 +48,24 @@ class Workload:
     sh_dc: torch.Tensor
     sh_rest: torch.Tensor
     features: torch.Tensor
+    w2c: torch.Tensor | None = None  # [4, 4] world-to-camera; the identity when None
+    intrinsics: tuple[float, float, float, float] | None = None  # (fx, fy, cx, cy); centred `focal` when None
+    sh_degree: int = 3
 
     @property
     def cam(self) -> dict:
-        return {"fx": self.focal, "fy": self.focal, "cx": self.width / 2, "cy": self.height / 2,
-                "width": self.width, "height": self.height}
+        fx, fy, cx, cy = self.intrinsics or (self.focal, self.focal, self.width / 2, self.height / 2)
+        return {"fx": fx, "fy": fy, "cx": cx, "cy": cy, "width": self.width, "height": self.height}
+
+    @property
+    def world_to_camera(self) -> torch.Tensor:
+        return torch.eye(4, device=self.means.device) if self.w2c is None else self.w2c
+
+    @property
+    def center(self) -> torch.Tensor:
+        """Camera position in world space: -R^T t."""
+        m = self.world_to_camera
+        return -(m[:3, :3].T @ m[:3, 3])
 
     def to(self, device) -> "Workload":
         fields = {k: (v.to(device) if isinstance(v, torch.Tensor) else v) for k, v in self.__dict__.items()}
