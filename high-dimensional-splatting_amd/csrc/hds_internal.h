@@ -244,22 +244,49 @@ __device__ static inline hds_f32x4 hds_mfma_split(const hds_bf16x8& a_hi, const 
 /* Blend helpers shared by the forward and backward tile walks.                                 */
 /* ------------------------------------------------------------------------------------------- */
 
-/* Conservative culling box of one gaussian: the alpha extent widened by 0.1% + 0.01 px so
- * rounding differences in the per-pixel exp never cull a gaussian some pixel still accepts; a
- * degenerate (NaN) extent keeps the gaussian (features.cu:8-17 does the same). */
-__device__ static inline float4 hds_cull_box(float2 mean, float4 conic_op) {
-	float ex, ey;
-	hds_alpha_extent(conic_op.x, conic_op.y, conic_op.z, conic_op.w, &ex, &ey);
-	ex = ex * 1.001f + 0.01f;
-	ey = ey * 1.001f + 0.01f;
-	if (!(ex >= 0.0f)) ex = 1e30f;
-	if (!(ey >= 0.0f)) ey = 1e30f;
-	return make_float4(mean.x - ex, mean.x + ex, mean.y - ey, mean.y + ey);
-}
-
-/* Does the box reach the rectangle [x0, x1] x [y0, y1] of pixel centres? */
-__device__ static inline bool hds_box_hits(float4 box, float x0, float x1, float y0, float y1) {
-	return box.y >= x0 && box.x <= x1 && box.w >= y0 && box.z <= y1;
+/* Can the gaussian reach alpha >= 1/255 anywhere in the rectangle [x0, x1] x [y0, y1] of pixel
+ * centres? A conservative cull: it only drops gaussians whose alpha is below 1/255 at every pixel
+ * of the rectangle, which the per-pixel test (forward.cu:207-208) would skip anyway, so no pixel's
+ * result changes (features.cu:8-22 culls with the looser bounding box of the same ellipse).
+ *
+ * alpha = op exp(-q / 2) >= 1/255 needs q <= 2 ln(255 op), with q(d) = a dx^2 + 2 b dx dy + c dy^2
+ * and d = pixel - mean. q is convex (a > 0, ac - b^2 > 0), so over the rectangle it is 0 when the
+ * mean lies inside and otherwise smallest on one of the four edges, where it is a quadratic in one
+ * variable, minimised at the clamped stationary point. On an edge dx = e it is evaluated as
+ * c (dy + b e / c)^2 + (det / c) e^2, a sum of non-negative terms with no cancellation.
+ *
+ * The margin covers the rounding of the per-pixel q, whose terms can cancel for elongated
+ * gaussians: 1e-5 of the largest term magnitude over the rectangle (the fp32 error of the
+ * per-pixel form is below 1e-6 of it), plus 0.1% of the threshold and 0.01 for the exp and log.
+ * Degenerate or NaN input keeps the gaussian. */
+__device__ static inline bool hds_block_reach(float2 mean, float4 conic_op, float x0, float x1, float y0, float y1) {
+	const float a = conic_op.x, b = conic_op.y, c = conic_op.z;
+	const float det = a * c - b * b;
+	const float thr = (2.0f * 0.693147182f) * __builtin_amdgcn_logf(255.0f * conic_op.w);
+	const float lx = x0 - mean.x, hx = x1 - mean.x, ly = y0 - mean.y, hy = y1 - mean.y;
+	if (!(a > 0.0f && c > 0.0f && det > 0.0f)) return true;
+	if (lx <= 0.0f && hx >= 0.0f && ly <= 0.0f && hy >= 0.0f) return true;
+	const float ia = __builtin_amdgcn_rcpf(a), ic = __builtin_amdgcn_rcpf(c);
+	float qmin = 3.0e38f;
+	// Vertical edges dx = e: dy* = -b e / c clamped to [ly, hy].
+#pragma unroll
+	for (int k = 0; k < 2; k++) {
+		const float e = k ? hx : lx;
+		const float dy = fminf(fmaxf(-b * e * ic, ly), hy);
+		const float t = dy + b * e * ic;
+		qmin = fminf(qmin, c * t * t + det * ic * e * e);
+	}
+	// Horizontal edges dy = e: dx* = -b e / a clamped to [lx, hx].
+#pragma unroll
+	for (int k = 0; k < 2; k++) {
+		const float e = k ? hy : ly;
+		const float dx = fminf(fmaxf(-b * e * ia, lx), hx);
+		const float t = dx + b * e * ia;
+		qmin = fminf(qmin, a * t * t + det * ia * e * e);
+	}
+	const float mx2 = fmaxf(lx * lx, hx * hx), my2 = fmaxf(ly * ly, hy * hy);
+	const float margin = 1e-5f * ((a + fabsf(b)) * mx2 + (c + fabsf(b)) * my2) + 1e-3f * fabsf(thr) + 0.01f;
+	return !(qmin > thr + margin);
 }
 
 /* Raw alpha of a gaussian at a pixel centre, forward.cu:197-208; G and the offsets are returned

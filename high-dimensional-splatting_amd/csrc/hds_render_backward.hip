@@ -310,8 +310,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void b
 		if (batch_start < wave_last) {
 			bool box_hit = false;
 			if (lane < cnt && batch_start + lane < wave_last) {
-				const float4 box = hds_cull_box(make_float2(h.mx[lane], h.my[lane]), h.conic[lane]);
-				box_hit = hds_box_hits(box, rx0, rx1, ry0, ry1);
+				box_hit = hds_block_reach(make_float2(h.mx[lane], h.my[lane]), h.conic[lane], rx0, rx1, ry0, ry1);
 			}
 			uint64_t hits = hds_ballot(box_hit);
 			while (hits) {
@@ -629,8 +628,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S >= 128 ? 
 		if (batch < wave_last) {
 			bool box_hit = false;
 			if (lane < cnt && batch + lane < wave_last) {
-				const float4 box = hds_cull_box(make_float2(h.mx[lane], h.my[lane]), h.conic[lane]);
-				box_hit = hds_box_hits(box, rx0, rx1, ry0, ry1);
+				box_hit = hds_block_reach(make_float2(h.mx[lane], h.my[lane]), h.conic[lane], rx0, rx1, ry0, ry1);
 			}
 			// Lane i holds the gaussian of batch slot i (read by the row bookkeeping below).
 			const int slot_gid = lane < cnt ? bgid[lane] : -1;

@@ -174,8 +174,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S >= 128 ? 
 				const int batch = b * kBatch;
 				bool box_hit = false;
 				if (lane < cnt) {
-					const float4 box = hds_cull_box(make_float2(h.mx[lane], h.my[lane]), h.conic[lane]);
-					box_hit = hds_box_hits(box, rx0, rx1, ry0, ry1);
+					box_hit = hds_block_reach(make_float2(h.mx[lane], h.my[lane]), h.conic[lane], rx0, rx1, ry0, ry1);
 				}
 				uint64_t hits = hds_ballot(box_hit);
 				while (hits) {
