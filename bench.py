@@ -410,9 +410,18 @@ def agree(got: dict, want: dict) -> dict:
     return report
 
 
+def _profiled() -> bool:
+    """True under rocprofv3, whose tool library is loaded into child processes too: amd-smi (a
+    script started through env) is then not run, so no child re-executes after GPU initialisation."""
+    return any(k.startswith(("ROCPROF_", "ROCPROFILER_")) for k in os.environ)
+
+
 def gpu_state() -> dict:
     """Mean GFX clock (MHz) over the XCDs and socket power (W) of GPU 0 from amd-smi; {} if unavailable
-    (the reference harness reads clocks and power capping from nvidia-smi, harness.py:117-128)."""
+    or under a profiler (the reference harness reads clocks and power capping from nvidia-smi,
+    harness.py:117-128)."""
+    if _profiled():
+        return {}
     try:
         out = subprocess.run(["amd-smi", "metric", "-g", "0", "--clock", "--power", "--json"], capture_output=True,
                              text=True, timeout=20, check=True).stdout
@@ -438,6 +447,8 @@ def environment() -> dict:
         digest.update(path.read_bytes())
     name = torch.cuda.get_device_name(0)
     try:
+        if _profiled():
+            raise RuntimeError("amd-smi is not run under a profiler")
         out = subprocess.run(["amd-smi", "static", "-g", "0", "--asic", "--json"], capture_output=True, text=True,
                              timeout=20, check=True).stdout
         data = json.loads(out)

@@ -423,13 +423,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void b
 					}
 				}
 				if (!active) continue;
-	#pragma unroll
-				for (int q = 0; q < kGeoGroup; q++) {
-					if (q >= count) {
-						tr_s[q * kRowStride + lane] = 0.0f;
-						if (do_rgb) tr_w[q * kRowStride + lane] = 0.0f;
-					}
-				}
+				// Rows of positions past count are stale: they only reach their own output columns,
+				// which nobody reads.
 				hds_wave_fence();
 
 				// mom[j][position] = sum_px P^T[j][px] s[px][position]; B lane = (pixels 32kk + 8(lane / 16)
