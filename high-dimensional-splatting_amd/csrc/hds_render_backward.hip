@@ -497,7 +497,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void b
 // holds the gaussian of row r (-1 for padding rows); gids: the wave's 32-int LDS scratch.
 template <int S>
 __device__ inline void flush_features(const hds_bf16x8 (&gb_hi)[4][S / 32], const hds_bf16x8 (&gb_lo)[4][S / 32],
-									  const uint32_t* rows, int gid_row, int* gids, float* grad_features, int channels,
+									  const uint32_t* rows, int gid_row, int* gids, float* grad_features, int channels_log2,
 									  int c0, int lane) {
 	if (lane < kFeatGroup) gids[lane] = gid_row;
 	hds_wave_fence();
@@ -511,25 +511,26 @@ __device__ inline void flush_features(const hds_bf16x8 (&gb_hi)[4][S / 32], cons
 		const uint32_t d[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
 		hds_unpack8(d, a_hi[kp], a_lo[kp]);
 	}
+	// D rows = positions 8(i / 4) + 4(lane / 32) + i % 4: their gaussians, read once for all channel
+	// blocks (a row's address is formed once; channel block cb is the atomic's constant offset).
+	int gid[16];
+#pragma unroll
+	for (int g = 0; g < 4; g++) {
+		const int4 v = *reinterpret_cast<const int4*>(gids + 8 * g + 4 * (lane >> 5));
+		gid[4 * g + 0] = v.x;
+		gid[4 * g + 1] = v.y;
+		gid[4 * g + 2] = v.z;
+		gid[4 * g + 3] = v.w;
+	}
+	float* const base = grad_features + c0 + (lane & 31);
 #pragma unroll
 	for (int cb = 0; cb < S / 32; cb++) {
 		hds_f32x16 acc = {};
 #pragma unroll
 		for (int kp = 0; kp < 4; kp++) acc = hds_mfma32_split(a_hi[kp], a_lo[kp], gb_hi[kp][cb], gb_lo[kp][cb], acc);
-		// D rows = positions 8(i / 4) + 4(lane / 32) + i % 4.
-		int gid[16];
-#pragma unroll
-		for (int g = 0; g < 4; g++) {
-			const int4 v = *reinterpret_cast<const int4*>(gids + 8 * g + 4 * (lane >> 5));
-			gid[4 * g + 0] = v.x;
-			gid[4 * g + 1] = v.y;
-			gid[4 * g + 2] = v.z;
-			gid[4 * g + 3] = v.w;
-		}
-		float* dst = grad_features + c0 + 32 * cb + (lane & 31);
 #pragma unroll
 		for (int i = 0; i < 16; i++)
-			if (gid[i] >= 0) atomicAdd(dst + (int64_t)gid[i] * channels, acc[i]);
+			if (gid[i] >= 0) atomicAdd(base + ((uint64_t)(uint32_t)gid[i] << channels_log2) + 32 * cb, acc[i]);
 	}
 	hds_wave_fence();
 }
@@ -559,6 +560,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S >= 128 ? 
 	const float rx0 = (float)wx0 + 0.5f, rx1 = (float)wx0 + 7.5f;
 	const float ry0 = (float)wy0 + 0.5f, ry1 = (float)wy0 + 7.5f;
 	const int c0 = slice * S;
+	const int channels_log2 = 31 - __builtin_clz((unsigned)a.channels);  // a power of two (32-512)
 	const int last = inside ? a.n_contrib[(int64_t)py * a.width + px] : 0;
 
 	// dL/dF, the B operand with K = pixels, for pixel steps kp = 0..3:
@@ -566,16 +568,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S >= 128 ? 
 	hds_bf16x8 gb_hi[4][kNcb], gb_lo[4][kNcb];
 #pragma unroll
 	for (int kp = 0; kp < 4; kp++) {
+		// The 8 pixels of this step: row 2 kp + lane / 32 of the block (zero outside the image).
+		const int y = wy0 + 2 * kp + (lane >> 5);
+		const float* src = a.grad_feature_image + (((int64_t)y * a.width + wx0) << channels_log2) + c0 + (lane & 31);
 #pragma unroll
 		for (int cb = 0; cb < kNcb; cb++) {
 			float v[8];
 #pragma unroll
 			for (int j = 0; j < 8; j++) {
-				const int p = 16 * kp + 8 * (lane >> 5) + j;
-				const int x = wx0 + (p & 7), y = wy0 + (p >> 3);
 				v[j] = 0.0f;
-				if (x < a.width && y < a.height)
-					v[j] = a.grad_feature_image[((int64_t)y * a.width + x) * a.channels + c0 + 32 * cb + (lane & 31)];
+				if (wx0 + j < a.width && y < a.height) v[j] = src[((int64_t)j << channels_log2) + 32 * cb];
 			}
 			uint32_t h[4], l[4];
 #pragma unroll
@@ -607,7 +609,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S >= 128 ? 
 		__syncthreads();
 	}
 	auto flush = [&]() {
-		flush_features<S>(gb_hi, gb_lo, rows, (lane & 31) < q ? gid_row : -1, gids, a.grad_features, a.channels, c0,
+		flush_features<S>(gb_hi, gb_lo, rows, (lane & 31) < q ? gid_row : -1, gids, a.grad_features, channels_log2, c0,
 						  lane);
 		q = 0;
 	};
@@ -659,7 +661,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S >= 128 ? 
 					}
 					// A gaussian no pixel of the block takes gets no row (and no atomics).
 					if (hds_ballot(contributes) != 0) {
-						rows[q * kRowStride + lane] = hds_split_pack(w);
+						s_w[wave][q * kRowStride + lane] = hds_split_pack(w);
 						const int g = __builtin_amdgcn_readlane(slot_gid, slot[u]);
 						if ((lane & 31) == q) gid_row = g;
 						q = __builtin_amdgcn_readfirstlane(q + 1);

@@ -39,6 +39,9 @@ class ProjectGaussians(torch.autograd.Function):
         ctx.save_for_backward(means, scales, quats, world_to_camera)
         ctx.camera = (fx, fy, cx, cy, width, height)
         ctx.mark_non_differentiable(outputs[1], outputs[2])
+        # Gradients of outputs the loss does not reach arrive as None instead of zero tensors
+        # (depths and radii never have one; filling them would cost two N-sized writes per step).
+        ctx.set_materialize_grads(False)
         return outputs
 
     @staticmethod

@@ -99,6 +99,8 @@ def synthetic_config(index: int, channels: int | None = None, n: int | None = No
     sh_rest = 0.05 * torch.randn(n, 15, 3, generator=g)
     gf = torch.Generator().manual_seed(1)
     features = torch.randn(n, c, generator=gf)
+    if c != CONFIGS[index][5]:
+        name = name.rsplit("-c", 1)[0] + f"-c{c}"  # the name states the channel count actually used
     return Workload(name, n, w, h, f, c, means, scales, quats, opacities, sh_dc, sh_rest, features)
 
 
