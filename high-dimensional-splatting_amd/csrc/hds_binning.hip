@@ -558,17 +558,38 @@ __global__ __launch_bounds__(kThreads) void zero_kernel(uint32_t* __restrict__ a
 		b[i - na] = 0u;
 }
 
-// [start, end) of each tile in the sorted pair list (forward.cu:115-139).
+// [start, end) of each tile in the sorted pair list (forward.cu:115-139): a pair starts its tile's
+// range where the key before it differs and ends it where the key after it differs. A thread takes
+// kRangeItems consecutive pairs with two 16-byte loads (keys are 256-byte aligned), plus the keys
+// on either side.
+constexpr int kRangeItems = 8;
 __global__ __launch_bounds__(kThreads) void ranges_kernel(int64_t num_pairs, const uint64_t* __restrict__ pairs_total,
 														   const uint32_t* __restrict__ tile_keys, int64_t num_tiles,
 														   int2* __restrict__ ranges) {
-	const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+	const int64_t p0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * kRangeItems;
 	num_pairs = device_count(pairs_total, num_pairs);
-	if (p >= num_pairs) return;
-	const uint32_t t = tile_keys[p];
-	if (t >= num_tiles) return;
-	if (p == 0 || tile_keys[p - 1] != t) ranges[t].x = (int)p;
-	if (p == num_pairs - 1 || tile_keys[p + 1] != t) ranges[t].y = (int)(p + 1);
+	if (p0 >= num_pairs) return;
+	// k[j] = key of pair p0 - 1 + j; outside [0, num_pairs) a value no tile has.
+	constexpr uint32_t kNone = 0xffffffffu;
+	uint32_t k[kRangeItems + 2];
+	k[0] = p0 > 0 ? tile_keys[p0 - 1] : kNone;
+	if (p0 + kRangeItems <= num_pairs && (reinterpret_cast<uintptr_t>(tile_keys) & 15u) == 0) {
+		const uint4 a = *reinterpret_cast<const uint4*>(tile_keys + p0);
+		const uint4 b = *reinterpret_cast<const uint4*>(tile_keys + p0 + 4);
+		k[1] = a.x; k[2] = a.y; k[3] = a.z; k[4] = a.w;
+		k[5] = b.x; k[6] = b.y; k[7] = b.z; k[8] = b.w;
+	} else {
+#pragma unroll
+		for (int i = 0; i < kRangeItems; i++) k[i + 1] = p0 + i < num_pairs ? tile_keys[p0 + i] : kNone;
+	}
+	k[kRangeItems + 1] = p0 + kRangeItems < num_pairs ? tile_keys[p0 + kRangeItems] : kNone;
+#pragma unroll
+	for (int i = 0; i < kRangeItems; i++) {
+		const uint32_t t = k[i + 1];
+		if (t >= num_tiles) continue;  // also every position past num_pairs
+		if (k[i] != t) ranges[t].x = (int)(p0 + i);
+		if (k[i + 2] != t) ranges[t].y = (int)(p0 + i + 1);
+	}
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -782,7 +803,7 @@ int bin_emit_launch(int64_t n, int64_t num_pairs, bool exact, int width, int hei
 	if (st != HDS_OK) return st;
 	const uint32_t* keys_sorted = (passes % 2 == 0) ? keys_a : keys_b;
 	HdsKernelTimer timer3("ranges_kernel", s);
-	ranges_kernel<<<hds_blocks(num_pairs, kThreads), kThreads, 0, s>>>(num_pairs, total, keys_sorted, num_tiles,
+	ranges_kernel<<<hds_blocks((num_pairs + kRangeItems - 1) / kRangeItems, kThreads), kThreads, 0, s>>>(num_pairs, total, keys_sorted, num_tiles,
 																		reinterpret_cast<int2*>(tile_ranges));
 	timer3.stop();
 	HDS_LAUNCH_CHECK("identify_tile_ranges", s);
