@@ -32,7 +32,6 @@ constexpr int kWaveItems = kTileItems / kWaves;         // a wave ranks 16 rows 
 constexpr int kRadixBits = 8;
 constexpr int kRadix = 1 << kRadixBits;
 constexpr int kMaxPasses = 4;                           // 32-bit keys
-constexpr int kEmitCache = 4096;                        // depth-ordered offsets one emit work-group caches
 // Copies of each global digit histogram: producers add into copy (block mod kHistCopies), so that
 // no histogram word takes more than ~1/16 of the producers' atomics; passes sum the copies.
 constexpr int kHistCopies = 16;
@@ -427,123 +426,69 @@ __global__ __launch_bounds__(kThreads) void prepare_kernel(
 	flush_digits(kMaxPasses, s_hist, hist);
 }
 
-// Last depth-ordered entry in [lo, hi] whose offset is <= target (gaussians with no tiles share
-// their successor's offset, so the owner of a pair is never one of them).
-__device__ inline int64_t owner_of(const uint32_t* __restrict__ offsets, int64_t lo, int64_t hi, uint32_t target) {
-	while (lo < hi) {
-		const int64_t mid = (lo + hi + 1) >> 1;
-		if (offsets[mid] <= target)
-			lo = mid;
-		else
-			hi = mid - 1;
-	}
-	return lo;
-}
-
-// owner_of over the whole depth order, by one wave: each round the 64 lanes probe 64 evenly spaced
-// entries of the remaining range [lo, hi] and keep the last one whose offset is <= target, so the
-// range shrinks 64-fold per memory latency (4 rounds for a million gaussians instead of 21
-// dependent loads). offsets[0] = 0 <= target keeps lane 0's probe valid.
-__device__ inline int64_t wave_owner_of(const uint32_t* __restrict__ offsets, int64_t n, uint32_t target) {
-	const int lane = threadIdx.x & (HDS_WAVE - 1);
-	int64_t lo = 0, hi = n - 1;
-	while (hi - lo >= HDS_WAVE) {
-		const int64_t step = (hi - lo + HDS_WAVE) / HDS_WAVE;  // 64 probes cover [lo, hi]
-		const int64_t idx = lo + lane * step;
-		const uint64_t ok = hds_ballot(idx <= hi && offsets[idx <= hi ? idx : hi] <= target);
-		const int64_t found = lo + (int64_t)(63 - __builtin_clzll(ok)) * step;
-		// The owner lies before the next probe, which failed or lies past hi.
-		hi = found + step - 1 < hi ? found + step - 1 : hi;
-		lo = found;
-	}
-	const int64_t idx = lo + lane;
-	const uint64_t ok = hds_ballot(idx <= hi && offsets[idx <= hi ? idx : hi] <= target);
-	return lo + (63 - __builtin_clzll(ok));
-}
-
-// Pairs [4096 b, 4096 b + 4096) per work-group, in depth order; tiles are enumerated row-major
-// inside each gaussian's rectangle (forward.cu:63-113). The owners of a work-group's pairs are a
-// contiguous run of the depth order, so their offsets are cached in LDS; the 16 rows of a thread
-// go through the owner search, the loads and the stores phase by phase, so each phase has 16
-// independent accesses in flight. Also counts the tile keys' digits for the pair sort.
-// order / rects_sorted: gaussian id and tile rectangle of each depth-ordered entry. With
-// pairs_total the grid covers num_pairs pairs and the count is read on the device.
+// Pair emission (forward.cu:63-113): the pairs of gaussian g are [offsets[g], offsets[g] + w * h),
+// tile (x0 + local % w, y0 + local / w) for local = 0 .. w * h - 1, in depth order. A wave takes 64
+// consecutive depth-ordered gaussians, whose pairs are one contiguous run of the output; lane l
+// writes pairs run_start + l, + 64, ... (coalesced), finding each pair's gaussian as the last of
+// the wave's 64 whose offset is <= the pair index (gaussians with no tiles share their successor's
+// offset, so they never own a pair) by binary search over the offsets in LDS, and reading that
+// gaussian's record from its lane. Also counts the tile keys' digits for the pair sort. order /
+// rects_sorted: gaussian id and tile rectangle of each depth-ordered entry. With pairs_total the
+// pair count is read on the device and pairs past it are not written.
 __global__ __launch_bounds__(kThreads) void emit_kernel(int64_t n, int64_t num_pairs, const uint64_t* __restrict__ pairs_total,
 														 const uint32_t* __restrict__ offsets,
 														 const uint32_t* __restrict__ order,
 														 const uint2* __restrict__ rects_sorted, int tiles_x,
 														 int passes, uint32_t* __restrict__ tile_keys,
 														 uint32_t* __restrict__ gids, uint32_t* __restrict__ hist) {
-	__shared__ uint32_t s_off[kEmitCache];
+	__shared__ uint32_t s_off[kWaves][HDS_WAVE];
 	__shared__ uint32_t s_hist[kMaxPasses][kRadix];
-	__shared__ int64_t s_range[2];
-	const int t = threadIdx.x;
-	const int64_t base = (int64_t)blockIdx.x * kTileItems;
+	const int t = threadIdx.x, lane = t & (HDS_WAVE - 1), wave = t / HDS_WAVE;
 	num_pairs = device_count(pairs_total, num_pairs);
-	if (base >= num_pairs) return;
-	const int64_t last = (base + kTileItems < num_pairs ? base + kTileItems : num_pairs) - 1;
-	if (t < 2 * HDS_WAVE) {
-		const int64_t g = wave_owner_of(offsets, n, (uint32_t)(t < HDS_WAVE ? base : last));
-		if ((t & (HDS_WAVE - 1)) == 0) s_range[t / HDS_WAVE] = g;
-	}
 #pragma unroll
 	for (int p = 0; p < kMaxPasses; p++) s_hist[p][t] = 0;
 	__syncthreads();
-	const int64_t g0 = s_range[0], g1 = s_range[1];
-	const bool cached = g1 - g0 < kEmitCache;
-	if (cached)
-		for (int64_t g = g0 + t; g <= g1; g += kThreads) s_off[g - g0] = offsets[g];
-	__syncthreads();
 
-	int64_t owner[kItemsPerThread];
-	uint32_t off[kItemsPerThread];
-	if (cached) {
-		// Largest index in [0, g1 - g0] whose cached offset is <= the pair index, 12 fixed steps.
-		const int top = (int)(g1 - g0);
-		int lo[kItemsPerThread];
-#pragma unroll
-		for (int r = 0; r < kItemsPerThread; r++) lo[r] = 0;
-#pragma unroll
-		for (int step = kEmitCache / 2; step > 0; step >>= 1) {
-#pragma unroll
-			for (int r = 0; r < kItemsPerThread; r++) {
-				const uint32_t target = (uint32_t)(base + r * kThreads + t);
-				const int cand = lo[r] + step;
-				if (cand <= top && s_off[cand] <= target) lo[r] = cand;
-			}
-		}
-#pragma unroll
-		for (int r = 0; r < kItemsPerThread; r++) {
-			owner[r] = g0 + lo[r];
-			off[r] = s_off[lo[r]];
-		}
-	} else {
-		for (int r = 0; r < kItemsPerThread; r++) {
-			const int64_t p = base + r * kThreads + t;
-			owner[r] = p < num_pairs ? owner_of(offsets, g0, g1, (uint32_t)p) : g0;
-			off[r] = offsets[owner[r]];
-		}
+	const int64_t first = ((int64_t)blockIdx.x * kWaves + wave) * HDS_WAVE;
+	const int64_t g = first + lane;
+	const bool real = g < n;
+	uint32_t off = 0, cnt = 0, gid = 0;
+	uint2 rc = make_uint2(0u, 0u);
+	if (real) {
+		off = offsets[g];
+		rc = rects_sorted[g];
+		cnt = (rc.y & 0xffffu) * (rc.y >> 16);
+		gid = order[g];
 	}
-	uint32_t gid[kItemsPerThread];
-	uint2 rc[kItemsPerThread];
+	// The wave's run [run_start, run_end): from its first gaussian's offset to its last one's end.
+	const int valid = first < n ? (int)min((int64_t)HDS_WAVE, n - first) : 0;
+	const uint32_t run_start = __shfl(off, 0, HDS_WAVE);
+	const uint32_t run_end = valid > 0 ? __shfl(off + cnt, valid - 1, HDS_WAVE) : run_start;
+	s_off[wave][lane] = real ? off : 0xffffffffu;  // padding lanes never own a pair
+	hds_wave_fence();
+
+	for (uint32_t base = run_start; base < run_end; base += HDS_WAVE) {
+		const uint32_t p = base + (uint32_t)lane;
+		const bool in_run = p < run_end;
+		// Last lane j of the wave with s_off[j] <= p (6 halvings over 64 entries).
+		int j = 0;
 #pragma unroll
-	for (int r = 0; r < kItemsPerThread; r++) {
-		gid[r] = order[owner[r]];
-		rc[r] = rects_sorted[owner[r]];
-	}
-#pragma unroll
-	for (int r = 0; r < kItemsPerThread; r++) {
-		const int64_t p = base + r * kThreads + t;
-		const bool valid = p < num_pairs;
+		for (int step = HDS_WAVE / 2; step > 0; step >>= 1)
+			if (s_off[wave][j + step] <= p) j += step;
+		const uint32_t jx = (uint32_t)__shfl((int)rc.x, j, HDS_WAVE);
+		const uint32_t jy = (uint32_t)__shfl((int)rc.y, j, HDS_WAVE);
+		const uint32_t jgid = (uint32_t)__shfl((int)gid, j, HDS_WAVE);
+		const uint32_t joff = s_off[wave][j];
+		const bool valid_pair = in_run && (int64_t)p < num_pairs;
 		uint32_t key = 0;
-		if (valid) {
-			const uint32_t x0 = rc[r].x & 0xffffu, y0 = rc[r].x >> 16, w = rc[r].y & 0xffffu;
-			const uint32_t local = (uint32_t)p - off[r];
+		if (valid_pair) {
+			const uint32_t x0 = jx & 0xffffu, y0 = jx >> 16, w = jy & 0xffffu;
+			const uint32_t local = p - joff;
 			key = (y0 + local / w) * (uint32_t)tiles_x + x0 + local % w;
 			tile_keys[p] = key;
-			gids[p] = gid[r];
+			gids[p] = jgid;
 		}
-		count_digits(key, valid, passes, s_hist);
+		count_digits(key, valid_pair, passes, s_hist);
 	}
 	flush_digits(passes, s_hist, hist);
 }
@@ -794,7 +739,7 @@ int bin_emit_launch(int64_t n, int64_t num_pairs, bool exact, int width, int hei
 	timer1.stop();
 	HDS_LAUNCH_CHECK("zero_sort_control", s);
 	HdsKernelTimer timer2("emit_kernel", s);
-	emit_kernel<<<(unsigned)parts_of(num_pairs), kThreads, 0, s>>>(n, num_pairs, total, offsets, order, rects_sorted,
+	emit_kernel<<<hds_blocks(n, kThreads), kThreads, 0, s>>>(n, num_pairs, total, offsets, order, rects_sorted,
 																	tiles_x, passes, keys_a, vals_a, ctrl->hist);
 	timer2.stop();
 	HDS_LAUNCH_CHECK("emit_pairs", s);
