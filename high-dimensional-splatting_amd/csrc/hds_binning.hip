@@ -142,10 +142,11 @@ __device__ inline uint32_t block_exclusive_scan(uint32_t v, uint32_t* s_wave, ui
 }
 
 // Lanes of this wave (among `active`) whose digit equals ours.
-__device__ inline uint64_t match_digit(uint32_t d, uint64_t active) {
+__device__ inline uint64_t match_digit(uint32_t d, uint64_t active, int bits = kRadixBits) {
 	uint64_t peers = active;
 #pragma unroll
 	for (int b = 0; b < kRadixBits; b++) {
+		if (b >= bits) break;
 		const bool bit = (d >> b) & 1u;
 		const uint64_t m = hds_ballot(bit);
 		peers &= bit ? m : ~m;
@@ -154,12 +155,13 @@ __device__ inline uint64_t match_digit(uint32_t d, uint64_t active) {
 }
 
 // Adds this row's keys (lanes in `active`) to the work-group's LDS digit histograms, one per pass.
-__device__ inline void count_digits(uint32_t key, bool valid, int passes, uint32_t (*s_hist)[kRadix]) {
+__device__ inline void count_digits(uint32_t key, bool valid, int passes, uint32_t (*s_hist)[kRadix],
+								 int key_bits = 32) {
 	const uint64_t active = hds_ballot(valid);
 	if (active == 0) return;
 	for (int p = 0; p < passes; p++) {
 		const uint32_t d = (key >> (p * kRadixBits)) & (kRadix - 1);
-		const uint64_t peers = match_digit(d, active);
+		const uint64_t peers = match_digit(d, active, key_bits - p * kRadixBits);
 		if (valid && hds_rank_below(peers) == 0) atomicAdd(&s_hist[p][d], (uint32_t)__popcll(peers));
 	}
 }
@@ -426,6 +428,27 @@ __global__ __launch_bounds__(kThreads) void prepare_kernel(
 	flush_digits(kMaxPasses, s_hist, hist);
 }
 
+// q = a / b, r = a % b: a float quotient estimate, within one of a / b for a < 2^22, corrected
+// once (exact); larger a (rectangles of over 4M tiles) take the integer division.
+__device__ inline void divmod_small(uint32_t a, uint32_t b, uint32_t& q, uint32_t& r) {
+	if (a >= (1u << 22)) {
+		q = a / b;
+		r = a % b;
+		return;
+	}
+	int qi = (int)((float)a * __builtin_amdgcn_rcpf((float)b));
+	int ri = (int)a - (int)__umul24((uint32_t)qi, b);
+	if (ri < 0) {
+		qi -= 1;
+		ri += (int)b;
+	} else if (ri >= (int)b) {
+		qi += 1;
+		ri -= (int)b;
+	}
+	q = (uint32_t)qi;
+	r = (uint32_t)ri;
+}
+
 // Pair emission (forward.cu:63-113): the pairs of gaussian g are [offsets[g], offsets[g] + w * h),
 // tile (x0 + local % w, y0 + local / w) for local = 0 .. w * h - 1, in depth order. A wave takes 64
 // consecutive depth-ordered gaussians, whose pairs are one contiguous run of the output; lane l
@@ -439,7 +462,7 @@ __global__ __launch_bounds__(kThreads) void emit_kernel(int64_t n, int64_t num_p
 														 const uint32_t* __restrict__ offsets,
 														 const uint32_t* __restrict__ order,
 														 const uint2* __restrict__ rects_sorted, int tiles_x,
-														 int passes, uint32_t* __restrict__ tile_keys,
+														 int passes, int key_bits, uint32_t* __restrict__ tile_keys,
 														 uint32_t* __restrict__ gids, uint32_t* __restrict__ hist) {
 	__shared__ uint32_t s_off[kWaves][HDS_WAVE];
 	__shared__ uint32_t s_hist[kMaxPasses][kRadix];
@@ -483,12 +506,13 @@ __global__ __launch_bounds__(kThreads) void emit_kernel(int64_t n, int64_t num_p
 		uint32_t key = 0;
 		if (valid_pair) {
 			const uint32_t x0 = jx & 0xffffu, y0 = jx >> 16, w = jy & 0xffffu;
-			const uint32_t local = p - joff;
-			key = (y0 + local / w) * (uint32_t)tiles_x + x0 + local % w;
+			uint32_t row, col;
+			divmod_small(p - joff, w, row, col);
+			key = (y0 + row) * (uint32_t)tiles_x + x0 + col;
 			tile_keys[p] = key;
 			gids[p] = jgid;
 		}
-		count_digits(key, valid_pair, passes, s_hist);
+		count_digits(key, valid_pair, passes, s_hist, key_bits);
 	}
 	flush_digits(passes, s_hist, hist);
 }
@@ -740,7 +764,7 @@ int bin_emit_launch(int64_t n, int64_t num_pairs, bool exact, int width, int hei
 	HDS_LAUNCH_CHECK("zero_sort_control", s);
 	HdsKernelTimer timer2("emit_kernel", s);
 	emit_kernel<<<hds_blocks(n, kThreads), kThreads, 0, s>>>(n, num_pairs, total, offsets, order, rects_sorted,
-																	tiles_x, passes, keys_a, vals_a, ctrl->hist);
+																	tiles_x, passes, tile_bits(num_tiles), keys_a, vals_a, ctrl->hist);
 	timer2.stop();
 	HDS_LAUNCH_CHECK("emit_pairs", s);
 	int st = onesweep_sort(keys_a, vals_a, keys_b, vals_b, num_pairs, total, passes, ctrl->hist, status,
