@@ -461,6 +461,58 @@ def test_dense_tile_walks_past_every_batch():
     assert_grads_close(("means2D", "conics", "colors", "opacities", "features"), got, want)
 
 
+def elongated_scene(seed, n, width, height):
+    """Thin, long, rotated gaussians centred near the corners and edges of the 8x8 pixel blocks, with
+    opacities down to just above 1/255: the cases where a cull of whole blocks could wrongly drop a
+    gaussian that reaches a pixel (the oracle renders every pixel without any block cull)."""
+    g = torch.Generator().manual_seed(seed)
+    corners = torch.randint(0, width // 8 + 1, (n,), generator=g) * 8.0, torch.randint(0, height // 8 + 1, (n,), generator=g) * 8.0
+    means2D = torch.stack(corners, -1) + (torch.rand(n, 2, generator=g) * 2 - 1) * 6.0
+    theta = torch.rand(n, generator=g) * math.pi
+    thin = 0.3 + torch.rand(n, generator=g) * 0.7            # covariance eigenvalues: 0.3-1 px^2 ...
+    long = torch.exp(torch.rand(n, generator=g) * math.log(600.0))  # ... against 1-600 px^2
+    cs, sn = torch.cos(theta), torch.sin(theta)
+    sxx = long * cs * cs + thin * sn * sn
+    syy = long * sn * sn + thin * cs * cs
+    sxy = (long - thin) * cs * sn
+    det = sxx * syy - sxy * sxy
+    conics = torch.stack([syy / det, -sxy / det, sxx / det], -1)
+    radii = 3.0 * torch.sqrt(torch.maximum(long, thin))
+    depths = 1.0 + torch.rand(n, generator=g) * 9.0
+    opac = torch.where(torch.rand(n, generator=g) < 0.3, 1.0 / 255 * (1.0 + torch.rand(n, generator=g) * 0.2),
+                       torch.rand(n, generator=g))[:, None]
+    colors = torch.rand(n, 3, generator=g)
+    return tuple(t.float().contiguous().to(DEV) for t in (means2D, depths, radii, conics, colors, opac))
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_block_cull_keeps_every_contributor(seed):
+    """The blend kernels visit a gaussian in an 8x8 block only if the minimum of its quadratic form over
+    the block's pixel-centre rectangle is under the 1/255 threshold; on adversarial ellipses the result
+    must still equal the oracle's (n_contrib equal up to exp ulps at the cut-offs, images and gradients
+    within the usual bars)."""
+    width, height = 96, 80
+    n = 3000
+    inputs = elongated_scene(seed, n, width, height)
+    bg = torch.tensor([0.3, 0.5, 0.7], device=DEV)
+    image, final_T, n_contrib, values, ranges, _, _ = _get_rasterizer().rasterize(*inputs, bg, width, height)
+    want_image, _, want_T, want_nc, want_values, _ = oracle_render(inputs, width, height, bg)
+    np.testing.assert_array_equal(np_(values), want_values)
+    assert_image_close(np_(image), want_image)
+    assert_image_close(np_(final_T), want_T)
+    assert (np_(n_contrib) != want_nc).mean() < 1e-3
+    g = torch.Generator().manual_seed(100 + seed)
+    features = torch.rand(n, 32, generator=g).to(DEV)
+    _, fimg = rasterize(*inputs, width, height, bg, features=features)
+    assert_image_close(np_(fimg), oracle_render(inputs, width, height, bg, features)[1], max_error=1e-3,
+                       max_perc_99=5e-4)
+    grad_image = torch.rand(height, width, 3, generator=g).to(DEV)
+    grad_feat = torch.rand(height, width, 32, generator=g).to(DEV)
+    got = grads_gpu(inputs, width, height, features, grad_image, grad_feat, bg)
+    want = grads_oracle(inputs, width, height, features, grad_image, grad_feat, bg)
+    assert_grads_close(("means2D", "conics", "colors", "opacities", "features"), got, want)
+
+
 def test_unsupported_feature_width_is_rejected():
     inputs = scene(0, 100, 32, 32)
     with pytest.raises(RuntimeError, match="32, 64, 128, 256 or 512"):
