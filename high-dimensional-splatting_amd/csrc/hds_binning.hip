@@ -28,7 +28,6 @@ constexpr int kThreads = 256;
 constexpr int kItemsPerThread = 16;
 constexpr int kTileItems = kThreads * kItemsPerThread;  // items one partition / work-group owns
 constexpr int kWaves = kThreads / HDS_WAVE;
-constexpr int kWaveItems = kTileItems / kWaves;         // a wave ranks 16 rows of 64 consecutive items
 constexpr int kRadixBits = 8;
 constexpr int kRadix = 1 << kRadixBits;
 constexpr int kMaxPasses = 4;                           // 32-bit keys
@@ -184,7 +183,7 @@ __device__ inline void flush_digits(int passes, uint32_t (*s_hist)[kRadix], uint
 // words. Item order inside a partition is (wave, row, lane): wave w owns items [w*1024, w*1024 +
 // 1024). With kGather, the value is an index and the pass also writes gathered[pos] = table[value]
 // (the depth sort's last pass carries each gaussian's tile rectangle into depth order this way).
-template <bool kKeysOut, bool kGather>
+template <bool kKeysOut, bool kGather, int kIPT>
 __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __restrict__ keys_in,
 															 const uint32_t* __restrict__ vals_in,
 															 uint32_t* __restrict__ keys_out,
@@ -194,8 +193,10 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __re
 															 uint64_t* status, uint32_t* ticket, uint32_t* error,
 															 const uint2* __restrict__ table,
 															 uint2* __restrict__ gathered) {
-	__shared__ uint32_t s_keys[kTileItems];
-	__shared__ uint32_t s_vals[kTileItems];
+	constexpr int kPartItems = kThreads * kIPT;         // items of one partition
+	constexpr int kPartWaveItems = kPartItems / kWaves;  // a wave ranks kIPT rows of 64 consecutive items
+	__shared__ uint32_t s_keys[kPartItems];
+	__shared__ uint32_t s_vals[kPartItems];
 	__shared__ uint32_t s_cnt[kWaves][kRadix];  // per-wave running counts, then per-wave offsets
 	__shared__ uint32_t s_local[kRadix];        // first slot of each digit in the partition
 	__shared__ uint32_t s_adj[kRadix];          // output index of slot j of digit d = s_adj[d] + j
@@ -209,13 +210,13 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __re
 	// Launched for n items; with n_total the count is read here, and tickets past its last
 	// partition leave at once (every partition the look-back waits for has a lower ticket).
 	n = device_count(n_total, n);
-	if (part >= parts_of(n)) return;
-	const int64_t base = part * kTileItems;
-	const int64_t wbase = base + (int64_t)wave * kWaveItems;
+	if (part >= (n + kPartItems - 1) / kPartItems) return;
+	const int64_t base = part * kPartItems;
+	const int64_t wbase = base + (int64_t)wave * kPartWaveItems;
 
-	uint32_t key[kItemsPerThread], val[kItemsPerThread];
+	uint32_t key[kIPT], val[kIPT];
 #pragma unroll
-	for (int r = 0; r < kItemsPerThread; r++) {
+	for (int r = 0; r < kIPT; r++) {
 		const int64_t i = wbase + r * HDS_WAVE + lane;
 		key[r] = i < n ? keys_in[i] : 0u;
 		val[r] = i < n ? vals_in[i] : 0u;
@@ -223,9 +224,9 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __re
 	// Rank inside the wave: earlier rows' count of the digit (s_cnt, kept by each digit group's
 	// first lane) plus the lanes below with the same digit. A wave's LDS accesses run in order, so
 	// the read of row r + 1 sees the update of row r.
-	uint32_t rank[kItemsPerThread];
+	uint32_t rank[kIPT];
 #pragma unroll
-	for (int r = 0; r < kItemsPerThread; r++) {
+	for (int r = 0; r < kIPT; r++) {
 		const bool valid = wbase + r * HDS_WAVE + lane < n;
 		const uint32_t d = (key[r] >> shift) & (kRadix - 1);
 		const uint64_t peers = match_digit(d, hds_ballot(valid));
@@ -264,7 +265,7 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __re
 	// Reorder the partition by digit in LDS, then write it out: consecutive threads write
 	// consecutive output positions inside each digit's run.
 #pragma unroll
-	for (int r = 0; r < kItemsPerThread; r++) {
+	for (int r = 0; r < kIPT; r++) {
 		if (wbase + r * HDS_WAVE + lane < n) {
 			const uint32_t d = (key[r] >> shift) & (kRadix - 1);
 			const uint32_t slot = s_local[d] + s_cnt[wave][d] + rank[r];
@@ -273,9 +274,9 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __re
 		}
 	}
 	__syncthreads();
-	const int64_t items = n - base < kTileItems ? n - base : kTileItems;
+	const int64_t items = n - base < kPartItems ? n - base : kPartItems;
 #pragma unroll
-	for (int r = 0; r < kItemsPerThread; r++) {
+	for (int r = 0; r < kIPT; r++) {
 		const int j = r * kThreads + t;
 		if (j < items) {
 			const uint32_t k = s_keys[j];
@@ -299,7 +300,10 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __re
 int onesweep_sort(uint32_t* keys_a, uint32_t* vals_a, uint32_t* keys_b, uint32_t* vals_b, int64_t n,
 				  const uint64_t* n_total, int passes, const uint32_t* hist, uint64_t* status, uint32_t* tickets, uint32_t* error, bool keys_final_needed,
 				  const uint2* table, uint2* gathered, hipStream_t s) {
-	const unsigned parts = (unsigned)parts_of(n);
+	// Passes over more than 16M items take 8192-item partitions: half the tickets and look-back
+	// steps (both are paid per partition); smaller ones keep 4096 so that the grid fills the chip.
+	const bool large = n > (int64_t(1) << 24);
+	const unsigned parts = (unsigned)(large ? (n + 2 * kTileItems - 1) / (2 * kTileItems) : parts_of(n));
 	uint32_t *kin = keys_a, *vin = vals_a, *kout = keys_b, *vout = vals_b;
 	for (int p = 0; p < passes; p++) {
 		const bool last = p == passes - 1;
@@ -307,14 +311,20 @@ int onesweep_sort(uint32_t* keys_a, uint32_t* vals_a, uint32_t* keys_b, uint32_t
 		const uint32_t* h = hist + p * kHistWords;
 		HdsKernelTimer timer("onesweep_kernel", s);
 		if (last && table)
-			onesweep_kernel<false, true><<<parts, kThreads, 0, s>>>(kin, vin, nullptr, vout, n, n_total, p, h, status,
-																	tickets + p, error, table, gathered);
+			onesweep_kernel<false, true, kItemsPerThread><<<parts, kThreads, 0, s>>>(kin, vin, nullptr, vout, n, n_total, p, h, status,
+																					  tickets + p, error, table, gathered);
+		else if (keys_out && large)
+			onesweep_kernel<true, false, 2 * kItemsPerThread><<<parts, kThreads, 0, s>>>(kin, vin, kout, vout, n, n_total, p, h,
+																						  status, tickets + p, error, nullptr, nullptr);
 		else if (keys_out)
-			onesweep_kernel<true, false><<<parts, kThreads, 0, s>>>(kin, vin, kout, vout, n, n_total, p, h, status,
-																	tickets + p, error, nullptr, nullptr);
+			onesweep_kernel<true, false, kItemsPerThread><<<parts, kThreads, 0, s>>>(kin, vin, kout, vout, n, n_total, p, h, status,
+																					  tickets + p, error, nullptr, nullptr);
+		else if (large)
+			onesweep_kernel<false, false, 2 * kItemsPerThread><<<parts, kThreads, 0, s>>>(kin, vin, nullptr, vout, n, n_total, p, h,
+																						   status, tickets + p, error, nullptr, nullptr);
 		else
-			onesweep_kernel<false, false><<<parts, kThreads, 0, s>>>(kin, vin, nullptr, vout, n, n_total, p, h, status,
-																	 tickets + p, error, nullptr, nullptr);
+			onesweep_kernel<false, false, kItemsPerThread><<<parts, kThreads, 0, s>>>(kin, vin, nullptr, vout, n, n_total, p, h, status,
+																					   tickets + p, error, nullptr, nullptr);
 		timer.stop();
 		HDS_LAUNCH_CHECK("onesweep_radix_pass", s);
 		uint32_t* t;
