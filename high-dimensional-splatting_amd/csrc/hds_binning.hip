@@ -310,7 +310,10 @@ int onesweep_sort(uint32_t* keys_a, uint32_t* vals_a, uint32_t* keys_b, uint32_t
 		const bool keys_out = !last || keys_final_needed;
 		const uint32_t* h = hist + p * kHistWords;
 		HdsKernelTimer timer("onesweep_kernel", s);
-		if (last && table)
+		if (last && table && large)
+			onesweep_kernel<false, true, 2 * kItemsPerThread><<<parts, kThreads, 0, s>>>(kin, vin, nullptr, vout, n, n_total, p, h,
+																						  status, tickets + p, error, table, gathered);
+		else if (last && table)
 			onesweep_kernel<false, true, kItemsPerThread><<<parts, kThreads, 0, s>>>(kin, vin, nullptr, vout, n, n_total, p, h, status,
 																					  tickets + p, error, table, gathered);
 		else if (keys_out && large)

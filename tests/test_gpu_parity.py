@@ -153,6 +153,40 @@ def test_binning_of_the_stress_scene_restricted_to_a_subset_equals_the_oracle():
     np.testing.assert_array_equal(got_tiles, want_tiles)
 
 
+def test_binning_of_more_than_16M_gaussians_is_complete_and_ordered():
+    """17M small gaussians on a 256x192 image, depths on a 0.01 grid (many ties): the depth sort and
+    the pair sort run on 8192-item partitions above 16M items. Every gaussian appears exactly as often
+    as the oracle's tile count says, tile_ranges cut [0, P) in tile order, and inside each tile the
+    depth bits increase with equal depths in index order, which together fix the sequence."""
+    n, width, height = 17_000_000, 256, 192
+    g = torch.Generator().manual_seed(21)
+    means2D = torch.rand(n, 2, generator=g) * torch.tensor([float(width), float(height)])
+    depths = torch.round(1.0 + torch.rand(n, generator=g) * 999.0) / 100.0
+    sigma = 0.5 + torch.rand(n, generator=g) * 1.5
+    conics = torch.stack([sigma ** -2, torch.zeros(n), sigma ** -2], -1)
+    radii = 3.0 * sigma
+    opac = (0.1 + 0.9 * torch.rand(n, generator=g))[:, None]
+    m2, d, r, c, op = (t.contiguous().to(DEV) for t in (means2D, depths, radii, conics, opac))
+    values, ranges, _, _ = _get_rasterizer().bin(m2, d, r, c, None, op, width, height)
+    p, t = values.numel(), ranges.shape[0]
+    assert p > (1 << 24), p
+    counts, _ = oracle.tile_counts(np_(m2), np_(r), np_(c), np_(op), width, height)
+    vals = values.long()
+    np.testing.assert_array_equal(np_(torch.bincount(vals, minlength=n)), counts)
+    lens = (ranges[:, 1] - ranges[:, 0]).long()
+    full = lens > 0
+    assert (ranges[~full] == 0).all()
+    starts, ends = ranges[full, 0].long(), ranges[full, 1].long()
+    assert int(starts[0]) == 0 and int(ends[-1]) == p and torch.equal(starts[1:], ends[:-1])
+    tile_of = torch.repeat_interleave(torch.arange(t, device=DEV)[full], lens[full])
+    key = tile_of * (1 << 32) + (d.view(torch.int32).long()[vals] & 0xFFFFFFFF)
+    step = key[1:] - key[:-1]
+    assert bool((step >= 0).all())
+    tie = step == 0
+    assert int(tie.sum()) > 1_000_000, "the scene should have many depth ties"
+    assert bool((vals[1:][tie] > vals[:-1][tie]).all())
+
+
 def test_binning_keeps_index_order_on_depth_ties():
     # 300 gaussians in 5 depth values over a 3x2 tile image: ties must stay in index order.
     g = torch.Generator().manual_seed(4)
