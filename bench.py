@@ -61,6 +61,11 @@ def parse_args():
                          "synthetic config, with features U[0, 1] as bench/harness.py:46 does (needs --camera)")
     ap.add_argument("--camera", type=Path, default=None,
                     help="JSON camera for --checkpoint (gaussian_splatting.utils.checkpoint.load_camera)")
+    ap.add_argument("--loss", choices=("auto", "none", "l1-ssim"), default="auto",
+                    help="l1-ssim: the image gradient comes from 0.8 L1 + 0.2 (1 - SSIM) against a U[0, 1] target "
+                         "(main.py:179-182), run through the SSIM kernels inside the step; none: dL/dimage U[0, 1] as "
+                         "bench/harness.py:49 does; auto: l1-ssim for configs 0 and 4, whose BASELINE definition "
+                         "includes the loss, none otherwise")
     ap.add_argument("--bwd-slice", type=int, default=None,
                     help="channels per backward work-group (gaussian_splatting.rasterizer.FEATURE_SLICE_WIDTH)")
     args = ap.parse_args()
@@ -114,6 +119,7 @@ def main() -> int:
 
     from gaussian_splatting.rasterizer import _get_rasterizer, project_gaussians, rasterize
     from gaussian_splatting.rasterizer._native import KernelProfile, StageTimer
+    from gaussian_splatting.utils.loss import l1_loss, ssim
     from gaussian_splatting.utils.sh import eval_sh
     from tests.scenes import synthetic_config, upstream, view_dirs
 
@@ -149,6 +155,10 @@ def main() -> int:
     if args.rgb_only:
         del leaves["features"]
     grad_image, grad_features = upstream(2, H, W, C, device=dev)
+    # With the loss, the U[0, 1] image drawn above is the target and dL/dimage comes from the loss.
+    loss_mode = args.loss if args.loss != "auto" else ("l1-ssim" if args.config in (0, 4) and args.checkpoint is None
+                                                        else "none")
+    target = grad_image if loss_mode == "l1-ssim" else None
     state = {}
 
     def forward():
@@ -159,7 +169,15 @@ def main() -> int:
                                  W, H, features=leaves.get("features"))
 
     def backward():
-        if args.rgb_only:
+        image = state["out"] if args.rgb_only else state["out"][0]
+        if target is not None:
+            # main.py:179-182: 0.8 L1 + 0.2 (1 - SSIM), the SSIM on the fused HIP kernels.
+            loss = 0.8 * l1_loss(image, target) + 0.2 * (1.0 - ssim(image, target))
+            if args.rgb_only:
+                loss.backward()
+            else:
+                torch.autograd.backward([loss, state["out"][1]], [None, grad_features])
+        elif args.rgb_only:
             torch.autograd.backward(state["out"], grad_image)
         else:
             torch.autograd.backward(state["out"], [grad_image, grad_features])
@@ -191,7 +209,7 @@ def main() -> int:
         gpu_out = {"image": state["out"][0], "feature_image": state["out"][1],
                    **{name: leaf.grad for name, leaf in leaves.items()}}
         gpu_out = {k: v.detach().cpu().numpy() for k, v in gpu_out.items()}
-        cpu, want = cpu_baseline(wl, colors, grad_image, grad_features)
+        cpu, want = cpu_baseline(wl, colors, grad_image, grad_features, loss_target=target)
         agreement = agree(gpu_out, want)
         print(f"[bench] agreement with the oracle: {agreement}", file=sys.stderr, flush=True)
         if not agreement["passed"]:
@@ -294,7 +312,8 @@ def main() -> int:
         "config": {"workload": wl.name + ("-rgb-only" if args.rgb_only else "")
                    + ("-frozen-features" if args.frozen_features else ""), "gaussians": N, "width": W, "height": H,
                    "channels": 0 if args.rgb_only else C,
-                   "visible": n_vis, "pairs": pairs, "parallelism": "single-gpu"},
+                   "visible": n_vis, "pairs": pairs, "parallelism": "single-gpu",
+                   "loss": "0.8 L1 + 0.2 (1 - SSIM)" if target is not None else "none (dL/dimage U[0, 1])"},
         "step_ms_median": round(statistics.median(step_ms), 4), **split,
         "step_hbm_frac": round(step_frac, 4), "step_algorithmic_MB": round(total_alg / 1e6, 1),
         "roofline": roofline, "stages": stage_report, "kernels": kernel_report, "cpu_baseline": cpu,
@@ -344,10 +363,11 @@ def traffic_per_step(kernel_names) -> int | None:
     return sum(per_kernel[k] for k in kernel_names)
 
 
-def cpu_baseline(wl, colors, grad_image, grad_features):
+def cpu_baseline(wl, colors, grad_image, grad_features, loss_target=None):
     """The CPU oracle (OpenMP, all host threads) on the same frame: projection, binning, blend forward,
-    blend backward and projection backward, once. Sample = the full frame. Returns the baseline record
-    and the oracle's outputs in the leaves' shapes (for the agreement gate)."""
+    blend backward and projection backward, once (with loss_target, dL/dimage of 0.8 L1 + 0.2 (1 - SSIM)
+    against it from the oracle's SSIM instead of grad_image). Sample = the full frame. Returns the
+    baseline record and the oracle's outputs in the leaves' shapes (for the agreement gate)."""
     import numpy as np
     import torch
 
@@ -368,6 +388,13 @@ def cpu_baseline(wl, colors, grad_image, grad_features):
     image, T, nc, fimg = oracle.render_forward(cam["width"], cam["height"], ranges, values, m2, c, opac, cols,
                                                np.zeros(3, np.float32), feats)
     t1 = time.perf_counter()
+    if loss_target is not None:
+        # d/dimage of 0.8 mean|image - target| + 0.2 (1 - mean SSIM): sign / numel, and the SSIM
+        # backward with dL/dmean = -0.2 (utils/loss.py:57-96 there).
+        tgt = np_(loss_target)
+        gi = (0.8 * np.sign(image - tgt) / image.size).astype(np.float32)
+        _, d_mu, d_aa, d_ab = oracle.ssim_forward(image, tgt)
+        gi += oracle.ssim_backward(-0.2, image, tgt, d_mu, d_aa, d_ab)
     dm, dc, dcol, dop, df = oracle.render_backward(cam["width"], cam["height"], ranges, values, m2, c, opac, cols,
                                                    np.zeros(3, np.float32), T, nc, gi, feats, gf)
     dmeans, dscales, dq = oracle.project_backward(dm, dc, means, scales, quats, w2c, cam["fx"], cam["fy"],
