@@ -109,8 +109,9 @@ def main() -> int:
     args = parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print("bench.py measures one GPU: the rasterizer path has no multi-GPU mode in this build "
-              "(see DESIGN.md for how it would shard over channels). Run with --gpus 1.", file=sys.stderr)
+        print("bench.py measures one GPU: the rasterizer path has no multi-GPU mode in this build (it would "
+              "shard over feature channels, with one all-reduce of the geometry gradients). Run with --gpus 1.",
+              file=sys.stderr)
         return 2
 
     import numpy as np
