@@ -115,6 +115,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S >= 128 ? 
 	__shared__ HdsHeaderSlot<kBatch, RGB> s_hdr0, s_hdr1;
 	__shared__ __attribute__((aligned(16))) float s_feat0[kRows];
 	__shared__ __attribute__((aligned(16))) float s_feat1[kRows];
+	// Per wave: the batch slots of its box-hits in list order, then kBatch (the zero row) as padding.
+	__shared__ __attribute__((aligned(16))) int s_hit[4][kBatch + kGroup];
 
 	const int tile = hds_xcd_tile(blockIdx.x, a.tiles_x, a.num_tiles);
 	if (tile < 0) return;
@@ -176,19 +178,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S >= 128 ? 
 				if (lane < cnt) {
 					box_hit = hds_block_reach(make_float2(h.mx[lane], h.my[lane]), h.conic[lane], rx0, rx1, ry0, ry1);
 				}
-				uint64_t hits = hds_ballot(box_hit);
-				while (hits) {
+				const uint64_t hits = hds_ballot(box_hit);
+				const int total = __builtin_popcountll(hits);
+				// List the hits once per batch: hit j goes to position rank(j); positions up to the
+				// next multiple of kGroup past the last hit point at the zero row.
+				int* hit_slot = s_hit[wave];
+				if (box_hit) hit_slot[hds_rank_below(hits)] = lane;
+				if (lane >= total && lane < ((total + kGroup - 1) & ~(kGroup - 1))) hit_slot[lane] = kBatch;
+				hds_wave_fence();
+				for (int g0 = 0; g0 < total; g0 += kGroup) {
 					// The next group: up to 16 box-hits in list order; missing positions use the zero row.
+					const int count = min(kGroup, total - g0);
 					int slot[kGroup];
-					int count = 0;
 #pragma unroll
-					for (int q = 0; q < kGroup; q++) {
-						slot[q] = kBatch;
-						if (hits) {
-							slot[q] = __builtin_ctzll(hits);
-							hits &= hits - 1;
-							count = q + 1;
-						}
+					for (int q4 = 0; q4 < kGroup; q4 += 4) {
+						const int4 v = *reinterpret_cast<const int4*>(hit_slot + g0 + q4);
+						slot[q4] = v.x;
+						slot[q4 + 1] = v.y;
+						slot[q4 + 2] = v.z;
+						slot[q4 + 3] = v.w;
 					}
 					float w[kGroup];
 #pragma unroll
