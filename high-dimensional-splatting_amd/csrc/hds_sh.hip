@@ -87,10 +87,23 @@ __device__ inline float sh_weight(const float* dc, const float* rest, int j, int
 	return j == 0 ? dc[c] : rest[(j - 1) * 3 + c];
 }
 
-__global__ __launch_bounds__(256) void eval_sh_kernel(int64_t n, int k, const float* __restrict__ sh_dc,
+constexpr int kShEvalBlock = 256;
+
+__global__ __launch_bounds__(kShEvalBlock) void eval_sh_kernel(int64_t n, int k, const float* __restrict__ sh_dc,
 													  const float* __restrict__ sh_rest, const float* __restrict__ dirs,
 													  const float* __restrict__ radii, float* __restrict__ rgb) {
-	const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+	// The block's higher-order rows are one contiguous run of count * 45 floats: read it coalesced
+	// into LDS (a thread's own row, read directly, puts 64 cache lines under every load). Row
+	// stride 45 is odd, so the per-thread LDS reads hit 64 different banks.
+	__shared__ float s_rest[kShEvalBlock * 45];
+	const int64_t first = (int64_t)blockIdx.x * kShEvalBlock;
+	const int64_t i = first + threadIdx.x;
+	if (k > 1) {
+		const int count = (int)(n - first < kShEvalBlock ? n - first : kShEvalBlock);
+		const float* src = sh_rest + first * 45;
+		for (int e = threadIdx.x; e < count * 45; e += kShEvalBlock) s_rest[e] = src[e];
+		__syncthreads();
+	}
 	if (i >= n) return;
 	if (!(radii[i] > 0.0f)) {
 		rgb[i * 3 + 0] = rgb[i * 3 + 1] = rgb[i * 3 + 2] = 0.0f;
@@ -99,7 +112,7 @@ __global__ __launch_bounds__(256) void eval_sh_kernel(int64_t n, int k, const fl
 	float b[16];
 	sh_basis(dirs[i * 3], dirs[i * 3 + 1], dirs[i * 3 + 2], k, b);
 	const float* dc = sh_dc + i * 3;
-	const float* rest = sh_rest + i * 45;
+	const float* rest = s_rest + threadIdx.x * 45;
 	for (int c = 0; c < 3; c++) {
 		float value = 0.5f;
 		for (int j = 0; j < k; j++) value += b[j] * sh_weight(dc, rest, j, c);
@@ -195,7 +208,7 @@ extern "C" int hds_eval_sh(int64_t n, int degree, const float* sh_dc, const floa
 	HDS_REQUIRE(sh_dc && sh_rest && dirs && radii && rgb, "eval_sh: null pointer argument");
 	hipStream_t s = (hipStream_t)stream;
 	HdsKernelTimer timer1("eval_sh_kernel", s);
-	eval_sh_kernel<<<hds_blocks(n, 256), 256, 0, s>>>(n, (degree + 1) * (degree + 1), sh_dc, sh_rest, dirs, radii, rgb);
+	eval_sh_kernel<<<hds_blocks(n, kShEvalBlock), kShEvalBlock, 0, s>>>(n, (degree + 1) * (degree + 1), sh_dc, sh_rest, dirs, radii, rgb);
 	timer1.stop();
 	HDS_LAUNCH_CHECK("eval_sh_forward", s);
 	return HDS_OK;
