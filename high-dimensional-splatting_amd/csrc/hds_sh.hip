@@ -153,6 +153,14 @@ __global__ __launch_bounds__(kShAdamBlock) void eval_sh_backward_adam_kernel(
 	const int64_t i = first + threadIdx.x;
 	float* gdc = s_dc + threadIdx.x * 3;
 	float* grest = s_rest + threadIdx.x * 45;
+	if (k > 1) {
+		// The block's coefficient rows, read coalesced into the gradient rows; a thread only
+		// touches its own row, reading each weight before its gradient replaces it.
+		const int rows = (int)min((int64_t)kShAdamBlock, n - first);
+		const float* src = sh_rest + first * 45;
+		for (int e = threadIdx.x; e < rows * 45; e += kShAdamBlock) s_rest[e] = src[e];
+		__syncthreads();
+	}
 	if (i < n) {
 		float dd[3] = {0.0f, 0.0f, 0.0f};
 		if (radii[i] > 0.0f) {
@@ -161,7 +169,7 @@ __global__ __launch_bounds__(kShAdamBlock) void eval_sh_backward_adam_kernel(
 			sh_basis(x, y, z, k, b);
 			sh_basis_grad(x, y, z, k, bx, by, bz);
 			const float* dc = sh_dc + i * 3;
-			const float* rest = sh_rest + i * 45;
+			const float* rest = grest;
 			// The colour clamp passes no gradient where it clipped; recomputed, not stored.
 			float g[3];
 			for (int c = 0; c < 3; c++) {
@@ -172,12 +180,13 @@ __global__ __launch_bounds__(kShAdamBlock) void eval_sh_backward_adam_kernel(
 			for (int j = 0; j < 16; j++) {
 				float t = 0.0f;
 				for (int c = 0; c < 3; c++) {
+					const float weight = j < k ? sh_weight(dc, rest, j, c) : 0.0f;
 					const float grad = j < k ? b[j] * g[c] : 0.0f;
 					if (j == 0)
 						gdc[c] = grad;
 					else
 						grest[(j - 1) * 3 + c] = grad;
-					if (j < k) t += sh_weight(dc, rest, j, c) * g[c];
+					if (j < k) t += weight * g[c];
 				}
 				if (j < k) {
 					dd[0] += t * bx[j];
