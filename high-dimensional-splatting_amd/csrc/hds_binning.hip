@@ -19,6 +19,8 @@
 // partitions whose owners are already running and never wait themselves before publishing. The
 // digit histograms every pass needs up front come from the kernel that produces the keys
 // (prepare for depths, emit for tile ids). The whole binning is 11 launches.
+#include <atomic>
+
 #include "hds_internal.h"
 #include "hds_rasterizer.h"
 
@@ -36,8 +38,11 @@ constexpr int kMaxPasses = 4;                           // 32-bit keys
 constexpr int kHistCopies = 16;
 constexpr int kHistWords = kHistCopies * kRadix;        // one pass's histogram copies
 // Polls of a silent predecessor before a look-back gives up and raises the error flag (seconds of
-// waiting; reached only if a launch is broken, never by a slow but running predecessor).
-constexpr uint32_t kSpinLimit = 1u << 22;
+// waiting; reached only if a launch is broken, never by a slow but running predecessor). Tests of
+// the failure path set it from the host (hds_set_lookback_limit): 0 makes every look-back give up
+// before its first poll, so the failure is certain while every kernel still runs to its end.
+constexpr uint32_t kSpinLimit = HDS_LOOKBACK_LIMIT_DEFAULT;
+std::atomic<uint32_t> g_spin_limit{kSpinLimit};
 
 static_assert(kRadix == kThreads, "one thread per radix bin");
 
@@ -76,11 +81,16 @@ __device__ inline void status_store(uint64_t* p, uint64_t v) {
 // loaded at a time, so a walk over many aggregates costs one memory latency per W partitions.
 template <int W>
 __device__ inline uint64_t lookback(uint64_t* status, int64_t stride, int64_t part, uint32_t epoch,
-									uint32_t* error) {
+									uint32_t* error, uint32_t spin_limit) {
 	const uint32_t agg = 2 * epoch + 1, inc = 2 * epoch + 2;
 	uint64_t sum = 0;
 	uint32_t spins = 0;
 	int64_t p = part - 1;
+	if (spin_limit == 0u) {
+		// Failure-path test mode (set from the host): give up before the first poll.
+		atomicOr(error, 1u);
+		return 0;
+	}
 	while (p >= 0) {
 		uint64_t v[W];
 #pragma unroll
@@ -97,7 +107,7 @@ __device__ inline uint64_t lookback(uint64_t* status, int64_t stride, int64_t pa
 			spins = 0;
 			continue;
 		}
-		if (++spins > kSpinLimit) {
+		if (++spins > spin_limit) {
 			atomicOr(error, 1u);
 			return sum;
 		}
@@ -191,7 +201,7 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __re
 															 const uint64_t* __restrict__ n_total, int pass,
 															 const uint32_t* __restrict__ digit_hist,
 															 uint64_t* status, uint32_t* ticket, uint32_t* error,
-															 const uint2* __restrict__ table,
+															 uint32_t spin_limit, const uint2* __restrict__ table,
 															 uint2* __restrict__ gathered) {
 	constexpr int kPartItems = kThreads * kIPT;         // items of one partition
 	constexpr int kPartWaveItems = kPartItems / kWaves;  // a wave ranks kIPT rows of 64 consecutive items
@@ -255,7 +265,7 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __re
 	const uint32_t local_start = block_exclusive_scan(count, s_wave, unused);
 	uint64_t before = 0;
 	if (part > 0) {
-		before = lookback<8>(status + t, kRadix, part, (uint32_t)pass, error);
+		before = lookback<8>(status + t, kRadix, part, (uint32_t)pass, error, spin_limit);
 		status_store(mine, status_word(2 * pass + 2, before + count));
 	}
 	s_local[t] = local_start;
@@ -287,7 +297,9 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __re
 				const uint32_t v = s_vals[j];
 				if (kKeysOut) keys_out[pos] = k;
 				vals_out[pos] = v;
-				if (kGather) gathered[pos] = table[v];
+				// A value is an index below n unless an earlier pass failed and left this slot
+				// unwritten (stale memory): the table is read only inside its n entries.
+				if (kGather) gathered[pos] = v < (uint64_t)n ? table[v] : make_uint2(0u, 0u);
 			}
 		}
 	}
@@ -312,22 +324,22 @@ int onesweep_sort(uint32_t* keys_a, uint32_t* vals_a, uint32_t* keys_b, uint32_t
 		HdsKernelTimer timer("onesweep_kernel", s);
 		if (last && table && large)
 			onesweep_kernel<false, true, 2 * kItemsPerThread><<<parts, kThreads, 0, s>>>(kin, vin, nullptr, vout, n, n_total, p, h,
-																						  status, tickets + p, error, table, gathered);
+																						  status, tickets + p, error, g_spin_limit.load(std::memory_order_relaxed), table, gathered);
 		else if (last && table)
 			onesweep_kernel<false, true, kItemsPerThread><<<parts, kThreads, 0, s>>>(kin, vin, nullptr, vout, n, n_total, p, h, status,
-																					  tickets + p, error, table, gathered);
+																					  tickets + p, error, g_spin_limit.load(std::memory_order_relaxed), table, gathered);
 		else if (keys_out && large)
 			onesweep_kernel<true, false, 2 * kItemsPerThread><<<parts, kThreads, 0, s>>>(kin, vin, kout, vout, n, n_total, p, h,
-																						  status, tickets + p, error, nullptr, nullptr);
+																						  status, tickets + p, error, g_spin_limit.load(std::memory_order_relaxed), nullptr, nullptr);
 		else if (keys_out)
 			onesweep_kernel<true, false, kItemsPerThread><<<parts, kThreads, 0, s>>>(kin, vin, kout, vout, n, n_total, p, h, status,
-																					  tickets + p, error, nullptr, nullptr);
+																					  tickets + p, error, g_spin_limit.load(std::memory_order_relaxed), nullptr, nullptr);
 		else if (large)
 			onesweep_kernel<false, false, 2 * kItemsPerThread><<<parts, kThreads, 0, s>>>(kin, vin, nullptr, vout, n, n_total, p, h,
-																						   status, tickets + p, error, nullptr, nullptr);
+																						   status, tickets + p, error, g_spin_limit.load(std::memory_order_relaxed), nullptr, nullptr);
 		else
 			onesweep_kernel<false, false, kItemsPerThread><<<parts, kThreads, 0, s>>>(kin, vin, nullptr, vout, n, n_total, p, h, status,
-																					   tickets + p, error, nullptr, nullptr);
+																					   tickets + p, error, g_spin_limit.load(std::memory_order_relaxed), nullptr, nullptr);
 		timer.stop();
 		HDS_LAUNCH_CHECK("onesweep_radix_pass", s);
 		uint32_t* t;
@@ -344,7 +356,8 @@ int onesweep_sort(uint32_t* keys_a, uint32_t* vals_a, uint32_t* keys_b, uint32_t
 
 __global__ __launch_bounds__(kThreads) void scan_kernel(const uint2* __restrict__ rects, int64_t n,
 														 uint32_t* __restrict__ out, uint64_t* status,
-														 uint32_t* ticket, uint32_t* error, uint64_t* __restrict__ total) {
+														 uint32_t* ticket, uint32_t* error, uint32_t spin_limit,
+														 uint64_t* __restrict__ total) {
 	// Items go through LDS so that global loads and stores stay coalesced while each thread
 	// scans 16 consecutive items; a pad word every 16 keeps the strided LDS reads conflict-free.
 	__shared__ uint32_t s_items[kTileItems + kTileItems / 16];
@@ -377,7 +390,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const uint2* __restrict_
 			status_store(status, status_word(2, block_total));
 		} else {
 			status_store(status + part, status_word(1, block_total));
-			before = lookback<16>(status, 1, part, 0, error);
+			before = lookback<16>(status, 1, part, 0, error, spin_limit);
 			status_store(status + part, status_word(2, before + block_total));
 		}
 		if (base + kTileItems >= n) *total = before + block_total;
@@ -496,10 +509,13 @@ __global__ __launch_bounds__(kThreads) void emit_kernel(int64_t n, int64_t num_p
 		cnt = (rc.y & 0xffffu) * (rc.y >> 16);
 		gid = order[g];
 	}
-	// The wave's run [run_start, run_end): from its first gaussian's offset to its last one's end.
+	// The wave's run [run_start, run_end): from its first gaussian's offset to its last one's end,
+	// cut at the pair count (which also bounds the loop when a failed count scan left the offsets
+	// meaningless: device_count then gives 0 pairs).
 	const int valid = first < n ? (int)min((int64_t)HDS_WAVE, n - first) : 0;
 	const uint32_t run_start = __shfl(off, 0, HDS_WAVE);
-	const uint32_t run_end = valid > 0 ? __shfl(off + cnt, valid - 1, HDS_WAVE) : run_start;
+	uint32_t run_end = valid > 0 ? __shfl(off + cnt, valid - 1, HDS_WAVE) : run_start;
+	if ((int64_t)run_end > num_pairs) run_end = (uint32_t)num_pairs;
 	s_off[wave][lane] = real ? off : 0xffffffffu;  // padding lanes never own a pair
 	hds_wave_fence();
 
@@ -544,11 +560,20 @@ __global__ __launch_bounds__(kThreads) void zero_kernel(uint32_t* __restrict__ a
 // range where the key before it differs and ends it where the key after it differs. A thread takes
 // kRangeItems consecutive pairs with two 16-byte loads (keys are 256-byte aligned), plus the keys
 // on either side.
+// When the pair sort's look-back gave up (*sort_error set), the sorted list cannot be trusted and
+// some of its slots may never have been written: no range is written (the ranges were zeroed
+// before the emit, so every tile is empty and nothing indexes the list) and the failure is copied
+// to *report, the word hds_bin_status hands to the host.
 constexpr int kRangeItems = 8;
 __global__ __launch_bounds__(kThreads) void ranges_kernel(int64_t num_pairs, const uint64_t* __restrict__ pairs_total,
 														   const uint32_t* __restrict__ tile_keys, int64_t num_tiles,
+														   const uint32_t* __restrict__ sort_error, uint32_t* __restrict__ report,
 														   int2* __restrict__ ranges) {
 	const int64_t p0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * kRangeItems;
+	if (*sort_error != 0u) {
+		if (blockIdx.x == 0 && threadIdx.x == 0) *report = 1u;
+		return;
+	}
 	num_pairs = device_count(pairs_total, num_pairs);
 	if (p0 >= num_pairs) return;
 	// k[j] = key of pair p0 - 1 + j; outside [0, num_pairs) a value no tile has.
@@ -584,8 +609,8 @@ inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 // flag sit together so that hds_bin_count reads both back in one 16-byte copy.
 struct Control {
 	uint64_t total;
-	uint32_t error;
-	uint32_t pad;
+	uint32_t error;       // a look-back of the depth sort or the scan gave up
+	uint32_t pair_error;  // (gaussian workspace) a look-back of the pair sort gave up
 	uint32_t tickets[kMaxPasses + 1];  // one per radix pass, then the scan's
 	uint32_t hist[kMaxPasses * kHistWords];
 };
@@ -710,17 +735,19 @@ int bin_count_launch(int64_t n, const float* means2D, const float* depths, const
 	if (st != HDS_OK) return st;
 	HdsKernelTimer timer3("scan_kernel", s);
 	scan_kernel<<<(unsigned)parts_of(n), kThreads, 0, s>>>(rects_sorted, n, offsets, scan_status,
-															ctrl->tickets + kMaxPasses, &ctrl->error, &ctrl->total);
+															ctrl->tickets + kMaxPasses, &ctrl->error,
+															g_spin_limit.load(std::memory_order_relaxed), &ctrl->total);
 	timer3.stop();
 	HDS_LAUNCH_CHECK("scan_tile_counts", s);
 	*launched = true;
 	return HDS_OK;
 }
 
-// The (pair count, error flag) words hds_bin_count_async copies out.
+// The (pair count, error flags) words hds_bin_count_async and hds_bin_status copy out: the first
+// three fields of the gaussian workspace's Control block.
 struct CountWords {
 	uint64_t total;
-	uint32_t error, pad;
+	uint32_t error, pair_error;
 };
 
 const CountWords* count_words(const void* workspace, int64_t n) {
@@ -729,7 +756,7 @@ const CountWords* count_words(const void* workspace, int64_t n) {
 
 // Enqueues the emitting half. With exact, num_pairs is the pair count; otherwise it is the
 // capacity the buffers were sized for and the kernels take min(count in the workspace, capacity).
-int bin_emit_launch(int64_t n, int64_t num_pairs, bool exact, int width, int height, const void* workspace,
+int bin_emit_launch(int64_t n, int64_t num_pairs, bool exact, int width, int height, void* workspace,
 					void* pairs_workspace, size_t pairs_workspace_bytes, int32_t* values_sorted, int32_t* tile_ranges,
 					hipStream_t s) {
 	HDS_REQUIRE(width > 0 && height > 0, "bin_emit: image size %dx%d must be positive", width, height);
@@ -751,7 +778,7 @@ int bin_emit_launch(int64_t n, int64_t num_pairs, bool exact, int width, int hei
 				pairs_workspace_bytes, p.bytes);
 	HDS_REQUIRE(workspace && values_sorted, "bin_emit: null pointer argument");
 	const GaussianSpace g = gaussian_space(n);
-	void* ws = const_cast<void*>(workspace);
+	void* ws = workspace;
 	const uint64_t* total = exact ? nullptr : &count_words(workspace, n)->total;
 	const uint32_t* offsets = at<uint32_t>(ws, g.offsets);
 	const uint32_t* order = at<uint32_t>(ws, g.vals_a);
@@ -785,8 +812,9 @@ int bin_emit_launch(int64_t n, int64_t num_pairs, bool exact, int width, int hei
 	if (st != HDS_OK) return st;
 	const uint32_t* keys_sorted = (passes % 2 == 0) ? keys_a : keys_b;
 	HdsKernelTimer timer3("ranges_kernel", s);
-	ranges_kernel<<<hds_blocks((num_pairs + kRangeItems - 1) / kRangeItems, kThreads), kThreads, 0, s>>>(num_pairs, total, keys_sorted, num_tiles,
-																		reinterpret_cast<int2*>(tile_ranges));
+	ranges_kernel<<<hds_blocks((num_pairs + kRangeItems - 1) / kRangeItems, kThreads), kThreads, 0, s>>>(
+		num_pairs, total, keys_sorted, num_tiles, &ctrl->error, &at<Control>(ws, g.ctrl)->pair_error,
+		reinterpret_cast<int2*>(tile_ranges));
 	timer3.stop();
 	HDS_LAUNCH_CHECK("identify_tile_ranges", s);
 	return HDS_OK;
@@ -835,14 +863,31 @@ extern "C" int hds_bin_count_async(int64_t n, const float* means2D, const float*
 	return HDS_OK;
 }
 
-extern "C" int hds_bin_emit(int64_t n, int64_t num_pairs, int width, int height, const void* workspace,
+extern "C" int hds_bin_status(int64_t n, const void* workspace, void* status_host, hds_stream_t stream) {
+	HDS_REQUIRE(status_host, "bin_status: status_host must not be NULL");
+	if (n <= 0) {
+		*static_cast<CountWords*>(status_host) = CountWords{0, 0, 0};
+		return HDS_OK;
+	}
+	HDS_REQUIRE(workspace, "bin_status: workspace must not be NULL");
+	HDS_HIP(hipMemcpyAsync(status_host, count_words(workspace, n), sizeof(CountWords), hipMemcpyDeviceToHost,
+						   (hipStream_t)stream));
+	return HDS_OK;
+}
+
+extern "C" int hds_set_lookback_limit(uint32_t polls) {
+	g_spin_limit.store(polls, std::memory_order_relaxed);
+	return HDS_OK;
+}
+
+extern "C" int hds_bin_emit(int64_t n, int64_t num_pairs, int width, int height, void* workspace,
 							void* pairs_workspace, size_t pairs_workspace_bytes, int32_t* values_sorted,
 							int32_t* tile_ranges, hds_stream_t stream) {
 	return bin_emit_launch(n, num_pairs, true, width, height, workspace, pairs_workspace, pairs_workspace_bytes,
 						   values_sorted, tile_ranges, (hipStream_t)stream);
 }
 
-extern "C" int hds_bin_emit_capped(int64_t n, int64_t capacity, int width, int height, const void* workspace,
+extern "C" int hds_bin_emit_capped(int64_t n, int64_t capacity, int width, int height, void* workspace,
 								   void* pairs_workspace, size_t pairs_workspace_bytes, int32_t* values_sorted,
 								   int32_t* tile_ranges, hds_stream_t stream) {
 	return bin_emit_launch(n, capacity, false, width, height, workspace, pairs_workspace, pairs_workspace_bytes,

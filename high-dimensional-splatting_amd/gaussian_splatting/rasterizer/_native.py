@@ -44,6 +44,8 @@ PROTOTYPES = {
     "hds_pairs_workspace_bytes": (_sz, [_i64, _i32, _i32]),
     "hds_bin_emit": (_i32, [_i64, _i64, _i32, _i32, _vp, _vp, _sz, _vp, _vp, _vp]),
     "hds_bin_emit_capped": (_i32, [_i64, _i64, _i32, _i32, _vp, _vp, _sz, _vp, _vp, _vp]),
+    "hds_bin_status": (_i32, [_i64, _vp, _vp, _vp]),
+    "hds_set_lookback_limit": (_i32, [ctypes.c_uint32]),
     "hds_render": (_i32, [_i64, _i32, _i32, _i32, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                           _vp]),
     "hds_render_backward": (_i32, [_i64, _i32, _i32, _i32, _i32, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp,
@@ -175,6 +177,16 @@ class StageTimer:
         return out
 
 
+def _raise_on_sort_error(status: torch.Tensor) -> None:
+    """Raises if the (pair count, depth/scan flag | pair-sort flag << 32) words of hds_bin_status
+    report a look-back that gave up."""
+    word = int(status[1])
+    if word & 0xFFFFFFFF:
+        raise RuntimeError("bin_count: a sort or scan look-back did not complete")
+    if (word >> 32) & 0xFFFFFFFF:
+        raise RuntimeError("bin_emit: a look-back of the tile sort did not complete (every tile range left empty)")
+
+
 class PendingBins:
     """A binning enqueued by HipRasterizer.bin_async whose pair count the host has not read yet.
 
@@ -182,7 +194,7 @@ class PendingBins:
     `color_opacity4` are final as soon as the stream has run the binning."""
 
     def __init__(self, values, tile_ranges, conic4, color_opacity4, *, capacity=None, event=None, count=None,
-                 workspace=None, emit_args=None):
+                 workspace=None, emit_args=None, status=None, status_event=None):
         self.values = values
         self.tile_ranges = tile_ranges
         self.conic4 = conic4
@@ -192,6 +204,8 @@ class PendingBins:
         self.count = count              # pinned int64 [2]: pair count, look-back error flag
         self.workspace = workspace      # per-gaussian workspace the exact re-emit reads
         self.emit_args = emit_args      # (n, width, height, device)
+        self.status = status            # pinned int64 [2] of hds_bin_status after the capped emit
+        self.status_event = status_event  # recorded after that copy
 
 
 class HipRasterizer:
@@ -327,6 +341,12 @@ class HipRasterizer:
                               dtype=torch.uint8)
             self._run("bin_emit", lambda: self.lib.hds_bin_emit(n, p, width, height, _ptr(ws), _ptr(pws), pws.numel(), _ptr(values_sorted),
                                          _ptr(tile_ranges), stream))
+            if p:
+                # The pair sort's look-back flag (a failed sort leaves every tile range empty).
+                status = torch.zeros(2, dtype=torch.int64, pin_memory=True)
+                _check(self.lib.hds_bin_status(n, _ptr(ws), _ptr(status), stream))
+                torch.cuda.current_stream(dev).synchronize()
+                _raise_on_sort_error(status)
         return values_sorted, tile_ranges, conic4, color_opacity4
 
     def bin_async(self, means2D, depths, radii, conics, colors, opacities, width, height) -> PendingBins:
@@ -364,8 +384,13 @@ class HipRasterizer:
             pws = torch.empty(self.lib.hds_pairs_workspace_bytes(cap, width, height), device=dev, dtype=torch.uint8)
             self._run("bin_emit", lambda: self.lib.hds_bin_emit_capped(
                 n, cap, width, height, _ptr(ws), _ptr(pws), pws.numel(), _ptr(values), _ptr(tile_ranges), stream))
+            status = torch.zeros(2, dtype=torch.int64, pin_memory=True)
+            _check(self.lib.hds_bin_status(n, _ptr(ws), _ptr(status), stream))
+            status_event = torch.cuda.Event()
+            status_event.record()
         return PendingBins(values, tile_ranges, conic4, color_opacity4, capacity=cap, event=event, count=count,
-                           workspace=ws, emit_args=(n, width, height, dev))
+                           workspace=ws, emit_args=(n, width, height, dev), status=status,
+                           status_event=status_event)
 
     def resolve(self, pending: PendingBins) -> bool:
         """Reads the pair count of a bin_async binning (waiting for its copy only, not for later
@@ -381,6 +406,9 @@ class HipRasterizer:
         pending.capacity = None
         if error:
             raise RuntimeError("bin_count: a sort or scan look-back did not complete")
+        # The capped emit's pair sort (its copy of the flags follows the sort, ahead of the render).
+        pending.status_event.synchronize()
+        _raise_on_sort_error(pending.status)
         if total >= 2**31 - 1:
             raise RuntimeError(f"bin_count: {total} tile-gaussian pairs overflow int32 indices")
         self._remember_pairs(dev, total)
@@ -394,6 +422,10 @@ class HipRasterizer:
             self._run("bin_emit", lambda: self.lib.hds_bin_emit(
                 n, total, width, height, _ptr(pending.workspace), _ptr(pws), pws.numel(), _ptr(values),
                 _ptr(pending.tile_ranges), _stream(dev)))
+            status = torch.zeros(2, dtype=torch.int64, pin_memory=True)
+            _check(self.lib.hds_bin_status(n, _ptr(pending.workspace), _ptr(status), _stream(dev)))
+            torch.cuda.current_stream(dev).synchronize()
+            _raise_on_sort_error(status)
         pending.values = values
         return True
 

@@ -104,8 +104,9 @@ HDS_API int hds_bin_count(int64_t n, const float* means2D, const float* depths, 
 /* hds_bin_count without the blocking read (forward.cu:311-326 with the host read deferred):
  * enqueues the same work, then an asynchronous copy of 16 bytes to count_host, which must be
  * pinned host memory (hipHostMalloc): uint64 P, uint32 look-back error flag (nonzero = the
- * counts are invalid), uint32 padding. The words are valid once the stream has passed this
- * call; the caller checks them before trusting what hds_bin_emit_capped produced. */
+ * counts are invalid), uint32 tile-sort flag (zero here; hds_bin_status reads it after the emit).
+ * The words are valid once the stream has passed this call; the caller checks them before
+ * trusting what hds_bin_emit_capped produced. */
 HDS_API int hds_bin_count_async(int64_t n, const float* means2D, const float* depths, const float* radii,
 						const float* conics, const float* colors, const float* opacities, int width,
 						int height, float* conic4, float* color_opacity4, void* workspace,
@@ -116,8 +117,10 @@ HDS_API size_t hds_pairs_workspace_bytes(int64_t num_pairs, int width, int heigh
 
 /* forward.cu:340-404: emits the (tile, gaussian) pairs, orders them by (tile, depth) keeping
  * index order on ties, and builds the per-tile [start, end) ranges, (0, 0) when untouched.
- * values_sorted [P] int32, tile_ranges [T,2] int32. */
-HDS_API int hds_bin_emit(int64_t n, int64_t num_pairs, int width, int height, const void* workspace,
+ * values_sorted [P] int32, tile_ranges [T,2] int32. If a look-back of the tile sort gives up
+ * (bounded wait, see hds_set_lookback_limit), every tile range is left (0, 0), so nothing reads
+ * the unsorted list, and the flag is raised in `workspace` for hds_bin_status. */
+HDS_API int hds_bin_emit(int64_t n, int64_t num_pairs, int width, int height, void* workspace,
 				 void* pairs_workspace, size_t pairs_workspace_bytes, int32_t* values_sorted,
 				 int32_t* tile_ranges, hds_stream_t stream);
 
@@ -128,9 +131,25 @@ HDS_API int hds_bin_emit(int64_t n, int64_t num_pairs, int width, int height, co
  * the depth order are sorted: tile_ranges stay consistent with what was written (every range
  * lies in [0, capacity)) but the binning is incomplete, and the caller runs hds_bin_emit again
  * with buffers for P. With the error flag set nothing is emitted (all ranges (0, 0)). */
-HDS_API int hds_bin_emit_capped(int64_t n, int64_t capacity, int width, int height, const void* workspace,
+HDS_API int hds_bin_emit_capped(int64_t n, int64_t capacity, int width, int height, void* workspace,
 						void* pairs_workspace, size_t pairs_workspace_bytes, int32_t* values_sorted,
 						int32_t* tile_ranges, hds_stream_t stream);
+
+/* No counterpart in the reference (CUB's sort reports nothing): enqueues an asynchronous copy of
+ * the binning's 16 status bytes from `workspace` (the one hds_bin_count(_async) filled for n
+ * gaussians) to pinned host memory status_host: uint64 pair count P, uint32 flag of the depth sort
+ * and count scan, uint32 flag of the tile sort of the last hds_bin_emit(_capped); a nonzero flag
+ * means a look-back gave up and the binning must not be used. Valid once the stream has passed
+ * this call. */
+HDS_API int hds_bin_status(int64_t n, const void* workspace, void* status_host, hds_stream_t stream);
+
+/* No counterpart in the reference; for tests of the failure path. Polls a look-back of the
+ * binning's sorts and scan makes on a silent predecessor before it gives up and raises its flag
+ * (HDS_LOOKBACK_LIMIT_DEFAULT, seconds of waiting). 0 makes every look-back give up before its
+ * first poll, so the failure is certain while every kernel still runs to its end. Applies to
+ * launches made after the call, on every thread. */
+#define HDS_LOOKBACK_LIMIT_DEFAULT 4194304u
+HDS_API int hds_set_lookback_limit(uint32_t polls);
 
 /* ---- blend forward: replaces render_gaussians (forward.cu:406-434) and rasterize_features
  *      (features.cu:299-346) with one tile walk ------------------------------------------------ */
