@@ -61,9 +61,11 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.orc_eval_sh_backward_adam.restype = None
     lib.orc_bin_count.argtypes = [i64, vp, vp, vp, vp, i32, i32, vp, vp]
     lib.orc_bin_count.restype = i64
-    lib.orc_bin_fill.argtypes = [i64, vp, vp, vp, i32, i32, i64, vp, vp]
+    lib.orc_bin_fill.argtypes = [i64, vp, vp, vp, i32, i32, i64, vp, vp, vp]
     lib.orc_bin_fill.restype = None
-    lib.orc_render_forward.argtypes = [i32, i32, vp, vp, vp, vp, vp, vp, vp, vp, i32, vp, vp, vp, vp]
+    lib.orc_bin_count_masked.argtypes = [i64, vp, vp, i32]
+    lib.orc_bin_count_masked.restype = i64
+    lib.orc_render_forward.argtypes = [i32, i32, vp, vp, vp, vp, vp, vp, vp, vp, i32, vp, vp, vp, vp, vp]
     lib.orc_render_forward.restype = None
     lib.orc_render_backward.argtypes = [i32, i32, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp,
                                         vp, i32, vp, vp, vp, vp, vp]
@@ -168,10 +170,14 @@ def tile_counts(means2D, radii, conics, opacities, width, height):
     return counts, rects
 
 
-def bin_gaussians(means2D, depths, radii, conics, opacities, width, height):
+def bin_gaussians(means2D, depths, radii, conics, opacities, width, height, tile_mask=None):
     """Binning of rasterize (forward.cu:13-139).
 
     Returns (counts [N] int32, values_sorted [P] int32, tile_ranges [T, 2] int32).
+
+    tile_mask ([T] bool, optional) keeps only the pairs of the selected tiles: their lists equal
+    the full binning's lists for those tiles, every other tile is empty, and values_sorted holds
+    only the selected tiles' pairs. counts stay the full per-gaussian tile counts.
     """
     means2D, depths, radii, conics = _f32(means2D), _f32(depths), _f32(radii), _f32(conics)
     opacities = _f32(opacities).reshape(-1)
@@ -182,17 +188,27 @@ def bin_gaussians(means2D, depths, radii, conics, opacities, width, height):
     lib = _load()
     total = lib.orc_bin_count(n, _p(means2D), _p(radii), _p(conics), _p(opacities), width, height,
                               _p(counts), _p(rects))
+    mask = None
+    if tile_mask is not None:
+        mask = np.ascontiguousarray(np.asarray(tile_mask, dtype=np.uint8).reshape(-1))
+        assert mask.size == tiles, (mask.size, tiles)
+        total = lib.orc_bin_count_masked(n, _p(rects), _p(mask), width)
     values = np.empty(total, np.int32)
     ranges = np.zeros((tiles, 2), np.int32)
-    lib.orc_bin_fill(n, _p(depths), _p(counts), _p(rects), width, height, total, _p(values), _p(ranges))
+    lib.orc_bin_fill(n, _p(depths), _p(counts), _p(rects), width, height, total, _p(mask), _p(values),
+                     _p(ranges))
     return counts, values, ranges
 
 
 def render_forward(width, height, tile_ranges, values_sorted, means2D, conics, opacities, colors=None,
-                   background=None, features=None):
+                   background=None, features=None, near_cut=False):
     """Front-to-back blend (forward.cu:141-237, features.cu:116-282).
 
-    Returns (image [H, W, 3] or None, final_T [H, W], n_contrib [H, W], feature_image [H, W, C] or None).
+    Returns (image [H, W, 3] or None, final_T [H, W], n_contrib [H, W], feature_image [H, W, C] or None),
+    and with near_cut=True also a [H, W] bool mask of the pixels whose walk passed an alpha or a
+    transmittance within twice its propagated rounding uncertainty of the 1/255 or 1e-4 cut:
+    the decisions that other rounding (the GPU's hardware exp2 and fused multiply-adds against libm's
+    expf and separate products) can flip.
     """
     ranges, values = _i32(tile_ranges), _i32(values_sorted)
     means2D, conics, opacities = _f32(means2D), _f32(conics), _f32(opacities).reshape(-1)
@@ -204,9 +220,12 @@ def render_forward(width, height, tile_ranges, values_sorted, means2D, conics, o
     final_T = np.empty((height, width), np.float32)
     n_contrib = np.empty((height, width), np.int32)
     fimg = np.empty((height, width, channels), np.float32) if feats is not None else None
+    near = np.zeros((height, width), np.uint8) if near_cut else None
     _load().orc_render_forward(width, height, _p(ranges), _p(values), _p(means2D), _p(conics), _p(opacities),
                                _p(colors), _p(bg), _p(feats), channels, _p(image), _p(final_T), _p(n_contrib),
-                               _p(fimg))
+                               _p(fimg), _p(near))
+    if near_cut:
+        return image, final_T, n_contrib, fimg, near.astype(bool)
     return image, final_T, n_contrib, fimg
 
 

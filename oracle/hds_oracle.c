@@ -18,9 +18,11 @@
  *   - The natural log inside tile_rect is hds_logf (hds_common.h), shared with the HIP kernels,
  *     so integer binning results can be compared bit for bit.
  *
- * Pinning (how this oracle is itself checked; see tests/test_oracle_*.py):
- *   projection fwd: closed-form special cases and rigid-motion / mirror invariance;
- *   projection bwd: central finite differences of the forward, in float64 on the restated math;
+ * Pinning (how this oracle is itself checked; see tests/test_oracle_pinning.py):
+ *   projection fwd: closed form of an isotropic gaussian on the axis, near-plane and off-screen
+ *     culling, an independent float64 torch matrix formulation, rigid motion of scene and camera;
+ *   projection bwd: torch autograd of that float64 matrix formulation, including the clamped
+ *     field-of-view and near-plane branches;
  *   SH fwd: orthonormality of the basis on the sphere, rgb_to_sh inverse, hand values at the poles;
  *   SH bwd + Adam: torch autograd of the closed form and torch.optim.Adam(fused=False);
  *   binning: brute-force enumeration of every (tile, gaussian) with the alpha test in float64;
@@ -34,6 +36,7 @@
 #include <string.h>
 
 #include "hds_common.h"
+#include "hds_ewa.h"
 
 #define ORC_EXPORT __attribute__((visibility("default")))
 
@@ -50,195 +53,39 @@ ORC_EXPORT int orc_tile_rect(float ux, float uy, float a, float b, float c, floa
 }
 
 /* ------------------------------------------------------------------------------------------- */
-/* Projection: projection.cu:36-111 (forward), 114-197 (backward); constants projection.py:3-5. */
+/* Projection: project_gaussians, projection.cu:36-111 (forward) and 114-197 (backward),         */
+/* constants projection.py:3-5. The per-gaussian arithmetic is hds_ewa.h, shared with the HIP     */
+/* kernels (the same bits on both sides); tests/test_oracle_pinning.py pins it against an         */
+/* independent float64 matrix formulation and its autograd, closed forms and rigid motion.        */
 /* ------------------------------------------------------------------------------------------- */
 
-typedef struct {
-	float fx, fy, cx, cy;
-	int width, height;
-	float near_plane, low_pass, fov_scale;
-} orc_camera;
-
-typedef struct {
-	float R[3][3], t[3], p[3];
-	float z, z_inv, jx, jy;
-	int clamped_x, clamped_y, behind;
-	float jw[2][3], M[3][3], T[2][3];
-	float a, b, c, det;
-} orc_projected;
-
-/* Rotation of a unit quaternion (w, x, y, z): projection.cu:15-20, projection.py:8-22. */
-static void orc_quat_to_rotmat(const float* q, float r[3][3]) {
-	const float w = q[0], x = q[1], y = q[2], z = q[3];
-	r[0][0] = 1 - 2 * (y * y + z * z);
-	r[0][1] = 2 * (x * y - w * z);
-	r[0][2] = 2 * (x * z + w * y);
-	r[1][0] = 2 * (x * y + w * z);
-	r[1][1] = 1 - 2 * (x * x + z * z);
-	r[1][2] = 2 * (y * z - w * x);
-	r[2][0] = 2 * (x * z - w * y);
-	r[2][1] = 2 * (y * z + w * x);
-	r[2][2] = 1 - 2 * (x * x + y * y);
-}
-
-/* EWA projection with the clamped Jacobian and the low-pass term: projection.cu:36-77. */
-static void orc_project_one(const orc_camera* cam, const float* w2c, const float* mean,
-							const float* scale, const float* quat, orc_projected* g) {
-	for (int i = 0; i < 3; i++) {
-		for (int j = 0; j < 3; j++) g->R[i][j] = w2c[i * 4 + j];
-		g->t[i] = w2c[i * 4 + 3];
-		g->p[i] = g->R[i][0] * mean[0] + g->R[i][1] * mean[1] + g->R[i][2] * mean[2] + g->t[i];
-	}
-	g->behind = g->p[2] <= cam->near_plane;
-	g->z = fmaxf(g->p[2], cam->near_plane);
-	g->z_inv = 1.0f / (g->z + 1e-6f);
-
-	const float limit_x = cam->fov_scale * (0.5f * (float)cam->width / cam->fx);
-	const float limit_y = cam->fov_scale * (0.5f * (float)cam->height / cam->fy);
-	const float rx = g->p[0] * g->z_inv, ry = g->p[1] * g->z_inv;
-	g->clamped_x = fabsf(rx) > limit_x;
-	g->clamped_y = fabsf(ry) > limit_y;
-	g->jx = fminf(fmaxf(rx, -limit_x), limit_x) * g->z;
-	g->jy = fminf(fmaxf(ry, -limit_y), limit_y) * g->z;
-
-	const float zz_inv = g->z_inv * g->z_inv;
-	for (int j = 0; j < 3; j++) {
-		g->jw[0][j] = cam->fx * g->z_inv * g->R[0][j] - cam->fx * g->jx * zz_inv * g->R[2][j];
-		g->jw[1][j] = cam->fy * g->z_inv * g->R[1][j] - cam->fy * g->jy * zz_inv * g->R[2][j];
-	}
-	float rot[3][3];
-	orc_quat_to_rotmat(quat, rot);
-	for (int j = 0; j < 3; j++)
-		for (int k = 0; k < 3; k++) g->M[j][k] = rot[j][k] * scale[k];
-	for (int r = 0; r < 2; r++)
-		for (int k = 0; k < 3; k++)
-			g->T[r][k] = g->jw[r][0] * g->M[0][k] + g->jw[r][1] * g->M[1][k] + g->jw[r][2] * g->M[2][k];
-	g->a = g->T[0][0] * g->T[0][0] + g->T[0][1] * g->T[0][1] + g->T[0][2] * g->T[0][2] + cam->low_pass;
-	g->b = g->T[0][0] * g->T[1][0] + g->T[0][1] * g->T[1][1] + g->T[0][2] * g->T[1][2];
-	g->c = g->T[1][0] * g->T[1][0] + g->T[1][1] * g->T[1][1] + g->T[1][2] * g->T[1][2] + cam->low_pass;
-	g->det = g->a * g->c - g->b * g->b;
-}
-
-/* project_forward: projection.cu:80-111. */
 ORC_EXPORT void orc_project_forward(int64_t n, const float* means, const float* scales,
 									const float* quats, const float* opacities, const float* w2c,
 									float fx, float fy, float cx, float cy, int width, int height,
 									float near_plane, float low_pass, float fov_scale,
 									float* means2D, float* depths, float* radii, float* conics) {
-	const orc_camera cam = {fx, fy, cx, cy, width, height, near_plane, low_pass, fov_scale};
-	const int tiles_x = (width + HDS_TILE - 1) / HDS_TILE;
-	const int tiles_y = (height + HDS_TILE - 1) / HDS_TILE;
+	const hds_camera cam = {fx, fy, cx, cy, width, height, near_plane, low_pass, fov_scale};
 #pragma omp parallel for schedule(static)
 	for (int64_t i = 0; i < n; i++) {
-		orc_projected g;
-		orc_project_one(&cam, w2c, means + i * 3, scales + i * 3, quats + i * 4, &g);
-		const float u = cam.fx * g.p[0] / g.z + cam.cx;
-		const float v = cam.fy * g.p[1] / g.z + cam.cy;
-		means2D[i * 2 + 0] = u;
-		means2D[i * 2 + 1] = v;
-		depths[i] = g.p[2];
-		const float scale_inv = g.det > 0.0f ? 1.0f / g.det : 1.0f;
-		const float a_conic = g.c * scale_inv;
-		const float b_conic = -g.b * scale_inv;
-		const float c_conic = g.a * scale_inv;
-		conics[i * 3 + 0] = a_conic;
-		conics[i * 3 + 1] = b_conic;
-		conics[i * 3 + 2] = c_conic;
-		const float trace = g.a + g.c;
-		const float radius = 3.0f * sqrtf(0.5f * (trace + sqrtf(fmaxf(trace * trace - 4.0f * g.det, 0.0f))));
-		int x0, y0, w, h;
-		const int visible = !g.behind && g.det > 0.0f &&
-							hds_tile_rect(u, v, a_conic, b_conic, c_conic, opacities[i], tiles_x,
-										  tiles_y, &x0, &y0, &w, &h);
-		radii[i] = visible ? radius : 0.0f;
+		hds_ewa g;
+		hds_ewa_project(&cam, w2c, means + i * 3, scales + i * 3, quats + i * 4, &g);
+		hds_ewa_screen(&cam, &g, opacities[i], means2D + i * 2, depths + i, conics + i * 3, radii + i);
 	}
 }
 
-/* project_backward: projection.cu:114-197. */
 ORC_EXPORT void orc_project_backward(int64_t n, const float* grad_means2D, const float* grad_conics,
 									 const float* means, const float* scales, const float* quats,
 									 const float* w2c, float fx, float fy, float cx, float cy,
 									 int width, int height, float near_plane, float low_pass,
 									 float fov_scale, float* grad_means, float* grad_scales,
 									 float* grad_quats) {
-	const orc_camera cam = {fx, fy, cx, cy, width, height, near_plane, low_pass, fov_scale};
+	const hds_camera cam = {fx, fy, cx, cy, width, height, near_plane, low_pass, fov_scale};
 #pragma omp parallel for schedule(static)
 	for (int64_t i = 0; i < n; i++) {
-		const float* scale = scales + i * 3;
-		const float* quat = quats + i * 4;
-		orc_projected g;
-		orc_project_one(&cam, w2c, means + i * 3, scale, quat, &g);
-
-		const float g0 = grad_conics[i * 3 + 0], g1 = grad_conics[i * 3 + 1], g2 = grad_conics[i * 3 + 2];
-		float da, db, dc;
-		if (g.det > 0.0f) {
-			/* conic = (c, -b, a) / det, differentiated through det = a c - b^2. */
-			const float inv = 1.0f / g.det, inv2 = inv * inv;
-			da = inv2 * (-g0 * g.c * g.c + g1 * g.b * g.c - g2 * g.b * g.b);
-			db = inv2 * (2.0f * g0 * g.b * g.c + 2.0f * g2 * g.a * g.b) - g1 * (inv + 2.0f * g.b * g.b * inv2);
-			dc = inv2 * (-g0 * g.b * g.b + g1 * g.a * g.b - g2 * g.a * g.a);
-		} else {
-			da = g2;
-			db = -g1;
-			dc = g0;
-		}
-		float dT[2][3];
-		for (int k = 0; k < 3; k++) {
-			dT[0][k] = 2.0f * da * g.T[0][k] + db * g.T[1][k];
-			dT[1][k] = 2.0f * dc * g.T[1][k] + db * g.T[0][k];
-		}
-		float rot[3][3];
-		orc_quat_to_rotmat(quat, rot);
-		float djw[2][3], drot[3][3], dscale[3] = {0.0f, 0.0f, 0.0f};
-		for (int j = 0; j < 3; j++) {
-			djw[0][j] = dT[0][0] * g.M[j][0] + dT[0][1] * g.M[j][1] + dT[0][2] * g.M[j][2];
-			djw[1][j] = dT[1][0] * g.M[j][0] + dT[1][1] * g.M[j][1] + dT[1][2] * g.M[j][2];
-			for (int k = 0; k < 3; k++) {
-				const float dM = g.jw[0][j] * dT[0][k] + g.jw[1][j] * dT[1][k];
-				dscale[k] += dM * rot[j][k];
-				drot[j][k] = dM * scale[k];
-			}
-		}
-		const float w = quat[0], x = quat[1], y = quat[2], z = quat[3];
-		grad_quats[i * 4 + 0] = 2.0f * (-drot[0][1] * z + drot[0][2] * y + drot[1][0] * z - drot[1][2] * x -
-										drot[2][0] * y + drot[2][1] * x);
-		grad_quats[i * 4 + 1] = 2.0f * (drot[0][1] * y + drot[0][2] * z + drot[1][0] * y - 2.0f * drot[1][1] * x -
-										drot[1][2] * w + drot[2][0] * z + drot[2][1] * w - 2.0f * drot[2][2] * x);
-		grad_quats[i * 4 + 2] = 2.0f * (-2.0f * drot[0][0] * y + drot[0][1] * x + drot[0][2] * w + drot[1][0] * x +
-										drot[1][2] * z - drot[2][0] * w + drot[2][1] * z - 2.0f * drot[2][2] * y);
-		grad_quats[i * 4 + 3] = 2.0f * (-2.0f * drot[0][0] * z - drot[0][1] * w + drot[0][2] * x + drot[1][0] * w -
-										2.0f * drot[1][1] * z + drot[1][2] * y + drot[2][0] * x + drot[2][1] * y);
-		for (int k = 0; k < 3; k++) grad_scales[i * 3 + k] = dscale[k];
-
-		const float zz_inv = g.z_inv * g.z_inv;
-		float dz_inv = 0.0f, djx = 0.0f, djy = 0.0f;
-		for (int j = 0; j < 3; j++) {
-			dz_inv += djw[0][j] * (cam.fx * g.R[0][j] - 2.0f * cam.fx * g.jx * g.z_inv * g.R[2][j]);
-			dz_inv += djw[1][j] * (cam.fy * g.R[1][j] - 2.0f * cam.fy * g.jy * g.z_inv * g.R[2][j]);
-			djx += djw[0][j] * (-cam.fx * zz_inv * g.R[2][j]);
-			djy += djw[1][j] * (-cam.fy * zz_inv * g.R[2][j]);
-		}
-		float dp[3] = {0.0f, 0.0f, 0.0f};
-		float dz = 0.0f;
-		/* jx = clamp(p.x / z) * z: the ratio only carries gradient inside the clamp. */
-		const float rx = g.jx / g.z, ry = g.jy / g.z;
-		dz += djx * rx + djy * ry;
-		if (!g.clamped_x) {
-			dp[0] += djx * g.z * g.z_inv;
-			dz_inv += djx * g.z * g.p[0];
-		}
-		if (!g.clamped_y) {
-			dp[1] += djy * g.z * g.z_inv;
-			dz_inv += djy * g.z * g.p[1];
-		}
-		const float gu = grad_means2D[i * 2 + 0], gv = grad_means2D[i * 2 + 1];
-		dp[0] += gu * cam.fx / g.z;
-		dp[1] += gv * cam.fy / g.z;
-		dz += -(gu * cam.fx * g.p[0] + gv * cam.fy * g.p[1]) / (g.z * g.z);
-		dz += dz_inv * (-zz_inv);
-		if (!g.behind) dp[2] += dz;
-		for (int k = 0; k < 3; k++)
-			grad_means[i * 3 + k] = g.R[0][k] * dp[0] + g.R[1][k] * dp[1] + g.R[2][k] * dp[2];
+		hds_ewa g;
+		hds_ewa_project(&cam, w2c, means + i * 3, scales + i * 3, quats + i * 4, &g);
+		hds_ewa_backward(&cam, w2c, scales + i * 3, quats + i * 4, &g, grad_means2D + i * 2, grad_conics + i * 3,
+						 grad_means + i * 3, grad_scales + i * 3, grad_quats + i * 4);
 	}
 }
 
@@ -458,14 +305,33 @@ static int orc_pair_cmp(const void* pa, const void* pb) {
 	return (a->gid > b->gid) - (a->gid < b->gid);
 }
 
+/* Pairs that fall in the tiles with tile_mask[tile] != 0 (tile_mask [T] bytes, row-major). */
+ORC_EXPORT int64_t orc_bin_count_masked(int64_t n, const int32_t* rects, const uint8_t* tile_mask, int width) {
+	const int tiles_x = (width + HDS_TILE - 1) / HDS_TILE;
+	int64_t total = 0;
+#pragma omp parallel for schedule(static) reduction(+ : total)
+	for (int64_t i = 0; i < n; i++) {
+		const int x0 = rects[i * 4], y0 = rects[i * 4 + 1], w = rects[i * 4 + 2], h = rects[i * 4 + 3];
+		for (int y = y0; y < y0 + h; y++)
+			for (int x = x0; x < x0 + w; x++) total += tile_mask[y * tiles_x + x] != 0;
+	}
+	return total;
+}
+
 /*
  * Emits every (tile, gaussian) pair, sorts by (tile, float bits of depth) keeping index order on
  * ties, and builds [start, end) per tile, zero for untouched tiles. Outputs values_sorted[P] and
  * tile_ranges[T][2] exactly as the reference rasterize returns them (forward.cu:434).
+ *
+ * With tile_mask != NULL only the pairs of the tiles whose mask byte is set are emitted: their
+ * lists are exactly the full binning's lists for those tiles (the order inside a tile depends only
+ * on the tile's own pairs), and every other tile is empty. Tiles are independent in the blend, so
+ * rendering such a binning reproduces the full frame on the masked tiles, and the backward with an
+ * upstream gradient that is zero outside them reproduces the full backward.
  */
 ORC_EXPORT void orc_bin_fill(int64_t n, const float* depths, const int32_t* counts,
 							 const int32_t* rects, int width, int height, int64_t num_pairs,
-							 int32_t* values_sorted, int32_t* tile_ranges) {
+							 const uint8_t* tile_mask, int32_t* values_sorted, int32_t* tile_ranges) {
 	const int tiles_x = (width + HDS_TILE - 1) / HDS_TILE;
 	const int tiles_y = (height + HDS_TILE - 1) / HDS_TILE;
 	orc_pair* pairs = (orc_pair*)malloc(sizeof(orc_pair) * (size_t)(num_pairs > 0 ? num_pairs : 1));
@@ -476,6 +342,7 @@ ORC_EXPORT void orc_bin_fill(int64_t n, const float* depths, const int32_t* coun
 		const int x0 = rects[i * 4], y0 = rects[i * 4 + 1], w = rects[i * 4 + 2], h = rects[i * 4 + 3];
 		for (int y = y0; y < y0 + h; y++)
 			for (int x = x0; x < x0 + w; x++) {
+				if (tile_mask && !tile_mask[y * tiles_x + x]) continue;
 				pairs[o].key = ((uint64_t)(uint32_t)(y * tiles_x + x) << 32) | depth_bits;
 				pairs[o].gid = (int32_t)i;
 				o++;
@@ -516,12 +383,26 @@ static inline float orc_alpha(float px, float py, const float* mean, const float
  * skipped but still counted in the list index; one that would leave T < 1e-4 ends the pixel
  * without blending. n_contrib is the 1-based list index of the last blended gaussian.
  */
+/*
+ * near_cut (optional, [H, W] bytes) marks the pixels whose walk passed a decision within rounding
+ * distance of its cut, where an implementation that rounds differently (a GPU's hardware exp2 and
+ * fused multiply-adds against libm's expf and separate products here) can decide the other way:
+ *   - a raw alpha against 1/255: alpha = op exp(-m / 2) is uncertain by a relative
+ *     eps_a = u (2 (|a dx^2| + 2 |b dx dy| + |c dy^2|) + m / 2 + 4), u = 2^-24: a few roundings of
+ *     the quadratic form's terms (which can cancel) carried through exp, the rounding of exp's
+ *     argument and a few ulps of exp itself;
+ *   - T (1 - alpha) against the 1e-4 floor, T carrying the sum of its factors' uncertainties
+ *     (alpha's, scaled by alpha / (1 - alpha), plus u per step).
+ * A decision counts as near when the value is within twice its uncertainty of the cut.
+ */
+#define ORC_U 5.9604645e-08f
+
 ORC_EXPORT void orc_render_forward(int width, int height, const int32_t* tile_ranges,
 								   const int32_t* values_sorted, const float* means2D,
 								   const float* conics, const float* opacities, const float* colors,
 								   const float* background, const float* features, int channels,
 								   float* image, float* final_T, int32_t* n_contrib,
-								   float* feature_image) {
+								   float* feature_image, uint8_t* near_cut) {
 	const int tiles_x = (width + HDS_TILE - 1) / HDS_TILE;
 	const int tiles_y = (height + HDS_TILE - 1) / HDS_TILE;
 	const int64_t num_tiles = (int64_t)tiles_x * tiles_y;
@@ -538,7 +419,8 @@ ORC_EXPORT void orc_render_forward(int width, int height, const int32_t* tile_ra
 					if (x >= width || y >= height) continue;
 					const float px = (float)x + 0.5f, py = (float)y + 0.5f;
 					float T = 1.0f, r = 0.0f, g = 0.0f, b = 0.0f;
-					int last = 0;
+					int last = 0, near = 0;
+					float eps_T = 0.0f;
 					for (int c = 0; c < channels; c++) acc[c] = 0.0f;
 					for (int j = start; j < end; j++) {
 						const int gid = values_sorted[j];
@@ -546,8 +428,15 @@ ORC_EXPORT void orc_render_forward(int width, int height, const int32_t* tile_ra
 						const float raw = orc_alpha(px, py, means2D + gid * 2, conics + gid * 3,
 													opacities[gid], &G, &dx, &dy);
 						const float alpha = fminf(HDS_MAX_ALPHA, raw);
+						const float* q = conics + gid * 3;
+						const float terms = fabsf(q[0] * dx * dx) + 2.0f * fabsf(q[1] * dx * dy) + fabsf(q[2] * dy * dy);
+						const float m = -2.0f * logf(G > 0.0f ? G : 1e-30f);
+						const float eps_a = ORC_U * (2.0f * terms + 0.5f * m + 4.0f);
+						near |= fabsf(raw - HDS_MIN_ALPHA) <= 2.0f * eps_a * raw;
 						if (alpha < HDS_MIN_ALPHA) continue;
 						const float test_T = T * (1.0f - alpha);
+						eps_T += ORC_U + eps_a * alpha / (1.0f - alpha);
+						near |= fabsf(test_T - HDS_MIN_TRANSMITTANCE) <= 2.0f * eps_T * test_T;
 						if (test_T < HDS_MIN_TRANSMITTANCE) break;
 						const float w = alpha * T;
 						if (colors) {
@@ -568,6 +457,7 @@ ORC_EXPORT void orc_render_forward(int width, int height, const int32_t* tile_ra
 					}
 					if (final_T) final_T[pix] = T;
 					if (n_contrib) n_contrib[pix] = last;
+					if (near_cut) near_cut[pix] = (uint8_t)near;
 					for (int c = 0; c < channels && feature_image; c++) feature_image[pix * channels + c] = acc[c];
 				}
 		}

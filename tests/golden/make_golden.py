@@ -11,7 +11,10 @@ hand_solved_pixels.json
     before the second gaussian.
 oracle_config0_small.npz
     Regression vectors of the CPU oracle (after it passes tests/test_oracle_pinning.py) on the first
-    2000 gaussians of BASELINE config 0: projection, binning and the RGB + 8-channel blend.
+    2000 gaussians of BASELINE config 0: projection, binning and the RGB + 8-channel blend. The inputs
+    (means, scales, quats, opacities, features, colours) are stored with the outputs: torch's CPU
+    generators and exp differ in the last bit between host CPUs, so regenerating them elsewhere would
+    not reproduce the same scene bit for bit.
 """
 import json
 import sys
@@ -66,8 +69,10 @@ def main():
     _, values, ranges = oracle.bin_gaussians(m2, d, r, c, np_(wl.opacities), cam["width"], cam["height"])
     image, fimg, _, _, _, _ = oracle.rasterize(m2, d, r, c, colors, np_(wl.opacities), cam["width"], cam["height"],
                                                np.zeros(3, np.float32), np_(wl.features))
-    np.savez_compressed(HERE / "oracle_config0_small.npz", n=n, means2D=m2, radii=r, values_sorted=values,
-                        tile_ranges=ranges, colors=colors, image=image, feature_image=fimg)
+    np.savez_compressed(HERE / "oracle_config0_small.npz", n=n, means=np_(wl.means), scales=np_(wl.scales),
+                        quats=np_(wl.quats), opacities=np_(wl.opacities), features=np_(wl.features), means2D=m2,
+                        depths=d, radii=r, conics=c, values_sorted=values, tile_ranges=ranges, colors=colors,
+                        image=image, feature_image=fimg)
 
 
 if __name__ == "__main__":

@@ -315,13 +315,24 @@ def test_rasterize_is_identical_with_and_without_the_pair_count_read():
 
 # ---- blend forward ----------------------------------------------------------------------------
 
-def oracle_render(inputs, width, height, background=None, features=None):
+def oracle_render(inputs, width, height, background=None, features=None, near_cut=False):
     m2, d, r, c, col, op = [np_(t) for t in inputs]
     _, values, ranges = oracle.bin_gaussians(m2, d, r, c, op, width, height)
-    image, final_T, n_contrib, fimg = oracle.render_forward(
-        width, height, ranges, values, m2, c, op, col,
-        None if background is None else np_(background), None if features is None else np_(features))
+    out = oracle.render_forward(width, height, ranges, values, m2, c, op, col,
+                                None if background is None else np_(background),
+                                None if features is None else np_(features), near_cut=near_cut)
+    image, final_T, n_contrib, fimg = out[:4]
+    if near_cut:
+        return image, fimg, final_T, n_contrib, values, ranges, out[4]
     return image, fimg, final_T, n_contrib, values, ranges
+
+
+def assert_same_decisions(n_contrib, want_nc, near):
+    """n_contrib equal on every pixel whose walk stayed clear of the alpha and transmittance cuts
+    (the oracle's near_cut mask, where other rounding can decide differently), and such pixels a
+    small share (a sanity bound of 2%: the adversarial elongated scenes flag about 0.2%)."""
+    assert near.mean() < 2e-2, f"{near.mean():.2e} of pixels near a cut"
+    np.testing.assert_array_equal(np_(n_contrib)[~near], want_nc[~near])
 
 
 def test_rgb_forward_matches_oracle():
@@ -329,13 +340,12 @@ def test_rgb_forward_matches_oracle():
     inputs = scene(0, 3000, width, height)
     bg = torch.tensor([0.3, 0.5, 0.7], device=DEV)
     image, final_T, n_contrib, values, ranges, _, _ = _get_rasterizer().rasterize(*inputs, bg, width, height)
-    want_image, _, want_T, want_nc, want_values, want_ranges = oracle_render(inputs, width, height, bg)
+    want_image, _, want_T, want_nc, want_values, want_ranges, near = oracle_render(inputs, width, height, bg,
+                                                                                  near_cut=True)
     np.testing.assert_array_equal(np_(values), want_values)
     assert_image_close(np_(image), want_image)
     assert_image_close(np_(final_T), want_T)
-    # exp differs by an ulp between libm and the GPU, which can flip a pixel's last contributor
-    # only for a gaussian sitting exactly on the 1/255 or 1e-4 cutoff.
-    assert (np_(n_contrib) != want_nc).mean() < 1e-3
+    assert_same_decisions(n_contrib, want_nc, near)
 
 
 @pytest.mark.parametrize("channels", [32, 64, 128, 256, 512])
@@ -523,18 +533,18 @@ def elongated_scene(seed, n, width, height):
 def test_block_cull_keeps_every_contributor(seed):
     """The blend kernels visit a gaussian in an 8x8 block only if the minimum of its quadratic form over
     the block's pixel-centre rectangle is under the 1/255 threshold; on adversarial ellipses the result
-    must still equal the oracle's (n_contrib equal up to exp ulps at the cut-offs, images and gradients
+    must still equal the oracle's (n_contrib equal away from the exp-rounding band at the cut-offs, images and gradients
     within the usual bars)."""
     width, height = 96, 80
     n = 3000
     inputs = elongated_scene(seed, n, width, height)
     bg = torch.tensor([0.3, 0.5, 0.7], device=DEV)
     image, final_T, n_contrib, values, ranges, _, _ = _get_rasterizer().rasterize(*inputs, bg, width, height)
-    want_image, _, want_T, want_nc, want_values, _ = oracle_render(inputs, width, height, bg)
+    want_image, _, want_T, want_nc, want_values, _, near = oracle_render(inputs, width, height, bg, near_cut=True)
     np.testing.assert_array_equal(np_(values), want_values)
     assert_image_close(np_(image), want_image)
     assert_image_close(np_(final_T), want_T)
-    assert (np_(n_contrib) != want_nc).mean() < 1e-3
+    assert_same_decisions(n_contrib, want_nc, near)
     g = torch.Generator().manual_seed(100 + seed)
     features = torch.rand(n, 32, generator=g).to(DEV)
     _, fimg = rasterize(*inputs, width, height, bg, features=features)
