@@ -285,6 +285,32 @@ def test_projection_matches_matrix_formulation_and_its_autograd():
     assert_grads_close(("means", "scales", "quats"), got, [t.grad.numpy() for t in leaves])
 
 
+def test_projection_backward_on_the_clamp_and_near_plane_branches_matches_autograd():
+    """Gaussians far outside the field of view (the Jacobian's x / z, y / z clamped) and behind the
+    near plane (z clamped to 0.2): the gradient flows only where the forward's clamps let it, as
+    torch autograd of the float64 matrix formulation says."""
+    g = gaussians(9, 600)
+    rng = np.random.default_rng(9)
+    means = g["means"].clone()
+    means[:200, 0] *= 6.0                                   # x / z far beyond 1.3 x the half field
+    means[200:400, 1] *= 6.0
+    means[400:500, 2] = torch.from_numpy(rng.uniform(-0.5, 0.2, 100).astype(np.float32))  # behind the near plane
+    cam = camera(120, 90)
+    args = (cam["fx"], cam["fy"], cam["cx"], cam["cy"], cam["width"], cam["height"])
+    w2c = torch.eye(4, dtype=torch.float64)
+    leaves = [means.double().requires_grad_(True), g["scales"].double().requires_grad_(True),
+              g["quats"].double().requires_grad_(True)]
+    tm2, _, tc, _ = ref.project_torch(*leaves, w2c, *args)
+    gm = rng.normal(size=(600, 2)).astype(np.float32)
+    gc = rng.normal(size=(600, 3)).astype(np.float32) * 10
+    torch.autograd.backward((tm2, tc), (torch.tensor(gm, dtype=torch.float64), torch.tensor(gc, dtype=torch.float64)))
+    got = oracle.project_backward(gm, gc, np_(means), np_(g["scales"]), np_(g["quats"]), np_(w2c), *args)
+    want = [t.grad.numpy() for t in leaves]
+    assert np.all(want[0][400:500, 2] == 0.0), "no depth gradient behind the near plane"
+    assert np.all(got[0][400:500, 2] == 0.0)
+    assert_grads_close(("means", "scales", "quats"), got, want)
+
+
 def test_rigid_motion_of_scene_and_camera_changes_nothing():
     g = gaussians(7, 800)
     rot = ref.quat_to_rotmat(F.normalize(torch.tensor([[0.9, 0.2, -0.3, 0.1]]), dim=-1))[0]
@@ -412,16 +438,15 @@ def test_ssim_of_image_with_itself_is_one():
 def test_config0_golden_vectors_are_reproduced():
     """Regression fixture: oracle outputs on a reduced config-0 scene (tests/golden/make_golden.py)."""
     data = np.load(GOLDEN / "oracle_config0_small.npz")
-    wl = synthetic_config(0, n=int(data["n"]), channels=int(data["feature_image"].shape[-1]))
-    cam = wl.cam
-    m2, d, r, c = oracle.project_forward(np_(wl.means), np_(wl.scales), np_(wl.quats), np_(wl.opacities), np.eye(4),
+    cam = synthetic_config(0, n=16).cam
+    m2, d, r, c = oracle.project_forward(data["means"], data["scales"], data["quats"], data["opacities"], np.eye(4),
                                          cam["fx"], cam["fy"], cam["cx"], cam["cy"], cam["width"], cam["height"])
-    np.testing.assert_array_equal(m2, data["means2D"])
-    np.testing.assert_array_equal(r, data["radii"])
-    counts, values, ranges = oracle.bin_gaussians(m2, d, r, c, np_(wl.opacities), cam["width"], cam["height"])
+    for name, got in (("means2D", m2), ("depths", d), ("radii", r), ("conics", c)):
+        np.testing.assert_array_equal(got, data[name], err_msg=name)
+    counts, values, ranges = oracle.bin_gaussians(m2, d, r, c, data["opacities"], cam["width"], cam["height"])
     np.testing.assert_array_equal(values, data["values_sorted"])
     np.testing.assert_array_equal(ranges, data["tile_ranges"])
-    image, fimg, T, nc, _, _ = oracle.rasterize(m2, d, r, c, data["colors"], np_(wl.opacities), cam["width"],
-                                               cam["height"], np.zeros(3, np.float32), np_(wl.features))
+    image, fimg, T, nc, _, _ = oracle.rasterize(m2, d, r, c, data["colors"], data["opacities"], cam["width"],
+                                               cam["height"], np.zeros(3, np.float32), data["features"])
     np.testing.assert_allclose(image, data["image"], rtol=1e-6, atol=1e-7)
     np.testing.assert_allclose(fimg, data["feature_image"], rtol=1e-5, atol=1e-6)
