@@ -1,10 +1,12 @@
-// Spherical-harmonic colours (degrees 0-3) and the fused SH backward + Adam step.
+// Spherical-harmonic colours (degrees 0-3) and the SH backward fused with the Adam step.
 //
 // eval_sh: one thread per gaussian, rgb = max(0.5 + sum_j b_j(dir) w_j, 0), culled -> 0
-// (sh.cu:62-83). The backward computes the 48 SH gradients of each gaussian into LDS, writes
-// grad_dirs, then the work-group steps Adam over its contiguous block of sh_dc / sh_rest with
-// coalesced loads, so SH gradients never reach HBM (sh.cu:104-154, docs/rasterizer.md:56-100).
-// The basis constants are the real SH of the 3DGS convention, sh.cu:9-15 / test_sh.py:27-47.
+// (sh.cu:62-83). The backward (sh.cu:104-154, utils/sh.py:26-109; the fusion is
+// docs/rasterizer.md:56-100) never materialises the 48 SH gradients of a gaussian: they are the
+// outer product b_j(dir) g_c of its basis and its masked colour gradient, so a work-group keeps only
+// those 19 numbers per gaussian and steps the parameters one thread per coefficient, forming each
+// gradient where Adam consumes it (eval_sh_backward_adam_kernel). The basis constants are the real
+// SH of the 3DGS convention, sh.cu:9-15 / test_sh.py:27-47.
 #include "hds_internal.h"
 #include "hds_rasterizer.h"
 
@@ -38,49 +40,6 @@ __device__ inline void sh_basis(float x, float y, float z, int k, float* b) {
 	b[13] = kShC[13] * x * (4 * zz - xx - yy);
 	b[14] = kShC[14] * z * (xx - yy);
 	b[15] = kShC[15] * x * (xx - 3 * yy);
-}
-
-// Gradient of each basis function with respect to the direction (sh.cu:34-55 semantics).
-__device__ inline void sh_basis_grad(float x, float y, float z, int k, float* bx, float* by, float* bz) {
-	const float xx = x * x, yy = y * y, zz = z * z;
-#pragma unroll
-	for (int j = 0; j < 16; j++) bx[j] = by[j] = bz[j] = 0.0f;
-	if (k <= 1) return;
-	by[1] = kShC[1];
-	bz[2] = kShC[2];
-	bx[3] = kShC[3];
-	if (k <= 4) return;
-	bx[4] = kShC[4] * y;
-	by[4] = kShC[4] * x;
-	by[5] = kShC[5] * z;
-	bz[5] = kShC[5] * y;
-	bx[6] = kShC[6] * (-2 * x);
-	by[6] = kShC[6] * (-2 * y);
-	bz[6] = kShC[6] * (4 * z);
-	bx[7] = kShC[7] * z;
-	bz[7] = kShC[7] * x;
-	bx[8] = kShC[8] * (2 * x);
-	by[8] = kShC[8] * (-2 * y);
-	if (k <= 9) return;
-	bx[9] = kShC[9] * (6 * x * y);
-	by[9] = kShC[9] * (3 * xx - 3 * yy);
-	bx[10] = kShC[10] * y * z;
-	by[10] = kShC[10] * x * z;
-	bz[10] = kShC[10] * x * y;
-	bx[11] = kShC[11] * (-2 * x * y);
-	by[11] = kShC[11] * (4 * zz - xx - 3 * yy);
-	bz[11] = kShC[11] * (8 * y * z);
-	bx[12] = kShC[12] * (-6 * x * z);
-	by[12] = kShC[12] * (-6 * y * z);
-	bz[12] = kShC[12] * (6 * zz - 3 * xx - 3 * yy);
-	bx[13] = kShC[13] * (4 * zz - 3 * xx - yy);
-	by[13] = kShC[13] * (-2 * x * y);
-	bz[13] = kShC[13] * (8 * x * z);
-	bx[14] = kShC[14] * (2 * x * z);
-	by[14] = kShC[14] * (-2 * y * z);
-	bz[14] = kShC[14] * (xx - yy);
-	bx[15] = kShC[15] * (3 * xx - 3 * yy);
-	by[15] = kShC[15] * (-6 * x * y);
 }
 
 __device__ inline float sh_weight(const float* dc, const float* rest, int j, int c) {
@@ -120,91 +79,185 @@ __global__ __launch_bounds__(kShEvalBlock) void eval_sh_kernel(int64_t n, int k,
 	}
 }
 
+// Direction gradient of the colour polynomial P(d) = sum_j t_j b_j(d), with t_j = sum_c w_jc g_c the
+// weight of basis function j in the loss: the partial derivatives of the degree-1..3 terms of the
+// basis above, collected per axis (degree 0 is constant).
+__device__ inline void sh_poly_grad(float x, float y, float z, int k, const float* t, float& gx, float& gy,
+									float& gz) {
+	gx = gy = gz = 0.0f;
+	if (k <= 1) return;
+	gx = t[3] * kShC[3];
+	gy = t[1] * kShC[1];
+	gz = t[2] * kShC[2];
+	if (k <= 4) return;
+	const float c4 = t[4] * kShC[4], c5 = t[5] * kShC[5], c6 = t[6] * kShC[6], c7 = t[7] * kShC[7],
+				c8 = t[8] * kShC[8];
+	gx += c4 * y - 2.0f * c6 * x + c7 * z + 2.0f * c8 * x;
+	gy += c4 * x + c5 * z - 2.0f * c6 * y - 2.0f * c8 * y;
+	gz += c5 * y + 4.0f * c6 * z + c7 * x;
+	if (k <= 9) return;
+	const float xx = x * x, yy = y * y, zz = z * z;
+	const float c9 = t[9] * kShC[9], c10 = t[10] * kShC[10], c11 = t[11] * kShC[11], c12 = t[12] * kShC[12],
+				c13 = t[13] * kShC[13], c14 = t[14] * kShC[14], c15 = t[15] * kShC[15];
+	gx += 6.0f * c9 * x * y + c10 * y * z - 2.0f * c11 * x * y - 6.0f * c12 * x * z + c13 * (4.0f * zz - 3.0f * xx - yy) +
+		  2.0f * c14 * x * z + 3.0f * c15 * (xx - yy);
+	gy += 3.0f * c9 * (xx - yy) + c10 * x * z + c11 * (4.0f * zz - xx - 3.0f * yy) - 6.0f * c12 * y * z -
+		  2.0f * c13 * x * y - 2.0f * c14 * y * z - 6.0f * c15 * x * y;
+	gz += c10 * x * y + 8.0f * c11 * y * z + c12 * (6.0f * zz - 3.0f * xx - 3.0f * yy) + 8.0f * c13 * x * z +
+		  c14 * (xx - yy);
+}
+
+// Adam as torch.optim.Adam defines it (exp_avg.lerp_(g, 1 - beta1), exp_avg_sq = beta2 v + (1 - beta2)
+// g^2, p -= lr / (1 - beta1^t) * m / (sqrt(v) / sqrt(1 - beta2^t) + eps)), with the 1 - beta terms
+// formed in double on the host as torch does.
+struct AdamStep {
+	float step_size, bias2_sqrt, beta2, one_minus_beta1, one_minus_beta2, eps;
+};
+
+__device__ inline AdamStep adam_step(float lr, float step, float beta1, float beta2, float omb1, float omb2, float eps) {
+	AdamStep a;
+	a.step_size = lr / (1.0f - powf(beta1, step));
+	a.bias2_sqrt = sqrtf(1.0f - powf(beta2, step));
+	a.beta2 = beta2;
+	a.one_minus_beta1 = omb1;
+	a.one_minus_beta2 = omb2;
+	a.eps = eps;
+	return a;
+}
+
+__device__ inline float adam_update(float p, float& m, float& v, float g, const AdamStep& a) {
+	m = m + a.one_minus_beta1 * (g - m);
+	v = a.beta2 * v + a.one_minus_beta2 * g * g;
+	return p - a.step_size * m / (sqrtf(v) / a.bias2_sqrt + a.eps);
+}
+
 struct AdamArgs {
 	float lr_dc, lr_rest, beta1, beta2, one_minus_beta1, one_minus_beta2, eps;
 };
 
-constexpr int kShAdamBlock = 256;
+constexpr int kShAdamBlock = 256;  // gaussians (and threads) per work-group
+constexpr int kWRow = 49;          // LDS words per gaussian: 48 weights, odd stride for conflict-free rows
+constexpr int kBRow = 17;          // basis values per gaussian (16, odd stride)
 
-// One Adam step over `len` contiguous parameters whose gradients sit in LDS.
-__device__ inline void adam_block(float* p, float* m, float* v, const float* g, int len, float step, float lr,
-								  const AdamArgs& a) {
-	const float step_size = lr / (1.0f - powf(a.beta1, step));
-	const float bc2_sqrt = sqrtf(1.0f - powf(a.beta2, step));
-	for (int t = threadIdx.x; t < len; t += blockDim.x) {
-		const float grad = g[t];
-		const float mt = m[t] + a.one_minus_beta1 * (grad - m[t]);
-		const float vt = a.beta2 * v[t] + a.one_minus_beta2 * grad * grad;
-		m[t] = mt;
-		v[t] = vt;
-		p[t] -= step_size * mt / (sqrtf(vt) / bc2_sqrt + a.eps);
-	}
-}
-
+// One work-group owns kShAdamBlock consecutive gaussians, i.e. one contiguous run of 3 * count sh_dc
+// and 45 * count sh_rest parameters and of their moments.
+//  1. The run's weights are read coalesced into LDS rows (row = gaussian: dc, then rest).
+//  2. Thread = gaussian: basis of its direction, colour per channel, the clamp mask (max(., 0) passes
+//     no gradient where it clipped), g_c = masked dL/drgb_c, the direction gradient from the colour
+//     polynomial, and (b_j, g_c) into LDS. Culled gaussians get b = g = 0.
+//  3. Thread = parameter: the whole run is stepped with coalesced 16-byte moment reads and writes,
+//     each coefficient's gradient formed on the fly as b_j g_c of its gaussian and channel (no
+//     gradient array is ever materialised) and its current value taken from the LDS copy. Culled
+//     gaussians and coefficients above the degree get a zero gradient and are still stepped, as an
+//     optimizer step over the whole tensors does.
 __global__ __launch_bounds__(kShAdamBlock) void eval_sh_backward_adam_kernel(
 	int64_t n, int k, const float* __restrict__ grad_rgb, float* __restrict__ sh_dc, float* __restrict__ sh_rest,
 	const float* __restrict__ dirs, const float* __restrict__ radii, float* __restrict__ m_dc,
 	float* __restrict__ v_dc, float* __restrict__ m_rest, float* __restrict__ v_rest,
-	const float* __restrict__ step_dc, const float* __restrict__ step_rest, AdamArgs a,
+	const float* __restrict__ step_dc, const float* __restrict__ step_rest, AdamArgs args,
 	float* __restrict__ grad_dirs) {
-	__shared__ float s_dc[kShAdamBlock * 3];
-	__shared__ float s_rest[kShAdamBlock * 45];
+	__shared__ float s_w[kShAdamBlock * kWRow];
+	__shared__ float s_b[kShAdamBlock * kBRow];
+	__shared__ float s_g[kShAdamBlock * 4];
 	const int64_t first = (int64_t)blockIdx.x * kShAdamBlock;
-	const int64_t i = first + threadIdx.x;
-	float* gdc = s_dc + threadIdx.x * 3;
-	float* grest = s_rest + threadIdx.x * 45;
-	if (k > 1) {
-		// The block's coefficient rows, read coalesced into the gradient rows; a thread only
-		// touches its own row, reading each weight before its gradient replaces it.
-		const int rows = (int)min((int64_t)kShAdamBlock, n - first);
-		const float* src = sh_rest + first * 45;
-		for (int e = threadIdx.x; e < rows * 45; e += kShAdamBlock) s_rest[e] = src[e];
-		__syncthreads();
-	}
-	if (i < n) {
-		float dd[3] = {0.0f, 0.0f, 0.0f};
+	const int count = (int)min((int64_t)kShAdamBlock, n - first);
+	const int tid = threadIdx.x;
+
+	const float* dc_run = sh_dc + first * 3;
+	const float* rest_run = sh_rest + first * 45;
+	for (int e = tid; e < count * 3; e += kShAdamBlock) s_w[(e / 3) * kWRow + e % 3] = dc_run[e];
+	for (int e = tid; e < count * 45; e += kShAdamBlock) s_w[(e / 45) * kWRow + 3 + e % 45] = rest_run[e];
+	__syncthreads();
+
+	if (tid < count) {
+		const int64_t i = first + tid;
+		const float* w = s_w + tid * kWRow;  // w[3 j + c]
+		float b[16];
+		float g[3] = {0.0f, 0.0f, 0.0f};
+		float gd[3] = {0.0f, 0.0f, 0.0f};
+#pragma unroll
+		for (int j = 0; j < 16; j++) b[j] = 0.0f;
 		if (radii[i] > 0.0f) {
-			float b[16], bx[16], by[16], bz[16];
 			const float x = dirs[i * 3], y = dirs[i * 3 + 1], z = dirs[i * 3 + 2];
 			sh_basis(x, y, z, k, b);
-			sh_basis_grad(x, y, z, k, bx, by, bz);
-			const float* dc = sh_dc + i * 3;
-			const float* rest = grest;
-			// The colour clamp passes no gradient where it clipped; recomputed, not stored.
-			float g[3];
+#pragma unroll
 			for (int c = 0; c < 3; c++) {
 				float value = 0.5f;
-				for (int j = 0; j < k; j++) value += b[j] * sh_weight(dc, rest, j, c);
+				for (int j = 0; j < k; j++) value += b[j] * w[3 * j + c];
 				g[c] = value > 0.0f ? grad_rgb[i * 3 + c] : 0.0f;
 			}
-			for (int j = 0; j < 16; j++) {
-				float t = 0.0f;
-				for (int c = 0; c < 3; c++) {
-					const float weight = j < k ? sh_weight(dc, rest, j, c) : 0.0f;
-					const float grad = j < k ? b[j] * g[c] : 0.0f;
-					if (j == 0)
-						gdc[c] = grad;
-					else
-						grest[(j - 1) * 3 + c] = grad;
-					if (j < k) t += weight * g[c];
-				}
-				if (j < k) {
-					dd[0] += t * bx[j];
-					dd[1] += t * by[j];
-					dd[2] += t * bz[j];
-				}
-			}
-		} else {
-			for (int c = 0; c < 3; c++) gdc[c] = 0.0f;
-			for (int j = 0; j < 45; j++) grest[j] = 0.0f;
+			float t[16];
+#pragma unroll
+			for (int j = 0; j < 16; j++) t[j] = j < k ? w[3 * j] * g[0] + w[3 * j + 1] * g[1] + w[3 * j + 2] * g[2] : 0.0f;
+			sh_poly_grad(x, y, z, k, t, gd[0], gd[1], gd[2]);
+#pragma unroll
+			for (int j = 0; j < 16; j++)
+				if (j >= k) b[j] = 0.0f;
 		}
-		for (int c = 0; c < 3; c++) grad_dirs[i * 3 + c] = dd[c];
+#pragma unroll
+		for (int c = 0; c < 3; c++) grad_dirs[i * 3 + c] = gd[c];
+#pragma unroll
+		for (int j = 0; j < 16; j++) s_b[tid * kBRow + j] = b[j];
+#pragma unroll
+		for (int c = 0; c < 3; c++) s_g[tid * 4 + c] = g[c];
 	}
 	__syncthreads();
-	const int count = (int)min((int64_t)kShAdamBlock, n - first);
-	adam_block(sh_dc + first * 3, m_dc + first * 3, v_dc + first * 3, s_dc, count * 3, *step_dc, a.lr_dc, a);
-	adam_block(sh_rest + first * 45, m_rest + first * 45, v_rest + first * 45, s_rest, count * 45, *step_rest,
-			   a.lr_rest, a);
+
+	const AdamStep a_dc = adam_step(args.lr_dc, *step_dc, args.beta1, args.beta2, args.one_minus_beta1,
+									args.one_minus_beta2, args.eps);
+	const AdamStep a_rest = adam_step(args.lr_rest, *step_rest, args.beta1, args.beta2, args.one_minus_beta1,
+									  args.one_minus_beta2, args.eps);
+	// sh_dc: coefficient j = 0 of gaussian e / 3, channel e % 3.
+	for (int e = tid; e < count * 3; e += kShAdamBlock) {
+		const int r = e / 3, c = e % 3;
+		const float grad = s_b[r * kBRow] * s_g[r * 4 + c];
+		float m = m_dc[first * 3 + e], v = v_dc[first * 3 + e];
+		sh_dc[first * 3 + e] = adam_update(s_w[r * kWRow + c], m, v, grad, a_dc);
+		m_dc[first * 3 + e] = m;
+		v_dc[first * 3 + e] = v;
+	}
+	// sh_rest: element e is coefficient 1 + (e % 45) / 3 of gaussian e / 45, channel e % 3; four
+	// consecutive elements per thread and step, the moments as 16-byte accesses when aligned.
+	float* pr = sh_rest + first * 45;
+	float* mr = m_rest + first * 45;
+	float* vr = v_rest + first * 45;
+	const int len = count * 45;
+	const bool vec = ((reinterpret_cast<uintptr_t>(pr) | reinterpret_cast<uintptr_t>(mr) |
+					   reinterpret_cast<uintptr_t>(vr)) & 15u) == 0;
+	for (int e0 = 4 * tid; e0 < len; e0 += 4 * kShAdamBlock) {
+		float m[4], v[4], p[4];
+		const int lanes = min(4, len - e0);
+		if (vec && lanes == 4) {
+			const float4 m4 = *reinterpret_cast<const float4*>(mr + e0);
+			const float4 v4 = *reinterpret_cast<const float4*>(vr + e0);
+			m[0] = m4.x; m[1] = m4.y; m[2] = m4.z; m[3] = m4.w;
+			v[0] = v4.x; v[1] = v4.y; v[2] = v4.z; v[3] = v4.w;
+		} else {
+			for (int u = 0; u < lanes; u++) {
+				m[u] = mr[e0 + u];
+				v[u] = vr[e0 + u];
+			}
+		}
+#pragma unroll
+		for (int u = 0; u < 4; u++) {
+			if (u < lanes) {
+				const int e = e0 + u, r = e / 45, q = e % 45;
+				const float grad = s_b[r * kBRow + 1 + q / 3] * s_g[r * 4 + q % 3];
+				p[u] = adam_update(s_w[r * kWRow + 3 + q], m[u], v[u], grad, a_rest);
+			}
+		}
+		if (vec && lanes == 4) {
+			*reinterpret_cast<float4*>(pr + e0) = make_float4(p[0], p[1], p[2], p[3]);
+			*reinterpret_cast<float4*>(mr + e0) = make_float4(m[0], m[1], m[2], m[3]);
+			*reinterpret_cast<float4*>(vr + e0) = make_float4(v[0], v[1], v[2], v[3]);
+		} else {
+			for (int u = 0; u < lanes; u++) {
+				pr[e0 + u] = p[u];
+				mr[e0 + u] = m[u];
+				vr[e0 + u] = v[u];
+			}
+		}
+	}
 }
 
 }  // namespace
