@@ -68,6 +68,10 @@ def parse_args():
                          "includes the loss, none otherwise")
     ap.add_argument("--bwd-slice", type=int, default=None,
                     help="channels per backward work-group (gaussian_splatting.rasterizer.FEATURE_SLICE_WIDTH)")
+    ap.add_argument("--sweep", default="auto",
+                    help="comma-separated channel counts of BASELINE config 3 timed after the headline on the same "
+                         "scene (fwd / bwd ms, backward roofline) and reported under 'channel_sweep'; 'auto' = "
+                         "32,64,256,512 for config 2, none otherwise; 'none' skips it")
     args = ap.parse_args()
     if (args.checkpoint is None) != (args.camera is None):
         ap.error("--checkpoint and --camera go together")
@@ -95,10 +99,14 @@ def checkpoint_workload(checkpoint: Path, camera: Path, channels: int | None):
 
 def algorithmic_bytes(n: int, n_vis: int, pairs: int, hw: int, c: int) -> dict[str, float]:
     """Minimal unique HBM bytes per stage (fp32), the roofline denominators: each input read once,
-    each output written once (gradient outputs counted once, not as zero-fill + read-modify-write)."""
+    each output written once (gradient outputs counted once, not as zero-fill + read-modify-write).
+    Binning: bin_count = the tile counts and their scan (12 B per gaussian); bin_emit = writing the
+    pairs (12 B), one read + write of keys and values for a one-pass sort (24 B) and the range build's
+    read (8 B), per pair."""
     return {
         "project_forward": 44 * n + 28 * n,
-        "binning": 12 * n + 48 * pairs,
+        "bin_count": 12 * n,
+        "bin_emit": 44 * pairs,
         "render": 4 * pairs + 36 * n_vis + 4 * c * n_vis + 20 * hw + 4 * c * hw,
         "render_backward": 20 * hw + 4 * pairs + 36 * n_vis + 4 * c * n_vis + 4 * c * hw + 4 * c * n + 36 * n,
         "project_backward": 60 * n + 40 * n,
@@ -162,10 +170,15 @@ def main() -> int:
     target = grad_image if loss_mode == "l1-ssim" else None
     state = {}
 
-    def forward():
+    def forward(retain=False):
         means2D, depths, radii, conics = project_gaussians(
             leaves["means"], leaves["scales"], F.normalize(leaves["quats"], dim=-1), leaves["opacities"][:, None],
             w2c, cam["fx"], cam["fy"], cam["cx"], cam["cy"], W, H)
+        if retain:
+            # The rasterizer's own gradients (the agreement gate compares each stage on its inputs).
+            means2D.retain_grad()
+            conics.retain_grad()
+            state["means2D"], state["conics"] = means2D, conics
         state["out"] = rasterize(means2D, depths, radii, conics, leaves["colors"], leaves["opacities"][:, None],
                                  W, H, features=leaves.get("features"))
 
@@ -205,11 +218,15 @@ def main() -> int:
     # Agreement gate and CPU baseline: the oracle runs the same frame; one GPU step must agree with it.
     cpu, agreement = None, None
     if not args.no_cpu_baseline and not args.rgb_only and not args.frozen_features:
-        step()
+        reset()
+        forward(retain=True)
+        backward()
         torch.cuda.synchronize()
         gpu_out = {"image": state["out"][0], "feature_image": state["out"][1],
+                   "means2D": state["means2D"].grad, "conics": state["conics"].grad,
                    **{name: leaf.grad for name, leaf in leaves.items()}}
         gpu_out = {k: v.detach().cpu().numpy() for k, v in gpu_out.items()}
+        state.pop("means2D"), state.pop("conics")
         cpu, want = cpu_baseline(wl, colors, grad_image, grad_features, loss_target=target)
         agreement = agree(gpu_out, want)
         print(f"[bench] agreement with the oracle: {agreement}", file=sys.stderr, flush=True)
@@ -261,50 +278,38 @@ def main() -> int:
 
     split = {}
     if not args.no_split:
-        # The harness method (bench/harness.py:130-177): events around forward alone, and around
-        # backward alone with an untimed forward before each sample, a pause of 1.5x the sample after
-        # each, median / min / max, GPU clock and power read before and after.
-        def time_ms(fn, before=None):
-            time.sleep(0.5)
-            start_state = gpu_state()
-            times = []
-            for _ in range(min(args.steps, 20)):
-                if before:
-                    before()
-                torch.cuda.synchronize()
-                s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                s.record()
-                fn()
-                e.record()
-                e.synchronize()
-                times.append(s.elapsed_time(e))
-                time.sleep(max(0.01, 1.5 * times[-1] / 1000))
-            return times, start_state, gpu_state()
-
-        fwd, fwd_start, _ = time_ms(lambda: (reset(), forward()))
-        bwd, _, bwd_end = time_ms(backward, before=lambda: (reset(), forward()))
-        split = {"fwd_ms_median": round(statistics.median(fwd), 4), "bwd_ms_median": round(statistics.median(bwd), 4),
-                 "fwd_ms_min_max": [round(min(fwd), 4), round(max(fwd), 4)],
-                 "bwd_ms_min_max": [round(min(bwd), 4), round(max(bwd), 4)],
-                 "gpu_state_split_start": fwd_start, "gpu_state_split_end": bwd_end}
+        split = harness_split(forward, backward, reset, min(args.steps, 20))
 
     # Roofline of the blend backward: one hds_render_backward call runs its two kernels (back-to-front
     # geometry/colour gradients, front-to-back feature gradients) side by side on two streams. The
     # duration is the pair's span, first start to last end, from the HIP events the library records
     # on each kernel's own stream over the timed region (rocprofv3's kernel trace gives the same
     # span); the per-kernel means, each longer than when run alone, are reported beside it.
-    bwd_names = [k for k in ("backward_geometry_kernel", "backward_features_kernel") if k in kernels]
-    bwd_ms = concurrent_span_ms(kprof.timeline, *bwd_names) if len(bwd_names) == 2 else kernels[bwd_names[0]]["mean_ms"]
+    bwd_names, bwd_ms = backward_span(kernels, kprof.timeline)
     achieved = alg["render_backward"] / (bwd_ms * 1e-3) / 1e9
-    roofline = {"kernel": " + ".join(bwd_names) + " (side by side, one hds_render_backward call)",
+    roofline = {"kernel": " + ".join(bwd_names) + (" (side by side, one hds_render_backward call)"
+                                                   if len(bwd_names) > 1 else ""),
                 "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_per_step(bwd_names),
+                "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": traffic_per_step(bwd_names, wl.name + ("-rgb-only" if args.rgb_only else "")),
                 "algorithmic_bytes": int(alg["render_backward"]), "ms_per_call": round(bwd_ms, 4),
                 "kernel_mean_ms": {k: round(kernels[k]["mean_ms"], 4) for k in bwd_names}}
     kernel_report = {k: {"launches_per_step": round(v["launches"] / args.steps, 2), "mean_ms": round(v["mean_ms"], 4)}
                      for k, v in sorted(kernels.items(), key=lambda kv: -kv[1]["total_ms"])}
     total_alg = sum(alg.values())
     step_frac = total_alg / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS
+
+    sweep_channels = ([32, 64, 256, 512] if args.config == 2 and args.checkpoint is None and not args.rgb_only
+                      else []) if args.sweep == "auto" else ([] if args.sweep == "none"
+                                                             else [int(c) for c in args.sweep.split(",")])
+    channel_sweep = None
+    if sweep_channels:
+        # Free the headline's feature buffers before the wider ones.
+        leaves.pop("features", None)
+        state.clear()
+        del grad_features
+        torch.cuda.empty_cache()
+        channel_sweep = measure_sweep(wl, leaves, w2c, sweep_channels, n_vis, pairs, args)
 
     line = {
         "metric": METRIC, "value": round(ms_per_step, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps,
@@ -318,7 +323,7 @@ def main() -> int:
         "step_ms_median": round(statistics.median(step_ms), 4), **split,
         "step_hbm_frac": round(step_frac, 4), "step_algorithmic_MB": round(total_alg / 1e6, 1),
         "roofline": roofline, "stages": stage_report, "kernels": kernel_report, "cpu_baseline": cpu,
-        "agreement": agreement, "environment": environment(),
+        "agreement": agreement, "channel_sweep": channel_sweep, "environment": environment(),
     }
     print(json.dumps(line), flush=True)
     if args.calibrate_copy_mib > 0:
@@ -330,6 +335,110 @@ def main() -> int:
         torch.cuda.synchronize()
         print(f"[bench] calibration copy: {n_floats * 4} bytes read and written", file=sys.stderr, flush=True)
     return 0
+
+
+def backward_span(kernels: dict, timeline) -> tuple[list[str], float]:
+    """The blend backward's kernels in the timed region and the mean duration of one
+    hds_render_backward call: with two kernels side by side on two streams, their span (first start
+    to last end); with one, its mean."""
+    names = [k for k in ("backward_geometry_kernel", "backward_features_kernel", "backward_fused_kernel")
+             if k in kernels]
+    if len(names) == 2:
+        return names, concurrent_span_ms(timeline, *names)
+    return names, kernels[names[0]]["mean_ms"]
+
+
+def harness_split(fn_fwd, fn_bwd, reset, samples: int) -> dict:
+    """bench/harness.py:130-177's method: events around the forward alone, and around the backward
+    alone with an untimed forward before each sample, a pause of 1.5x the sample after each, median /
+    min / max, GPU clock and power before and after."""
+    import torch
+
+    def time_ms(fn, before=None):
+        time.sleep(0.5)
+        start_state = gpu_state()
+        times = []
+        for _ in range(samples):
+            if before:
+                before()
+            torch.cuda.synchronize()
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            fn()
+            e.record()
+            e.synchronize()
+            times.append(s.elapsed_time(e))
+            time.sleep(max(0.01, 1.5 * times[-1] / 1000))
+        return times, start_state, gpu_state()
+
+    fwd, fwd_start, _ = time_ms(lambda: (reset(), fn_fwd()))
+    bwd, _, bwd_end = time_ms(fn_bwd, before=lambda: (reset(), fn_fwd()))
+    return {"fwd_ms_median": round(statistics.median(fwd), 4), "bwd_ms_median": round(statistics.median(bwd), 4),
+            "fwd_ms_min_max": [round(min(fwd), 4), round(max(fwd), 4)],
+            "bwd_ms_min_max": [round(min(bwd), 4), round(max(bwd), 4)],
+            "gpu_state_split_start": fwd_start, "gpu_state_split_end": bwd_end}
+
+
+def measure_sweep(wl, leaves: dict, w2c, channels_list, n_vis: int, pairs: int, args) -> list[dict]:
+    """the headline scene's gaussians with C feature channels ~ N(0, 1) (seed 1, as
+    tests/scenes.py draws them) and dL/dimage, dL/dF ~ U[0, 1] (seed 2), for each C: the fwd+bwd step
+    (a few warm-up steps, then HIP events around each timed step), the harness fwd / bwd split and the
+    blend backward's roofline over the span of its kernels."""
+    import torch
+    import torch.nn.functional as F
+
+    from gaussian_splatting.rasterizer import project_gaussians, rasterize
+    from gaussian_splatting.rasterizer._native import KernelProfile
+    from tests.scenes import upstream
+
+    dev = leaves["means"].device
+    cam = wl.cam
+    W, H, N = wl.width, wl.height, wl.n
+    out = []
+    for c in channels_list:
+        print(f"[bench] channel sweep: C={c}", file=sys.stderr, flush=True)
+        feats = torch.randn(N, c, generator=torch.Generator().manual_seed(1)).to(dev).requires_grad_(True)
+        grad_image, grad_features = upstream(2, H, W, c, device=dev)
+        holder = {}
+        sweep_leaves = [leaves[k] for k in ("means", "scales", "quats", "opacities", "colors")] + [feats]
+
+        def forward():
+            m2, d, r, con = project_gaussians(leaves["means"], leaves["scales"], F.normalize(leaves["quats"], dim=-1),
+                                              leaves["opacities"][:, None], w2c, cam["fx"], cam["fy"], cam["cx"],
+                                              cam["cy"], W, H)
+            holder["out"] = rasterize(m2, d, r, con, leaves["colors"], leaves["opacities"][:, None], W, H,
+                                      features=feats)
+
+        def backward():
+            torch.autograd.backward(holder["out"], [grad_image, grad_features])
+
+        def reset():
+            for leaf in sweep_leaves:
+                leaf.grad = None
+
+        for _ in range(3):
+            reset(), forward(), backward()
+        steps = min(args.steps, 20)
+        events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+        torch.cuda.synchronize()
+        with KernelProfile() as kprof:
+            for start, end in events:
+                start.record()
+                reset(), forward(), backward()
+                end.record()
+            torch.cuda.synchronize()
+        step_ms = [s.elapsed_time(e) for s, e in events]
+        names, bwd_ms = backward_span(kprof.summary(), kprof.timeline)
+        alg = algorithmic_bytes(N, n_vis, pairs, W * H, c)["render_backward"]
+        gbs = alg / (bwd_ms * 1e-3) / 1e9
+        split = harness_split(forward, backward, reset, min(args.steps, 10))
+        out.append({"channels": c, "step_ms_median": round(statistics.median(step_ms), 4),
+                    "fwd_ms_median": split["fwd_ms_median"], "bwd_ms_median": split["bwd_ms_median"],
+                    "render_backward_ms": round(bwd_ms, 4), "render_backward_algorithmic_MB": round(alg / 1e6, 1),
+                    "render_backward_GBs": round(gbs, 1), "render_backward_hbm_frac": round(gbs / HBM_PEAK_GBS, 4)})
+        del feats, grad_image, grad_features, holder
+        torch.cuda.empty_cache()
+    return out
 
 
 def concurrent_span_ms(timeline, first: str, second: str) -> float:
@@ -347,14 +456,31 @@ def concurrent_span_ms(timeline, first: str, second: str) -> float:
 TRAFFIC_FILE = ROOT / "profiles" / "render_backward_headline_c128_pmc.md"
 
 
-def traffic_per_step(kernel_names) -> int | None:
+def source_digest() -> str:
+    """sha256 (first 16 hex digits) of the HIP sources and the public header."""
+    digest = hashlib.sha256()
+    for path in sorted((ROOT / "high-dimensional-splatting_amd" / "csrc").glob("*")) + [ROOT / "include" / "hds_rasterizer.h"]:
+        digest.update(path.read_bytes())
+    return digest.hexdigest()[:16]
+
+
+def traffic_per_step(kernel_names, workload: str) -> int | None:
     """HBM bytes the named kernels move per step, from the committed rocprofv3 --pmc summary
-    (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by a copy kernel of known size); None if that
-    summary does not cover every one of them."""
+    (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by a copy kernel of known size); None unless that
+    summary was taken on this workload with this build (its "workload:" and "source:" header lines)
+    and covers every one of the kernels."""
     if not TRAFFIC_FILE.exists():
         return None
+    text = TRAFFIC_FILE.read_text()
+    header = {}
+    for line in text.splitlines():
+        for key in ("workload:", "source:"):
+            if line.strip().lower().startswith(key):
+                header[key] = line.split(":", 1)[1].strip().strip("`")
+    if header.get("workload:") != workload or header.get("source:") != source_digest():
+        return None
     per_kernel = {}
-    for line in TRAFFIC_FILE.read_text().splitlines():
+    for line in text.splitlines():
         # rows of the form "| kernel | ... | traffic_bytes |" with the bytes in the last column
         cells = [c.strip() for c in line.strip().strip("|").split("|")]
         if len(cells) >= 2 and cells[0] in kernel_names and cells[-1].isdigit():
@@ -386,8 +512,8 @@ def cpu_baseline(wl, colors, grad_image, grad_features, loss_target=None):
     m2, d, r, c = oracle.project_forward(means, scales, quats, opac, w2c, cam["fx"], cam["fy"], cam["cx"],
                                          cam["cy"], cam["width"], cam["height"])
     _, values, ranges = oracle.bin_gaussians(m2, d, r, c, opac, cam["width"], cam["height"])
-    image, T, nc, fimg = oracle.render_forward(cam["width"], cam["height"], ranges, values, m2, c, opac, cols,
-                                               np.zeros(3, np.float32), feats)
+    image, T, nc, fimg, near = oracle.render_forward(cam["width"], cam["height"], ranges, values, m2, c, opac, cols,
+                                                     np.zeros(3, np.float32), feats, near_cut=True)
     t1 = time.perf_counter()
     if loss_target is not None:
         # d/dimage of 0.8 mean|image - target| + 0.2 (1 - mean SSIM): sign / numel, and the SSIM
@@ -401,39 +527,70 @@ def cpu_baseline(wl, colors, grad_image, grad_features, loss_target=None):
     dmeans, dscales, dq = oracle.project_backward(dm, dc, means, scales, quats, w2c, cam["fx"], cam["fy"],
                                                   cam["cx"], cam["cy"], cam["width"], cam["height"])
     t2 = time.perf_counter()
-    # The quats leaf goes through F.normalize before the projection: chain its gradient on the CPU.
-    q = wl.quats.detach().clone().requires_grad_(True)
-    torch.nn.functional.normalize(q, dim=-1).backward(torch.from_numpy(np.ascontiguousarray(dq)))
-    want = {"image": image, "feature_image": fimg, "means": dmeans, "scales": dscales, "quats": q.grad.numpy(),
-            "opacities": np.asarray(dop).reshape(-1), "colors": dcol, "features": df}
+
+    def normalize_backward(d_unit):
+        # The quats leaf goes through F.normalize before the projection: its gradient, on the CPU.
+        q = wl.quats.detach().clone().requires_grad_(True)
+        torch.nn.functional.normalize(q, dim=-1).backward(torch.from_numpy(np.ascontiguousarray(d_unit)))
+        return q.grad.numpy()
+
+    def projection_stage(grad_means2D, grad_conics):
+        # The oracle's projection backward (and the normalize chain) on given upstream gradients.
+        pm, ps, pq = oracle.project_backward(grad_means2D, grad_conics, means, scales, quats, w2c, cam["fx"],
+                                             cam["fy"], cam["cx"], cam["cy"], cam["width"], cam["height"])
+        return {"means": pm, "scales": ps, "quats": normalize_backward(pq)}
+
+    want = {"image": image, "feature_image": fimg, "near_cut": near, "means2D": dm, "conics": dc,
+            "opacities": np.asarray(dop).reshape(-1), "colors": dcol, "features": df,
+            "chain": {"means": dmeans, "scales": dscales, "quats": normalize_backward(dq)},
+            "projection_stage": projection_stage}
     return ({"value": round((t2 - t0) * 1e3, 1), "unit": "ms", "cores": oracle.num_threads(), "kind": "port",
              "fwd_ms": round((t1 - t0) * 1e3, 1), "bwd_ms": round((t2 - t1) * 1e3, 1),
              "sample": f"one full fwd+bwd frame of {wl.name} (same inputs) on the C oracle, OpenMP",
              "cpu": _cpu_model()}, want)
 
 
-# Largest gradient error allowed by the gate, relative to max|want|. The parity tests' 2e-3 holds on
-# their scenes; over the 1.18M gaussians of a full frame a gaussian whose alpha sits exactly on the
-# 1/255 or 0.99 cut can blend on one side and not the other (the reference's assert_grads_close says
-# the same), and its few gradients then differ by up to a few 1e-3.
-GATE_MAX_REL = 1e-2
+# Largest gradient error allowed by the gate, relative to max|want|: the parity tests' bar, from the
+# reference's assert_grads_close (tests/test_render.py:45-58 there).
+GATE_MAX_REL = 2e-3
 
 
 def agree(got: dict, want: dict) -> dict:
-    """The parity tests' bars on this frame: images by max / 99th percentile error, gradients by the
-    share of values outside rtol 1e-3 (< 0.1%) and the largest error relative to max|want|
-    (GATE_MAX_REL)."""
+    """The parity tests' bars on this frame, stage by stage, each stage on identical inputs:
+      - images by max / 99th percentile error on the pixels clear of the oracle's near_cut mask (an
+        alpha or transmittance within rounding distance of its cut, where the GPU's exp2 and libm's
+        expf may decide differently), which must be under 0.1% of the frame;
+      - the rasterizer's gradients (means2D, conics, colors, opacities, features) against the oracle's
+        rasterizer on the same projected inputs;
+      - the projection backward (means, scales and the quats leaf through normalize) against the
+        oracle's projection backward fed the GPU's own means2D / conics gradients;
+    each gradient with < 0.1% of values outside rtol 1e-3 and the largest error within GATE_MAX_REL
+    of max|want|. The end-to-end leaf errors (the oracle's projection backward on the oracle's own
+    rasterizer gradients) are reported under "chain" without a bar: composing the two stages
+    amplifies their ~1e-6 relative differences by the conditioning of the conic -> quaternion map of
+    elongated gaussians."""
     from tests.tolerances import grad_error, image_error
 
     report, passed = {}, True
+    near = want["near_cut"]
+    report["near_cut_pixels"] = int(near.sum())
+    passed &= near.mean() < 1e-3
     for name, (max_error, max_p99) in (("image", (2e-3, 1e-4)), ("feature_image", (1e-3, 5e-4))):
-        worst, p99 = image_error(got[name], want[name])
+        worst, p99 = image_error(got[name][~near], want[name][~near])
         report[name] = {"max": worst, "p99": p99}
         passed &= worst < max_error and p99 < max_p99
-    for name in ("means", "scales", "quats", "opacities", "colors", "features"):
+    for name in ("means2D", "conics", "colors", "opacities", "features"):
         outside, rel = grad_error(got[name].reshape(want[name].shape), want[name])
         report[name] = {"outside": outside, "max_rel": rel}
         passed &= outside < 1e-3 and rel <= GATE_MAX_REL
+    stage = want["projection_stage"](got["means2D"], got["conics"])
+    report["chain"] = {}
+    for name in ("means", "scales", "quats"):
+        outside, rel = grad_error(got[name].reshape(stage[name].shape), stage[name])
+        report[name] = {"outside": outside, "max_rel": rel}
+        passed &= outside < 1e-3 and rel <= GATE_MAX_REL
+        outside, rel = grad_error(got[name].reshape(want["chain"][name].shape), want["chain"][name])
+        report["chain"][name] = {"outside": outside, "max_rel": rel}
     report["passed"] = bool(passed)
     return report
 
@@ -470,9 +627,6 @@ def environment() -> dict:
     record (tests/test_golden.py:34-35)."""
     import torch
 
-    digest = hashlib.sha256()
-    for path in sorted((ROOT / "high-dimensional-splatting_amd" / "csrc").glob("*")) + [ROOT / "include" / "hds_rasterizer.h"]:
-        digest.update(path.read_bytes())
     name = torch.cuda.get_device_name(0)
     try:
         if _profiled():
@@ -485,7 +639,7 @@ def environment() -> dict:
         name = data["asic"]["market_name"]
     except Exception:  # noqa: BLE001 - torch's device name stands in
         pass
-    return {"gpu": name, "torch": torch.__version__, "hip": torch.version.hip, "source": digest.hexdigest()[:16],
+    return {"gpu": name, "torch": torch.__version__, "hip": torch.version.hip, "source": source_digest(),
             **gpu_state()}
 
 
