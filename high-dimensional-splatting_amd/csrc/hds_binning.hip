@@ -20,6 +20,8 @@
 // digit histograms every pass needs up front come from the kernel that produces the keys
 // (prepare for depths, emit for tile ids). The whole binning is 11 launches.
 #include <atomic>
+#include <mutex>
+#include <vector>
 
 #include "hds_internal.h"
 #include "hds_rasterizer.h"
@@ -892,4 +894,75 @@ extern "C" int hds_bin_emit_capped(int64_t n, int64_t capacity, int width, int h
 								   int32_t* tile_ranges, hds_stream_t stream) {
 	return bin_emit_launch(n, capacity, false, width, height, workspace, pairs_workspace, pairs_workspace_bytes,
 						   values_sorted, tile_ranges, (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Binning with the library's own scratch, for callers that cannot allocate device memory.
+// ---------------------------------------------------------------------------------------------
+
+namespace {
+
+// Both workspaces of one binning (the per-gaussian one, then the per-pair one, each 256-byte
+// aligned) live in this array. Every GPU the library runs on holds its own copy until the process
+// ends. On the host the name is only a stand-in for the device address: host code uses the
+// per-device address hipGetSymbolAddress returns (static_scratch_ptr), never the name.
+constexpr size_t kStaticScratchBytes = size_t(HDS_BIN_STATIC_SCRATCH_MIB) << 20;
+__device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+// The device address of `scratch` on the current device, looked up once per device.
+int static_scratch_ptr(void** out) {
+	static std::mutex mutex;
+	static std::vector<void*> ptrs;
+	int device = 0;
+	HDS_HIP(hipGetDevice(&device));
+	std::lock_guard<std::mutex> lock(mutex);
+	if ((int)ptrs.size() <= device) ptrs.resize(device + 1, nullptr);
+	if (!ptrs[device]) {
+		void* ptr = nullptr;
+		HDS_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+		HDS_REQUIRE(ptr != nullptr, "bin_static: no device address for the static scratch");
+		ptrs[device] = ptr;
+	}
+	*out = ptrs[device];
+	return HDS_OK;
+}
+
+}  // namespace
+
+extern "C" int hds_bin_static(int64_t n, const float* means2D, const float* depths, const float* radii,
+							  const float* conics, const float* colors, const float* opacities, int width, int height,
+							  float* conic4, float* color_opacity4, int64_t capacity, int32_t* values_sorted,
+							  int32_t* tile_ranges, void* status, hds_stream_t stream) {
+	HDS_REQUIRE(n >= 0 && capacity >= 0, "bin_static: negative gaussian count or capacity");
+	HDS_REQUIRE(status && tile_ranges, "bin_static: null pointer argument");
+	const size_t gaussian_bytes = gaussian_space(n).bytes;
+	const size_t pair_bytes = pair_space(capacity).bytes;
+	HDS_REQUIRE(gaussian_bytes + pair_bytes <= kStaticScratchBytes,
+				"bin_static: %lld gaussians and %lld pairs need %zu bytes of scratch, more than its %d MiB",
+				(long long)n, (long long)capacity, gaussian_bytes + pair_bytes, HDS_BIN_STATIC_SCRATCH_MIB);
+	void* ptr = nullptr;
+	int st = static_scratch_ptr(&ptr);
+	if (st != HDS_OK) return st;
+	hipStream_t s = (hipStream_t)stream;
+	void* ws = ptr;
+	void* pws = static_cast<char*>(ptr) + align256(gaussian_bytes);
+	bool launched = false;
+	st = bin_count_launch(n, means2D, depths, radii, conics, colors, opacities, width, height, conic4, color_opacity4,
+						  ws, gaussian_bytes, s, &launched);
+	if (st != HDS_OK) return st;
+	if (!launched) {
+		// No gaussians: empty tile ranges and zero status words, from a zeroed control block.
+		const GaussianSpace g = gaussian_space(0);
+		zero_kernel<<<1, kThreads, 0, s>>>(at<uint32_t>(ws, g.ctrl), sizeof(CountWords) / 4, nullptr, 0);
+		HDS_LAUNCH_CHECK("zero_static_status", s);
+		st = bin_emit_launch(0, 0, false, width, height, ws, pws, pair_bytes, values_sorted, tile_ranges, s);
+		if (st != HDS_OK) return st;
+		HDS_HIP(hipMemcpyAsync(status, count_words(ws, 0), sizeof(CountWords), hipMemcpyDefault, s));
+		return HDS_OK;
+	}
+	HDS_REQUIRE(capacity == 0 || values_sorted, "bin_static: null values_sorted");
+	st = bin_emit_launch(n, capacity, false, width, height, ws, pws, pair_bytes, values_sorted, tile_ranges, s);
+	if (st != HDS_OK) return st;
+	HDS_HIP(hipMemcpyAsync(status, count_words(ws, n), sizeof(CountWords), hipMemcpyDefault, s));
+	return HDS_OK;
 }

@@ -21,7 +21,8 @@
  *   - Returns HDS_OK (0) or an error status; hds_last_error() then holds a message for the
  *     calling thread. Invalid arguments are rejected before anything is enqueued.
  *   - The library never allocates device memory: scratch comes in as caller-owned workspaces
- *     whose sizes the *_workspace_bytes queries give.
+ *     whose sizes the *_workspace_bytes queries give, except for hds_bin_static, whose workspaces
+ *     are a static device array of the library (for callers that cannot allocate at all).
  *   - Gradient outputs of the backward calls are zeroed by the library before accumulation.
  */
 #ifndef HDS_RASTERIZER_H
@@ -150,6 +151,26 @@ HDS_API int hds_bin_status(int64_t n, const void* workspace, void* status_host, 
  * launches made after the call, on every thread. */
 #define HDS_LOOKBACK_LIMIT_DEFAULT 4194304u
 HDS_API int hds_set_lookback_limit(uint32_t polls);
+
+/* No counterpart in the reference. For callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc): hds_bin_count_async
+ * followed by hds_bin_emit_capped in one call, with both workspaces in a static device array of
+ * HDS_BIN_STATIC_SCRATCH_MIB MiB inside the library (one per GPU, held until the process ends)
+ * instead of caller-supplied ones; no allocation of any kind, and no host wait. The caller passes
+ * the inputs and outputs of those two calls: conic4 / color_opacity4 [N,4], values_sorted sized for
+ * `capacity` pairs, tile_ranges [T,2], and `status`, 16 bytes of pinned host or device memory
+ * that receive uint64 P, uint32 depth-sort / scan flag, uint32 tile-sort flag once the stream has
+ * passed this call. As with hds_bin_emit_capped, the binning is complete when P <= capacity and
+ * both flags are zero; otherwise call again with a larger capacity. Rejects (status 1) a gaussian
+ * count and capacity whose workspaces exceed the scratch: hds_bin_workspace_bytes(n) +
+ * hds_pairs_workspace_bytes(capacity) must fit, which holds for 1.5M gaussians with 4M pairs.
+ * Every call on a GPU shares that GPU's scratch: calls that overlap on one GPU (other streams,
+ * other host threads) race and must be serialised by the caller. */
+#define HDS_BIN_STATIC_SCRATCH_MIB 112
+HDS_API int hds_bin_static(int64_t n, const float* means2D, const float* depths, const float* radii,
+					   const float* conics, const float* colors, const float* opacities, int width,
+					   int height, float* conic4, float* color_opacity4, int64_t capacity,
+					   int32_t* values_sorted, int32_t* tile_ranges, void* status, hds_stream_t stream);
 
 /* ---- blend forward: replaces render_gaussians (forward.cu:406-434) and rasterize_features
  *      (features.cu:299-346) with one tile walk ------------------------------------------------ */

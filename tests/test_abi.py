@@ -152,3 +152,11 @@ def test_sh_backward_requires_the_named_adam():
 
     with pytest.raises(RuntimeError, match="needs the Adam"):
         EvalSH.backward(Ctx(), torch.zeros(1, 3))
+
+
+def test_static_binning_scratch_holds_the_documented_scene(lib):
+    """hds_bin_static's scratch (HDS_BIN_STATIC_SCRATCH_MIB) fits the workspaces of 1.5M gaussians
+    with 4M pairs, as its declaration states, and the headline scene with 25% pair headroom."""
+    mib = int(re.search(r"#define HDS_BIN_STATIC_SCRATCH_MIB (\d+)", HEADER.read_text()).group(1))
+    for n, pairs in ((1_500_000, 4_000_000), (1_180_000, int(1.25 * 1_921_191))):
+        assert lib.hds_bin_workspace_bytes(n, 979, 546) + lib.hds_pairs_workspace_bytes(pairs, 979, 546) <= mib << 20
