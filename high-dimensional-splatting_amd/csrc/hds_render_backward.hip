@@ -343,8 +343,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void b
 					for (int kk = 0; kk < kKc; kk++) {
 						// Logical chunks 8kk + 2(lane / 16) and the next one of the (swizzled) row.
 						const int lc = 8 * kk + 2 * (lane >> 4);
-						const float4 f0 = *reinterpret_cast<const float4*>(frow + 4 * hds_stage_chunk<true>(lc, frow_idx));
-						const float4 f1 = *reinterpret_cast<const float4*>(frow + 4 * hds_stage_chunk<true>(lc + 1, frow_idx));
+						const float4 f0 = *reinterpret_cast<const float4*>(frow + 4 * hds_stage_chunk<true, S / 4>(lc, frow_idx));
+						const float4 f1 = *reinterpret_cast<const float4*>(frow + 4 * hds_stage_chunk<true, S / 4>(lc + 1, frow_idx));
 						const float v[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
 						hds_bf16x8 f_hi, f_lo;
 						hds_split8(v, f_hi, f_lo);

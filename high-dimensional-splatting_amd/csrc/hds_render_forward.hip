@@ -2,9 +2,9 @@
 //
 // Work-group = one 16x16 tile (and one slice of S <= 128 channels); wave w owns the 8x8 block
 // ((w & 1) * 8, (w >> 1) * 8) and lane l the pixel (l & 7, l >> 3) of it. Gaussians of the tile's
-// sorted list are staged 64 at a time in LDS (geometry, culling box and the slice's features as
-// split-bf16 words); each wave ballots which of the 64 box-hit its block and walks only those, in
-// order, updating T, RGB and n_contrib per lane exactly as render_gaussians does
+// sorted list are staged 64 at a time in LDS (geometry, culling box and the slice's feature rows as
+// raw fp32, split into bf16 operands when read); each wave ballots which of the 64 box-hit its block
+// and walks only those, in order, updating T, RGB and n_contrib per lane exactly as render_gaussians does
 // (forward.cu:181-225): alpha = min(0.99, op * exp(-m/2)), skip below 1/255, stop before T would
 // drop below 1e-4, n_contrib = 1-based list index of the last blended gaussian.
 //
@@ -17,8 +17,10 @@
 // weights never touch LDS. The 16-hit groups depend on geometry only and the batch size is fixed,
 // so each output channel sees the same operation sequence whatever C or the slicing is: channels
 // are bitwise independent and RGB is bitwise equal with or without features (the properties the
-// reference's tests/test_properties.py pins). The accumulators (S registers per lane) stay in
-// AGPRs and everything else fits in 128 VGPRs, so the 128-channel slice runs two waves per SIMD.
+// reference's tests/test_properties.py pins). The accumulators take S registers per lane (ordinary
+// VGPRs: the compiler assigns no AGPRs here); with the walk's registers the 128-channel slice needs
+// about 240 and runs two waves per SIMD, the 64-channel slice three, the 32-channel slice three with
+// RGB (four would cap it at 128 registers, which spills) and four without.
 #include <cstdlib>
 
 #include "hds_internal.h"
@@ -103,7 +105,7 @@ struct Pixel {
 // LDS DMA while b is walked, and the gids of b+2 are read; one barrier, after each wave has waited
 // for its copies, hands the next batch over.
 template <int S, bool RGB>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S >= 128 ? 2 : S == 64 ? 3 : 4))) void render_forward_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S >= 128 ? 2 : (S == 64 || RGB) ? 3 : 4))) void render_forward_kernel(
 	const RenderArgs a) {
 	constexpr int kNcb = S > 0 ? S / 32 : 1;
 	constexpr int kRows = S > 0 ? (kBatch + 1) * S : 1;

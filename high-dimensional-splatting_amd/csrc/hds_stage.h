@@ -20,12 +20,14 @@ typedef __attribute__((address_space(3))) void hds_lds_void;
  * makes every wave's staged rows visible to the whole work-group. */
 __device__ static inline void hds_wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-/* Physical 16-byte chunk of logical chunk c in staged row r. With kSwizzle the chunks of a row are
- * XOR-permuted by the row's low three bits, so 8 lanes reading the same logical chunk of 8
- * consecutive rows with ds_read_b128 hit 8 different bank groups. */
-template <bool kSwizzle>
+/* Physical 16-byte chunk of logical chunk c in staged row r of kChunks chunks. With kSwizzle the
+ * chunks of a row are XOR-permuted by the row's low four bits (three for 8-chunk rows), so 16 lanes
+ * reading the same logical chunk of rows with distinct r mod 16 hit 16 different bank groups of the
+ * 64 banks (rows are whole multiples of 64 words apart for S >= 64). */
+template <bool kSwizzle, int kChunks>
 __device__ static inline int hds_stage_chunk(int c, int r) {
-	return kSwizzle ? (c ^ (r & 7)) : c;
+	static_assert(kChunks >= 8 && (kChunks & (kChunks - 1)) == 0, "rows of 8, 16 or 32 chunks");
+	return kSwizzle ? (c ^ (r & (kChunks >= 16 ? 15 : 7))) : c;
 }
 
 /* Issues the copy of rows 0..cnt-1 (S channels from c0 of features[gids[row]]) into buf, one
@@ -45,7 +47,7 @@ __device__ inline void hds_stage_rows_async(float* buf, const float* features, i
 	for (int op = wave; op < kOps; op += 4) {
 		const int row = op * kRowsPerOp + lane / kChunks;
 		if (row < cnt) {
-			const float* src = features + (size_t)gids[row] * channels + c0 + 4 * hds_stage_chunk<kSwizzle>(chunk, row);
+			const float* src = features + (size_t)gids[row] * channels + c0 + 4 * hds_stage_chunk<kSwizzle, kChunks>(chunk, row);
 			__builtin_amdgcn_global_load_lds(src, (hds_lds_void*)(buf + op * 256), 16, 0, 0);
 		}
 	}

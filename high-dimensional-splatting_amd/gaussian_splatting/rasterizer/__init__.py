@@ -3,8 +3,10 @@
 Mirrors gaussian_splatting/rasterizer/__init__.py of the reference: the same `rasterize` signature and
 return values, the `RasterizeGaussians` autograd node, the `FEATURE_SLICE_WIDTH` knob and
 `_get_rasterizer()`, which here returns the ctypes binding of the HIP library instead of a JIT-built
-CUDA extension. The forward renders RGB and features in one tile walk and the backward replays both
-in one back-to-front walk.
+CUDA extension. The forward renders RGB and features in one tile walk. The backward runs two tile
+kernels side by side: a back-to-front replay for the geometry gradients (means2D, conics, opacities,
+colours), and a front-to-back replay that contracts the blend weights with dL/dF for the feature
+gradients.
 """
 from __future__ import annotations
 
@@ -18,7 +20,9 @@ from gaussian_splatting.rasterizer.projection import project_gaussians  # noqa: 
 _rasterizer_module: Any | None = None
 
 # Channels each feature backward work-group owns (32, 64 or 128, dividing C). None picks
-# min(C, 64), which keeps the backward at two waves per SIMD.
+# min(C, 128), as the reference does: every slice replays the tile walk and issues its own geometry
+# atomics, so the widest slice is fastest, and dL/dF for 128 channels still fits the registers of two
+# waves per SIMD.
 FEATURE_SLICE_WIDTH: int | None = None
 
 
@@ -80,7 +84,7 @@ class RasterizeGaussians(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_image, grad_features=None):
-        """Replays each pixel's list back to front for RGB and features at once.
+        """Gradients of the blend for RGB and features from one library call (two kernels side by side).
 
         Returns:
             Gradients for means2D, conics, colors, opacities and features; None for depths, radii,
@@ -93,13 +97,16 @@ class RasterizeGaussians(torch.autograd.Function):
         # means2D, conics, opacities or features needs a gradient (rasterizer/__init__.py:150-152).
         feature_term = (features is not None and grad_features is not None
                         and any(ctx.needs_input_grad[i] for i in (0, 3, 5, 7)))
-        g_means, g_conics, g_colors, g_opac, g_feat = _get_rasterizer().render_backward(
-            means2D, conic, color_opacity, values_sorted, tile_ranges, final_T, n_contrib, width, height,
-            grad_image=grad_image.contiguous(), background=background,
-            features=features if feature_term else None,
-            grad_feature_image=grad_features.contiguous() if feature_term else None,
-            slice_width=(FEATURE_SLICE_WIDTH or default_slice_width(features.shape[1])) if feature_term else None,
-            want_feature_grad=feature_term and ctx.needs_input_grad[7], prezeroed=ctx.prezeroed)
+        # One marker range (a roctx range on ROCm) for what the reference marks as rasterize_backward and
+        # rasterize_features_backward (rasterizer/__init__.py:135, 153): here both are one call.
+        with torch.cuda.nvtx.range("rasterize_backward"):
+            g_means, g_conics, g_colors, g_opac, g_feat = _get_rasterizer().render_backward(
+                means2D, conic, color_opacity, values_sorted, tile_ranges, final_T, n_contrib, width, height,
+                grad_image=grad_image.contiguous(), background=background,
+                features=features if feature_term else None,
+                grad_feature_image=grad_features.contiguous() if feature_term else None,
+                slice_width=(FEATURE_SLICE_WIDTH or default_slice_width(features.shape[1])) if feature_term else None,
+                want_feature_grad=feature_term and ctx.needs_input_grad[7], prezeroed=ctx.prezeroed)
         ctx.prezeroed = None
         return g_means, None, None, g_conics, g_colors, g_opac, None, g_feat, None, None, None
 

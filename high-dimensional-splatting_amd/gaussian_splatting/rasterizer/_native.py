@@ -14,6 +14,7 @@ from __future__ import annotations
 import ctypes
 import math
 import os
+import sys
 from pathlib import Path
 
 import torch
@@ -188,6 +189,16 @@ def _raise_on_sort_error(status: torch.Tensor) -> None:
         raise RuntimeError("bin_emit: a look-back of the tile sort did not complete (every tile range left empty)")
 
 
+def _debug_pairs(n: int, width: int, height: int, pairs: int) -> None:
+    """With HDS_DEBUG or GS_DEBUG set, one line of binning statistics on stderr once the pair count
+    is known, in the reference's debug format (common.cuh:93-101)."""
+    if not (os.environ.get("HDS_DEBUG") or os.environ.get("GS_DEBUG")):
+        return
+    tx, ty = (width + TILE - 1) // TILE, (height + TILE - 1) // TILE
+    print(f"[gs] gaussians={n}  tiles={tx}x{ty}({tx * ty})  duplicates={pairs}  "
+          f"dup/gaussian={pairs / max(n, 1):.1f}  dup/tile={pairs / (tx * ty):.1f}", file=sys.stderr, flush=True)
+
+
 class PendingBins:
     """A binning enqueued by HipRasterizer.bin_async whose pair count the host has not read yet.
 
@@ -337,6 +348,7 @@ class HipRasterizer:
                                           _ptr(opacities), width, height, _ptr(conic4), _ptr(color_opacity4),
                                           _ptr(ws), ws.numel(), ctypes.byref(pairs), stream))
             p = int(pairs.value)
+            _debug_pairs(n, width, height, p)
             values_sorted = torch.empty((p,), device=dev, dtype=torch.int32)
             pws = torch.empty(self.lib.hds_pairs_workspace_bytes(p, width, height) if p else 0, device=dev,
                               dtype=torch.uint8)
@@ -412,6 +424,7 @@ class HipRasterizer:
         _raise_on_sort_error(pending.status)
         if total >= 2**31 - 1:
             raise RuntimeError(f"bin_count: {total} tile-gaussian pairs overflow int32 indices")
+        _debug_pairs(n, width, height, total)
         self._remember_pairs(dev, total)
         if total <= cap:
             pending.values = pending.values[:total]
@@ -469,7 +482,8 @@ class HipRasterizer:
     def render_backward(self, means2D, conic4, color_opacity4, values_sorted, tile_ranges, final_T, n_contrib,
                         width, height, grad_image=None, background=None, features=None, grad_feature_image=None,
                         slice_width=None, want_feature_grad=True, prezeroed=None):
-        """One back-to-front walk (backward.cu:7-164 + features.cu:350-542). `prezeroed` is a
+        """The blend backward (backward.cu:7-164 + features.cu:350-542): geometry gradients from a
+        back-to-front replay, feature gradients from a front-to-back replay beside it. `prezeroed` is a
         (buffers, event) pair from prezeroed_gradients: the gradients are then added into those
         buffers once the event has passed, instead of into buffers zeroed here.
 

@@ -54,9 +54,10 @@ class ProjectGaussians(torch.autograd.Function):
             grad_means2D = torch.zeros(means.shape[0], 2, device=means.device)
         if grad_conics is None:
             grad_conics = torch.zeros(means.shape[0], 3, device=means.device)
-        grads = _get_rasterizer().project_gaussians_backward(
-            grad_means2D.contiguous(), grad_conics.contiguous(), means, scales, quats, world_to_camera,
-            *ctx.camera, NEAR_PLANE, LOW_PASS, JACOBIAN_FOV_SCALE)
+        with torch.cuda.nvtx.range("project_backward"):  # a roctx range on ROCm (projection.py:88)
+            grads = _get_rasterizer().project_gaussians_backward(
+                grad_means2D.contiguous(), grad_conics.contiguous(), means, scales, quats, world_to_camera,
+                *ctx.camera, NEAR_PLANE, LOW_PASS, JACOBIAN_FOV_SCALE)
         return (*grads, None, None, None, None, None, None, None, None)
 
 

@@ -43,10 +43,11 @@ class EvalSH(torch.autograd.Function):
         dc, dc_group, dc_state = _adam_slot(ctx.optimizer, "sh_dc")
         rest, rest_group, rest_state = _adam_slot(ctx.optimizer, "sh_rest")
         beta1, beta2 = dc_group["betas"]
-        grad_dirs = _get_rasterizer().eval_sh_backward_adam(
-            grad_rgb.contiguous(), dc.data, rest.data, dirs, ctx.degree, radii,
-            dc_state["exp_avg"], dc_state["exp_avg_sq"], rest_state["exp_avg"], rest_state["exp_avg_sq"],
-            dc_state["step"], rest_state["step"], dc_group["lr"], rest_group["lr"], beta1, beta2, dc_group["eps"])
+        with torch.cuda.nvtx.range("sh_backward"):  # a roctx range on ROCm (utils/sh.py:76)
+            grad_dirs = _get_rasterizer().eval_sh_backward_adam(
+                grad_rgb.contiguous(), dc.data, rest.data, dirs, ctx.degree, radii,
+                dc_state["exp_avg"], dc_state["exp_avg_sq"], rest_state["exp_avg"], rest_state["exp_avg_sq"],
+                dc_state["step"], rest_state["step"], dc_group["lr"], rest_group["lr"], beta1, beta2, dc_group["eps"])
         return None, None, grad_dirs, None, None, None
 
 

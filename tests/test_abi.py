@@ -160,3 +160,18 @@ def test_static_binning_scratch_holds_the_documented_scene(lib):
     mib = int(re.search(r"#define HDS_BIN_STATIC_SCRATCH_MIB (\d+)", HEADER.read_text()).group(1))
     for n, pairs in ((1_500_000, 4_000_000), (1_180_000, int(1.25 * 1_921_191))):
         assert lib.hds_bin_workspace_bytes(n, 979, 546) + lib.hds_pairs_workspace_bytes(pairs, 979, 546) <= mib << 20
+
+
+def test_debug_mode_prints_the_reference_binning_line(monkeypatch, capsys):
+    """GS_DEBUG (or HDS_DEBUG) prints the reference's one-line binning statistics (common.cuh:93-101)
+    once the pair count is known; without it nothing is printed."""
+    from gaussian_splatting.rasterizer._native import _debug_pairs
+
+    monkeypatch.delenv("HDS_DEBUG", raising=False)
+    monkeypatch.delenv("GS_DEBUG", raising=False)
+    _debug_pairs(1000, 979, 546, 2500)
+    assert capsys.readouterr().err == ""
+    monkeypatch.setenv("GS_DEBUG", "1")
+    _debug_pairs(1000, 979, 546, 2500)
+    assert capsys.readouterr().err == (
+        "[gs] gaussians=1000  tiles=62x35(2170)  duplicates=2500  dup/gaussian=2.5  dup/tile=1.2\n")
