@@ -118,6 +118,55 @@ __device__ inline uint64_t lookback(uint64_t* status, int64_t stride, int64_t pa
 	return sum;
 }
 
+// Single-column look-back walked by a whole wave (every lane of the wave calls it with the same
+// arguments and gets the sum): each step loads the words of the 64 partitions before p at once, so
+// the walk advances up to 64 partitions per memory latency. Status words written by work-groups on
+// other XCDs are read at agent scope, which costs a trip past the L2, so the number of dependent
+// steps is what a look-back's time is made of.
+__device__ inline uint64_t wave_sum64(uint64_t v) {
+#pragma unroll
+	for (int off = 1; off < HDS_WAVE; off <<= 1) v += __shfl_xor(v, off, HDS_WAVE);
+	return v;
+}
+
+__device__ inline uint64_t lookback_wave(uint64_t* status, int64_t part, uint32_t epoch, uint32_t* error,
+										 uint32_t spin_limit) {
+	const uint32_t agg = 2 * epoch + 1, inc = 2 * epoch + 2;
+	const int lane = threadIdx.x & (HDS_WAVE - 1);
+	if (spin_limit == 0u) {
+		// Failure-path test mode (set from the host): give up before the first poll.
+		if (lane == 0) atomicOr(error, 1u);
+		return 0;
+	}
+	uint64_t sum = 0;
+	uint32_t spins = 0;
+	int64_t p = part - 1;
+	while (p >= 0) {
+		// Lane l reads partition p - l; below partition 0 reads as an inclusive prefix of 0.
+		const int64_t q = p - lane;
+		const uint64_t v = q >= 0 ? status_load(status + q) : status_word(inc, 0);
+		const uint32_t flag = (uint32_t)(v >> 56);
+		const uint64_t inc_lanes = hds_ballot(flag == inc);
+		const uint64_t unready_lanes = hds_ballot(flag != inc && flag != agg);
+		const int first_inc = inc_lanes ? (int)__builtin_ctzll(inc_lanes) : HDS_WAVE;
+		const int first_unready = unready_lanes ? (int)__builtin_ctzll(unready_lanes) : HDS_WAVE;
+		if (first_inc < first_unready) return sum + wave_sum64(lane <= first_inc ? (v & kValueMask) : 0);
+		// Lanes below the first unpublished word hold aggregates.
+		sum += wave_sum64(lane < first_unready ? (v & kValueMask) : 0);
+		p -= first_unready;
+		if (first_unready > 0) {
+			spins = 0;
+			continue;
+		}
+		if (++spins > spin_limit) {
+			if (lane == 0) atomicOr(error, 1u);
+			return sum;
+		}
+		__builtin_amdgcn_s_sleep(2);
+	}
+	return sum;
+}
+
 // Partition index in launch order (the look-back's progress guarantee), broadcast through LDS.
 __device__ inline int64_t take_ticket(uint32_t* ticket, int64_t* s_part) {
 	if (threadIdx.x == 0) *s_part = (int64_t)atomicAdd(ticket, 1u);
@@ -386,17 +435,21 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const uint2* __restrict_
 	}
 	uint32_t block_total;
 	const uint32_t before_thread = block_exclusive_scan(sum, s_wave, block_total);
-	if (threadIdx.x == 0) {
+	if (threadIdx.x < HDS_WAVE) {
+		// Wave 0 publishes the partition's total and walks the look-back together.
+		const bool lead = threadIdx.x == 0;
 		uint64_t before = 0;
 		if (part == 0) {
-			status_store(status, status_word(2, block_total));
+			if (lead) status_store(status, status_word(2, block_total));
 		} else {
-			status_store(status + part, status_word(1, block_total));
-			before = lookback<16>(status, 1, part, 0, error, spin_limit);
-			status_store(status + part, status_word(2, before + block_total));
+			if (lead) status_store(status + part, status_word(1, block_total));
+			before = lookback_wave(status, part, 0, error, spin_limit);
+			if (lead) status_store(status + part, status_word(2, before + block_total));
 		}
-		if (base + kTileItems >= n) *total = before + block_total;
-		s_before = before;
+		if (lead) {
+			if (base + kTileItems >= n) *total = before + block_total;
+			s_before = before;
+		}
 	}
 	__syncthreads();
 	const uint32_t offset = (uint32_t)s_before + before_thread;
