@@ -49,6 +49,9 @@ def parse_args():
     ap.add_argument("--no-cpu-baseline", action="store_true",
                     help="skip the CPU oracle (its timing and the agreement check it provides)")
     ap.add_argument("--no-split", action="store_true", help="skip the separate fwd / bwd median timing")
+    ap.add_argument("--breakdown-steps", type=int, default=10,
+                    help="steps after the timed region with events around every call and kernel, for the "
+                         "per-stage and per-kernel figures")
     ap.add_argument("--frozen-features", action="store_true",
                     help="features without requires_grad: the backward keeps the feature term of the geometry "
                          "gradients but writes no grad_features (reference test_render.py:118-134)")
@@ -235,14 +238,14 @@ def main() -> int:
                               "error": "disagrees with the oracle; not timed", "agreement": agreement}), flush=True)
             return 1
 
-    # Timed region: exactly `steps` fwd+bwd steps between two device synchronisations, with the
-    # library's stage timer recording HIP events around every call on the compute stream.
-    timer = StageTimer()
-    ext.timer = timer
+    # Timed region: exactly `steps` fwd+bwd steps between two device synchronisations. The library
+    # records HIP events around the blend backward's kernels only (the roofline's duration): every
+    # recorded launch adds two timed events to its stream, a few microseconds each, which around every
+    # kernel and call of the step added about 0.19 ms to it.
     step_events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                    for _ in range(args.steps)]
     torch.cuda.synchronize()
-    with KernelProfile() as kprof:
+    with KernelProfile(only=BACKWARD_KERNELS) as kprof:
         t0 = time.perf_counter()
         for start, end in step_events:
             start.record()
@@ -250,13 +253,23 @@ def main() -> int:
             end.record()
         torch.cuda.synchronize()
         wall_ms = (time.perf_counter() - t0) * 1e3
-    ext.timer = None
     kernels = kprof.summary()
-    stages = timer.summary()
     step_ms = [s.elapsed_time(e) for s, e in step_events]
     ms_per_step = wall_ms / args.steps
     print(f"[bench] timed {args.steps} steps: {ms_per_step:.3f} ms/step wall, median {statistics.median(step_ms):.3f}",
           file=sys.stderr, flush=True)
+
+    # Breakdown, after the timed region: a few more steps with events around every library call
+    # (stages) and every kernel, for the per-stage and per-kernel figures of the JSON line.
+    timer = StageTimer()
+    ext.timer = timer
+    with KernelProfile() as breakdown_prof:
+        for _ in range(args.breakdown_steps):
+            step()
+        torch.cuda.synchronize()
+    ext.timer = None
+    stages = timer.summary()
+    breakdown_kernels = breakdown_prof.summary()
 
     # Counts the roofline needs: visible gaussians and tile-gaussian pairs of this frame.
     with torch.no_grad():
@@ -269,7 +282,7 @@ def main() -> int:
     alg = algorithmic_bytes(N, n_vis, pairs, hw, C)
     stage_report = {}
     for name, row in stages.items():
-        entry = {"launches_per_step": row["launches"] / args.steps, "mean_ms": round(row["mean_ms"], 4)}
+        entry = {"launches_per_step": row["launches"] / max(args.breakdown_steps, 1), "mean_ms": round(row["mean_ms"], 4)}
         if name in alg and row["mean_ms"] > 0:
             gbs = alg[name] / (row["mean_ms"] * 1e-3) / 1e9
             entry.update({"algorithmic_MB": round(alg[name] / 1e6, 2), "achieved_GBs": round(gbs, 1),
@@ -294,8 +307,9 @@ def main() -> int:
                 "traffic": traffic_per_step(bwd_names, wl.name + ("-rgb-only" if args.rgb_only else "")),
                 "algorithmic_bytes": int(alg["render_backward"]), "ms_per_call": round(bwd_ms, 4),
                 "kernel_mean_ms": {k: round(kernels[k]["mean_ms"], 4) for k in bwd_names}}
-    kernel_report = {k: {"launches_per_step": round(v["launches"] / args.steps, 2), "mean_ms": round(v["mean_ms"], 4)}
-                     for k, v in sorted(kernels.items(), key=lambda kv: -kv[1]["total_ms"])}
+    kernel_report = {k: {"launches_per_step": round(v["launches"] / max(args.breakdown_steps, 1), 2),
+                         "mean_ms": round(v["mean_ms"], 4)}
+                     for k, v in sorted(breakdown_kernels.items(), key=lambda kv: -kv[1]["total_ms"])}
     total_alg = sum(alg.values())
     step_frac = total_alg / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS
 
@@ -322,7 +336,8 @@ def main() -> int:
                    "loss": "0.8 L1 + 0.2 (1 - SSIM)" if target is not None else "none (dL/dimage U[0, 1])"},
         "step_ms_median": round(statistics.median(step_ms), 4), **split,
         "step_hbm_frac": round(step_frac, 4), "step_algorithmic_MB": round(total_alg / 1e6, 1),
-        "roofline": roofline, "stages": stage_report, "kernels": kernel_report, "cpu_baseline": cpu,
+        "roofline": roofline, "breakdown_steps": args.breakdown_steps, "stages": stage_report,
+        "kernels": kernel_report, "cpu_baseline": cpu,
         "agreement": agreement, "channel_sweep": channel_sweep, "environment": environment(),
     }
     print(json.dumps(line), flush=True)
@@ -337,12 +352,15 @@ def main() -> int:
     return 0
 
 
+# The blend backward's kernels: the only launches the library times inside the timed region.
+BACKWARD_KERNELS = ("backward_geometry_kernel", "backward_features_kernel")
+
+
 def backward_span(kernels: dict, timeline) -> tuple[list[str], float]:
     """The blend backward's kernels in the timed region and the mean duration of one
     hds_render_backward call: with two kernels side by side on two streams, their span (first start
     to last end); with one, its mean."""
-    names = [k for k in ("backward_geometry_kernel", "backward_features_kernel", "backward_fused_kernel")
-             if k in kernels]
+    names = [k for k in BACKWARD_KERNELS if k in kernels]
     if len(names) == 2:
         return names, concurrent_span_ms(timeline, *names)
     return names, kernels[names[0]]["mean_ms"]
@@ -421,7 +439,7 @@ def measure_sweep(wl, leaves: dict, w2c, channels_list, n_vis: int, pairs: int, 
         steps = min(args.steps, 20)
         events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
         torch.cuda.synchronize()
-        with KernelProfile() as kprof:
+        with KernelProfile(only=BACKWARD_KERNELS) as kprof:
             for start, end in events:
                 start.record()
                 reset(), forward(), backward()

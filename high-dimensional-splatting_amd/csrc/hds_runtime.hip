@@ -5,7 +5,9 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
 #include <mutex>
+#include <string>
 #include <vector>
 
 #include "hds_internal.h"
@@ -66,11 +68,19 @@ std::mutex g_profile_mutex;
 bool g_profile_on = false;
 std::vector<ProfileRecord> g_profile;
 int64_t g_profile_used = 0;
+std::vector<std::string> g_profile_only;  // kernels to record; empty = all
+
+bool profile_wanted(const char* name) {
+	if (g_profile_only.empty()) return true;
+	for (const std::string& k : g_profile_only)
+		if (k == name) return true;
+	return false;
+}
 }  // namespace
 
 HdsKernelTimer::HdsKernelTimer(const char* name, hipStream_t stream) : slot_(-1), stream_(stream) {
 	std::lock_guard<std::mutex> lock(g_profile_mutex);
-	if (!g_profile_on) return;
+	if (!g_profile_on || !profile_wanted(name)) return;
 	if (g_profile_used == (int64_t)g_profile.size()) {
 		ProfileRecord r{name, nullptr, nullptr};
 		if (hipEventCreate(&r.start) != hipSuccess) return;
@@ -93,12 +103,24 @@ void HdsKernelTimer::stop() {
 	slot_ = -1;
 }
 
-extern "C" int hds_profile_begin(void) {
+extern "C" int hds_profile_begin_only(const char* kernels) {
 	std::lock_guard<std::mutex> lock(g_profile_mutex);
+	g_profile_only.clear();
+	if (kernels) {
+		const char* p = kernels;
+		while (*p) {
+			const char* comma = std::strchr(p, ',');
+			const size_t len = comma ? (size_t)(comma - p) : std::strlen(p);
+			if (len > 0) g_profile_only.emplace_back(p, len);
+			p += len + (comma ? 1 : 0);
+		}
+	}
 	g_profile_used = 0;
 	g_profile_on = true;
 	return HDS_OK;
 }
+
+extern "C" int hds_profile_begin(void) { return hds_profile_begin_only(nullptr); }
 
 extern "C" int64_t hds_profile_end(void) {
 	std::lock_guard<std::mutex> lock(g_profile_mutex);

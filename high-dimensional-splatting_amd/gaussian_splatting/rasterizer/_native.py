@@ -58,6 +58,7 @@ PROTOTYPES = {
     "hds_ssim_backward": (_i32, [_i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "hds_densification_stats": (_i32, [_i64, _vp, _vp, _i32, _i32, _vp, _vp, _vp, _vp]),
     "hds_profile_begin": (_i32, []),
+    "hds_profile_begin_only": (_i32, [ctypes.c_char_p]),
     "hds_profile_end": (_i64, []),
     "hds_profile_record": (_i32, [_i64, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_float)]),
     "hds_profile_timeline": (_i32, [_i64, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_float),
@@ -95,14 +96,17 @@ class KernelProfile:
 
     Used as a context manager around a timed region; afterwards `summary()` gives
     {kernel: {"launches": n, "total_ms": t, "mean_ms": t / n}}. Every hot-path launch is bracketed
-    with events on its own stream, so the durations are those of the kernels themselves."""
+    with events on its own stream, so the durations are those of the kernels themselves; with `only`
+    (kernel names) just those launches are, which keeps the events' own cost out of the rest."""
 
-    def __init__(self):
+    def __init__(self, only=None):
+        self.only = None if only is None else ",".join(only)
         self.records: list[tuple[str, float]] = []
         self.timeline: list[tuple[str, float, float]] = []  # (kernel, start ms, end ms) from the first start
 
     def __enter__(self):
-        _check(load_library().hds_profile_begin())
+        lib = load_library()
+        _check(lib.hds_profile_begin() if self.only is None else lib.hds_profile_begin_only(self.only.encode()))
         return self
 
     def __exit__(self, *exc):

@@ -238,6 +238,12 @@ HDS_API int hds_densification_stats(int64_t n, const float* grad_means2D, const 
  * blend-backward kernels) is bracketed by HIP events on its own stream. Clears earlier records. */
 HDS_API int hds_profile_begin(void);
 
+/* hds_profile_begin restricted to the kernels named in `kernels`, a comma-separated list of kernel
+ * names as hds_profile_record reports them (NULL or "" records every kernel). Each recorded launch
+ * adds two timed events to its stream, a few microseconds each, so a benchmark that times a whole
+ * step records only the kernels whose durations it needs. */
+HDS_API int hds_profile_begin_only(const char* kernels);
+
 /* Stops recording, waits for the recorded events and returns how many launches were recorded
  * (negative on error). */
 HDS_API int64_t hds_profile_end(void);
