@@ -75,7 +75,7 @@ __device__ static inline int hds_rank_below(uint64_t mask) {
 	return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
 }
 
-__device__ static inline uint64_t hds_ballot(bool pred) { return (uint64_t)__ballot(pred); }
+__device__ static inline uint64_t hds_ballot(bool pred) { return __builtin_amdgcn_ballot_w64(pred); }
 
 /* Keeps the compiler from moving the LDS accesses of one wave across this point. A wave's LDS
  * instructions execute in order, so lanes then see each other's earlier LDS writes. It is not a
@@ -151,10 +151,14 @@ typedef uint32_t hds_u32x4 __attribute__((ext_vector_type(4)));
 
 __device__ static inline uint32_t hds_bf16_bits(__bf16 h) { return (uint32_t)__builtin_bit_cast(unsigned short, h); }
 
+/* x -> hi (bits 0-15) | lo (bits 16-31). The second packed conversion rounds x again, to the same hi,
+ * beside the residual, so the pair is packed by the conversion itself (4 instructions). */
 __device__ static inline uint32_t hds_split_pack(float x) {
-	const __bf16 hi = (__bf16)x;
-	const __bf16 lo = (__bf16)(x - (float)hi);
-	return hds_bf16_bits(hi) | (hds_bf16_bits(lo) << 16);
+	typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+	typedef float f32x2 __attribute__((ext_vector_type(2)));
+	const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){x, 0.0f}, bf16x2));
+	const float hi = __builtin_bit_cast(float, h << 16);
+	return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){x, x - hi}, bf16x2));
 }
 
 /* Eight packed words -> the hi and lo bf16x8 operands of one MFMA. */

@@ -492,14 +492,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void b
 	flush_gradients(num_batches - 1);
 }
 
-// dF[position][c] += sum_px W[position][px] dL/dF[px][c] for one group of 32 positions, then one
-// atomic per (position, channel). rows: W as [position][pixel] split-packed; gid_row: lane r < 32
-// holds the gaussian of row r (-1 for padding rows); gids: the wave's 32-int LDS scratch.
+// dF[position][c] += sum_px W[position][px] dL/dF[px][c] for one group of up to 32 positions, then
+// one atomic per (position, channel). rows: W as [position][pixel] split-packed; gids: the gaussian
+// of each of the wave's `used` rows (rows from `used` on are stale and skipped).
 template <int S>
 __device__ inline void flush_features(const hds_bf16x8 (&gb_hi)[4][S / 32], const hds_bf16x8 (&gb_lo)[4][S / 32],
-									  const uint32_t* rows, int gid_row, int* gids, float* grad_features, int channels_log2,
-									  int c0, int lane) {
-	if (lane < kFeatGroup) gids[lane] = gid_row;
+									  const uint32_t* rows, const int* gids, int used, float* grad_features,
+									  int channels_log2, int c0, int lane) {
 	hds_wave_fence();
 	// A = W: row lane % 32 = position, k = pixels 16kp + 8(lane / 32) + 0..7.
 	hds_bf16x8 a_hi[4], a_lo[4];
@@ -516,11 +515,12 @@ __device__ inline void flush_features(const hds_bf16x8 (&gb_hi)[4][S / 32], cons
 	int gid[16];
 #pragma unroll
 	for (int g = 0; g < 4; g++) {
-		const int4 v = *reinterpret_cast<const int4*>(gids + 8 * g + 4 * (lane >> 5));
-		gid[4 * g + 0] = v.x;
-		gid[4 * g + 1] = v.y;
-		gid[4 * g + 2] = v.z;
-		gid[4 * g + 3] = v.w;
+		const int r = 8 * g + 4 * (lane >> 5);
+		const int4 v = *reinterpret_cast<const int4*>(gids + r);
+		gid[4 * g + 0] = r + 0 < used ? v.x : -1;
+		gid[4 * g + 1] = r + 1 < used ? v.y : -1;
+		gid[4 * g + 2] = r + 2 < used ? v.z : -1;
+		gid[4 * g + 3] = r + 3 < used ? v.w : -1;
 	}
 	float* const base = grad_features + c0 + (lane & 31);
 #pragma unroll
@@ -594,8 +594,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S >= 128 ? 
 	int* gids = s_ggid[wave];
 
 	float T = 1.0f;
-	int q = 0;          // filled positions of the wave's current group (wave-uniform)
-	int gid_row = -1;   // lane r < 32: gaussian of group row r
+	int q = 0;  // filled positions of the wave's current group (wave-uniform)
 	const int num_batches = (num + kBatch - 1) / kBatch;
 	auto batch_count = [&](int b) { return b < num_batches ? min(kBatch, num - b * kBatch) : 0; };
 	if (num_batches > 0) {
@@ -609,8 +608,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S >= 128 ? 
 		__syncthreads();
 	}
 	auto flush = [&]() {
-		flush_features<S>(gb_hi, gb_lo, rows, (lane & 31) < q ? gid_row : -1, gids, a.grad_features, channels_log2, c0,
-						  lane);
+		flush_features<S>(gb_hi, gb_lo, rows, gids, q, a.grad_features, channels_log2, c0, lane);
 		q = 0;
 	};
 	// One batch: stage b+1, read the gids of b+2, walk b.
@@ -659,12 +657,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S >= 128 ? 
 						w = alpha[u] * T;
 						T = test_T;
 					}
-					// A gaussian no pixel of the block takes gets no row (and no atomics).
+					// A gaussian no pixel of the block takes gets no row (and no atomics). Every lane
+					// writes the row's gaussian id to the same word.
 					if (hds_ballot(contributes) != 0) {
-						s_w[wave][q * kRowStride + lane] = hds_split_pack(w);
-						const int g = __builtin_amdgcn_readlane(slot_gid, slot[u]);
-						if ((lane & 31) == q) gid_row = g;
-						q = __builtin_amdgcn_readfirstlane(q + 1);
+						rows[q * kRowStride + lane] = hds_split_pack(w);
+						gids[q] = __builtin_amdgcn_readlane(slot_gid, slot[u]);
+						q++;
 					}
 				}
 			}
