@@ -182,6 +182,7 @@ def main() -> int:
             means2D.retain_grad()
             conics.retain_grad()
             state["means2D"], state["conics"] = means2D, conics
+            state["projected"] = (means2D, depths, radii, conics)
         state["out"] = rasterize(means2D, depths, radii, conics, leaves["colors"], leaves["opacities"][:, None],
                                  W, H, features=leaves.get("features"))
 
@@ -229,6 +230,9 @@ def main() -> int:
                    "means2D": state["means2D"].grad, "conics": state["conics"].grad,
                    **{name: leaf.grad for name, leaf in leaves.items()}}
         gpu_out = {k: v.detach().cpu().numpy() for k, v in gpu_out.items()}
+        # The rasterizer's own inputs, for the oracle's forward on identical inputs.
+        gpu_out["rasterizer_inputs"] = [t.detach().cpu().numpy() for t in state.pop("projected")] + [
+            leaves["colors"].detach().cpu().numpy(), leaves["opacities"].detach().cpu().numpy()]
         state.pop("means2D"), state.pop("conics")
         cpu, want = cpu_baseline(wl, colors, grad_image, grad_features, loss_target=target)
         agreement = agree(gpu_out, want)
@@ -530,8 +534,8 @@ def cpu_baseline(wl, colors, grad_image, grad_features, loss_target=None):
     m2, d, r, c = oracle.project_forward(means, scales, quats, opac, w2c, cam["fx"], cam["fy"], cam["cx"],
                                          cam["cy"], cam["width"], cam["height"])
     _, values, ranges = oracle.bin_gaussians(m2, d, r, c, opac, cam["width"], cam["height"])
-    image, T, nc, fimg, near = oracle.render_forward(cam["width"], cam["height"], ranges, values, m2, c, opac, cols,
-                                                     np.zeros(3, np.float32), feats, near_cut=True)
+    image, T, nc, fimg = oracle.render_forward(cam["width"], cam["height"], ranges, values, m2, c, opac, cols,
+                                               np.zeros(3, np.float32), feats)
     t1 = time.perf_counter()
     if loss_target is not None:
         # d/dimage of 0.8 mean|image - target| + 0.2 (1 - mean SSIM): sign / numel, and the SSIM
@@ -552,16 +556,23 @@ def cpu_baseline(wl, colors, grad_image, grad_features, loss_target=None):
         torch.nn.functional.normalize(q, dim=-1).backward(torch.from_numpy(np.ascontiguousarray(d_unit)))
         return q.grad.numpy()
 
+    def forward_stage(m2_, d_, r_, c_, col_, op_):
+        # The oracle's binning and blend forward on the GPU projection's outputs (identical inputs).
+        _, values_, ranges_ = oracle.bin_gaussians(m2_, d_, r_, c_, op_, cam["width"], cam["height"])
+        out = oracle.render_forward(cam["width"], cam["height"], ranges_, values_, m2_, c_, op_, col_,
+                                    np.zeros(3, np.float32), feats)
+        return out[0], out[3]
+
     def projection_stage(grad_means2D, grad_conics):
         # The oracle's projection backward (and the normalize chain) on given upstream gradients.
         pm, ps, pq = oracle.project_backward(grad_means2D, grad_conics, means, scales, quats, w2c, cam["fx"],
                                              cam["fy"], cam["cx"], cam["cy"], cam["width"], cam["height"])
         return {"means": pm, "scales": ps, "quats": normalize_backward(pq)}
 
-    want = {"image": image, "feature_image": fimg, "near_cut": near, "means2D": dm, "conics": dc,
+    want = {"image": image, "feature_image": fimg, "means2D": dm, "conics": dc,
             "opacities": np.asarray(dop).reshape(-1), "colors": dcol, "features": df,
             "chain": {"means": dmeans, "scales": dscales, "quats": normalize_backward(dq)},
-            "projection_stage": projection_stage}
+            "projection_stage": projection_stage, "forward_stage": forward_stage}
     return ({"value": round((t2 - t0) * 1e3, 1), "unit": "ms", "cores": oracle.num_threads(), "kind": "port",
              "fwd_ms": round((t1 - t0) * 1e3, 1), "bwd_ms": round((t2 - t1) * 1e3, 1),
              "sample": f"one full fwd+bwd frame of {wl.name} (same inputs) on the C oracle, OpenMP",
@@ -575,9 +586,9 @@ GATE_MAX_REL = 2e-3
 
 def agree(got: dict, want: dict) -> dict:
     """The parity tests' bars on this frame, stage by stage, each stage on identical inputs:
-      - images by max / 99th percentile error on the pixels clear of the oracle's near_cut mask (an
-        alpha or transmittance within rounding distance of its cut, where the GPU's exp2 and libm's
-        expf may decide differently), which must be under 0.1% of the frame;
+      - the blend forward on the GPU projection's outputs: the RGB image bit for bit (both sides take
+        alpha from hds_gauss_alpha and blend with the same fused multiply-adds), the feature image by
+        max / 99th percentile error;
       - the rasterizer's gradients (means2D, conics, colors, opacities, features) against the oracle's
         rasterizer on the same projected inputs;
       - the projection backward (means, scales and the quats leaf through normalize) against the
@@ -587,16 +598,18 @@ def agree(got: dict, want: dict) -> dict:
     rasterizer gradients) are reported under "chain" without a bar: composing the two stages
     amplifies their ~1e-6 relative differences by the conditioning of the conic -> quaternion map of
     elongated gaussians."""
+    import numpy as np
+
     from tests.tolerances import grad_error, image_error
 
     report, passed = {}, True
-    near = want["near_cut"]
-    report["near_cut_pixels"] = int(near.sum())
-    passed &= near.mean() < 1e-3
-    for name, (max_error, max_p99) in (("image", (2e-3, 1e-4)), ("feature_image", (1e-3, 5e-4))):
-        worst, p99 = image_error(got[name][~near], want[name][~near])
-        report[name] = {"max": worst, "p99": p99}
-        passed &= worst < max_error and p99 < max_p99
+    want_image, want_fimg = want["forward_stage"](*got["rasterizer_inputs"])
+    differ = int(np.sum(got["image"] != want_image))
+    report["image"] = {"values_differing": differ}
+    passed &= differ == 0
+    worst, p99 = image_error(got["feature_image"], want_fimg)
+    report["feature_image"] = {"max": worst, "p99": p99}
+    passed &= worst < 1e-3 and p99 < 5e-4
     for name in ("means2D", "conics", "colors", "opacities", "features"):
         outside, rel = grad_error(got[name].reshape(want[name].shape), want[name])
         report[name] = {"outside": outside, "max_rel": rel}

@@ -299,11 +299,8 @@ __device__ static inline float hds_raw_alpha(float px, float py, float2 mean, fl
 											 float& dx, float& dy) {
 	dx = px - mean.x;
 	dy = py - mean.y;
-	const float m = dx * (conic_op.x * dx + conic_op.y * dy) + dy * (conic_op.y * dx + conic_op.z * dy);
-	// exp(-m / 2) as the hardware exp2 of m * (-log2(e) / 2): halving is exact, so the product is
-	// bit for bit the (-0.5 m) * log2(e) that __expf(-0.5 m) forms, with one multiply less.
-	G = __builtin_amdgcn_exp2f(m * (-0.5f * 1.44269502162933349609375f));
-	return conic_op.w * G;
+	// The oracle's arithmetic (hds_common.h), bit for bit.
+	return hds_gauss_alpha(dx, dy, conic_op.x, conic_op.y, conic_op.z, conic_op.w, &G);
 }
 
 #endif /* HDS_INTERNAL_H */

@@ -231,9 +231,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S >= 128 ? 
 								} else {
 									w[q] = alpha[u] * st.T;
 									if constexpr (RGB) {
-										st.r += w[q] * col[u].x;
-										st.g += w[q] * col[u].y;
-										st.b += w[q] * col[u].z;
+										// fmaf as the oracle does: the RGB image is bit-exact.
+										st.r = fmaf(w[q], col[u].x, st.r);
+										st.g = fmaf(w[q], col[u].y, st.g);
+										st.b = fmaf(w[q], col[u].z, st.b);
 									}
 									st.T = test_T;
 									st.last = batch + slot[q] + 1;
@@ -265,9 +266,9 @@ write_out:
 	if (inside && slice == 0) {
 		const int64_t pix = (int64_t)py * a.width + px;
 		if constexpr (RGB) {
-			a.image[pix * 3 + 0] = st.r + st.T * a.background[0];
-			a.image[pix * 3 + 1] = st.g + st.T * a.background[1];
-			a.image[pix * 3 + 2] = st.b + st.T * a.background[2];
+			a.image[pix * 3 + 0] = fmaf(st.T, a.background[0], st.r);
+			a.image[pix * 3 + 1] = fmaf(st.T, a.background[1], st.g);
+			a.image[pix * 3 + 2] = fmaf(st.T, a.background[2], st.b);
 		}
 		a.final_T[pix] = st.T;
 		a.n_contrib[pix] = st.last;

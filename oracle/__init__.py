@@ -47,6 +47,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     i64, i32, f32, f64, vp = ctypes.c_int64, ctypes.c_int, ctypes.c_float, ctypes.c_double, ctypes.c_void_p
     lib.orc_logf.argtypes = [f32]
     lib.orc_logf.restype = f32
+    lib.orc_exp2f.argtypes = [i64, vp, vp]
+    lib.orc_exp2f.restype = None
     lib.orc_tile_rect.argtypes = [f32] * 6 + [i32, i32, vp]
     lib.orc_tile_rect.restype = i32
     cam = [f32, f32, f32, f32, i32, i32, f32, f32, f32]
@@ -97,6 +99,14 @@ def num_threads() -> int:
 def logf(x: float) -> float:
     """hds_logf, the shared float32 natural log used by the tile rectangle on both CPU and GPU."""
     return float(_load().orc_logf(float(x)))
+
+
+def exp2f(x: np.ndarray) -> np.ndarray:
+    """hds_exp2f elementwise: the shared float32 2^x behind every blend alpha on CPU and GPU."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    _load().orc_exp2f(x.size, x.ctypes.data, y.ctypes.data)
+    return y
 
 
 def tile_rect(ux, uy, a, b, c, opacity, tiles_x, tiles_y):
@@ -207,8 +217,9 @@ def render_forward(width, height, tile_ranges, values_sorted, means2D, conics, o
     Returns (image [H, W, 3] or None, final_T [H, W], n_contrib [H, W], feature_image [H, W, C] or None),
     and with near_cut=True also a [H, W] bool mask of the pixels whose walk passed an alpha or a
     transmittance within twice its propagated rounding uncertainty of the 1/255 or 1e-4 cut:
-    the decisions that other rounding (the GPU's hardware exp2 and fused multiply-adds against libm's
-    expf and separate products) can flip.
+    the decisions that an implementation with other rounding (another exp, other fused
+    multiply-adds) could flip. The HIP kernels share this oracle's alpha arithmetic
+    (hds_gauss_alpha) and take every decision identically on identical inputs.
     """
     ranges, values = _i32(tile_ranges), _i32(values_sorted)
     means2D, conics, opacities = _f32(means2D), _f32(conics), _f32(opacities).reshape(-1)

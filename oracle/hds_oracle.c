@@ -12,9 +12,12 @@
  * cpu_baseline leg may load it. The product path is the HIP library, which has no CPU fallback.
  *
  * Differences from the reference, all deliberate:
- *   - The blend uses libm expf where the reference uses __expf, and plain float products where the
- *     reference's feature kernel rounds weights and features to TF32 (features.cu:50-58). So this
- *     is the float32 semantics of tests/oracle.py, not the L4's rounding.
+ *   - The blend takes alpha from hds_gauss_alpha (hds_common.h: the quadratic form in fmaf and an
+ *     exp2 of its own, shared with the HIP kernels) where the reference uses __expf, accumulates
+ *     RGB and the background term with fmaf as the HIP forward does, and uses plain float products
+ *     where the reference's feature kernel rounds weights and features to TF32
+ *     (features.cu:50-58). So alpha, T, n_contrib and the RGB image come out bit for bit as on the
+ *     GPU; the feature channels are the float32 semantics of tests/oracle.py.
  *   - The natural log inside tile_rect is hds_logf (hds_common.h), shared with the HIP kernels,
  *     so integer binning results can be compared bit for bit.
  *
@@ -45,6 +48,11 @@
 /* ------------------------------------------------------------------------------------------- */
 
 ORC_EXPORT float orc_logf(float x) { return hds_logf(x); }
+
+/* hds_exp2f over an array (pinned by tests/test_oracle_pinning.py against 2^x in double). */
+ORC_EXPORT void orc_exp2f(int64_t n, const float* x, float* y) {
+	for (int64_t i = 0; i < n; i++) y[i] = hds_exp2f(x[i]);
+}
 
 ORC_EXPORT int orc_tile_rect(float ux, float uy, float a, float b, float c, float op, int tiles_x,
 							 int tiles_y, int* rect4) {
@@ -369,12 +377,9 @@ static inline float orc_alpha(float px, float py, const float* mean, const float
 							  float* gauss, float* dx_out, float* dy_out) {
 	const float dx = px - mean[0];
 	const float dy = py - mean[1];
-	const float m = dx * (conic[0] * dx + conic[1] * dy) + dy * (conic[1] * dx + conic[2] * dy);
-	const float G = expf(-0.5f * m);
-	*gauss = G;
 	*dx_out = dx;
 	*dy_out = dy;
-	return opacity * G;
+	return hds_gauss_alpha(dx, dy, conic[0], conic[1], conic[2], opacity, gauss);
 }
 
 /*
@@ -385,8 +390,9 @@ static inline float orc_alpha(float px, float py, const float* mean, const float
  */
 /*
  * near_cut (optional, [H, W] bytes) marks the pixels whose walk passed a decision within rounding
- * distance of its cut, where an implementation that rounds differently (a GPU's hardware exp2 and
- * fused multiply-adds against libm's expf and separate products here) can decide the other way:
+ * distance of its cut, where an implementation that rounds differently (another exp, other fused
+ * multiply-adds; the HIP kernels share this file's alpha arithmetic and decide identically) could
+ * decide the other way:
  *   - a raw alpha against 1/255: alpha = op exp(-m / 2) is uncertain by a relative
  *     eps_a = u (2 (|a dx^2| + 2 |b dx dy| + |c dy^2|) + m / 2 + 4), u = 2^-24: a few roundings of
  *     the quadratic form's terms (which can cancel) carried through exp, the rounding of exp's
@@ -440,9 +446,9 @@ ORC_EXPORT void orc_render_forward(int width, int height, const int32_t* tile_ra
 						if (test_T < HDS_MIN_TRANSMITTANCE) break;
 						const float w = alpha * T;
 						if (colors) {
-							r += w * colors[gid * 3 + 0];
-							g += w * colors[gid * 3 + 1];
-							b += w * colors[gid * 3 + 2];
+							r = fmaf(w, colors[gid * 3 + 0], r);
+							g = fmaf(w, colors[gid * 3 + 1], g);
+							b = fmaf(w, colors[gid * 3 + 2], b);
 						}
 						const float* f = features ? features + (int64_t)gid * channels : NULL;
 						for (int c = 0; c < channels && f; c++) acc[c] += w * f[c];
@@ -451,9 +457,9 @@ ORC_EXPORT void orc_render_forward(int width, int height, const int32_t* tile_ra
 					}
 					const int64_t pix = (int64_t)y * width + x;
 					if (image) {
-						image[pix * 3 + 0] = r + T * background[0];
-						image[pix * 3 + 1] = g + T * background[1];
-						image[pix * 3 + 2] = b + T * background[2];
+						image[pix * 3 + 0] = fmaf(T, background[0], r);
+						image[pix * 3 + 1] = fmaf(T, background[1], g);
+						image[pix * 3 + 2] = fmaf(T, background[2], b);
 					}
 					if (final_T) final_T[pix] = T;
 					if (n_contrib) n_contrib[pix] = last;

@@ -74,6 +74,22 @@ def test_logf_is_within_two_ulp_of_float64_log():
     assert oracle.logf(0.0) == -np.inf and np.isnan(oracle.logf(-1.0)) and oracle.logf(np.inf) == np.inf
 
 
+def test_exp2f_is_within_one_ulp_of_float64_exp2():
+    """hds_exp2f, behind every blend alpha on both CPU and GPU: at most one ulp from 2^x in double over
+    the range where alpha can reach 1/255 and far beyond, exact at the integers, 0 below 2^-150."""
+    rng = np.random.default_rng(4)
+    xs = np.concatenate([np.linspace(-30.0, 0.5, 300001), rng.uniform(-126, 10, 100000),
+                         -np.arange(0, 126), [-0.5, 0.5, -1e-7, 1e-7]]).astype(np.float32)
+    got = oracle.exp2f(xs).astype(np.float64)
+    want = np.exp2(xs.astype(np.float64))
+    ulp = np.spacing(want.astype(np.float32)).astype(np.float64)
+    err = np.abs(got - want) / ulp
+    assert err.max() <= 1.0, f"max error {err.max():.2f} ulp at {xs[err.argmax()]}"
+    ints = -np.arange(0, 126, dtype=np.float32)
+    assert np.array_equal(oracle.exp2f(ints), np.exp2(ints.astype(np.float64)).astype(np.float32))
+    assert oracle.exp2f(np.array([-151.0, -1e30, np.nan], np.float32)).tolist() == [0.0, 0.0, 0.0]
+
+
 def test_tile_rect_covers_every_pixel_the_gaussian_can_reach():
     """Brute force in float64: a pixel with alpha >= 1/255 (a little margin) is always inside the rect."""
     rng = np.random.default_rng(1)
