@@ -552,6 +552,30 @@ def test_block_cull_keeps_every_contributor(seed):
     assert_grads_close(("means2D", "conics", "colors", "opacities", "features"), got, want)
 
 
+def test_kernel_profile_records_only_the_named_kernels():
+    """hds_profile_begin_only: with kernel names given, only those launches get timing events (what
+    bench.py relies on inside its timed region); without, every hot-path launch does."""
+    from gaussian_splatting.rasterizer._native import KernelProfile
+
+    width, height = 64, 48
+    inputs = scene(0, 800, width, height)
+    features = torch.rand(800, 32, generator=torch.Generator().manual_seed(2)).to(DEV).requires_grad_(True)
+
+    def step():
+        image, fimg = rasterize(*inputs, width, height, features=features)
+        torch.autograd.backward((image, fimg), (torch.ones_like(image), torch.ones_like(fimg)))
+        torch.cuda.synchronize()
+
+    step()
+    with KernelProfile(only=("backward_geometry_kernel", "backward_features_kernel")) as only:
+        step()
+    with KernelProfile() as every:
+        step()
+    assert set(only.summary()) == {"backward_geometry_kernel", "backward_features_kernel"}
+    assert {"render_forward_kernel", "backward_geometry_kernel", "backward_features_kernel"} <= set(every.summary())
+    assert all(v["mean_ms"] > 0 for v in only.summary().values())
+
+
 def test_unsupported_feature_width_is_rejected():
     inputs = scene(0, 100, 32, 32)
     with pytest.raises(RuntimeError, match="32, 64, 128, 256 or 512"):
