@@ -12,7 +12,10 @@ Prints ONE JSON line: the metric (ms per fwd+bwd, lower is better), the fwd / bw
 harness way (events around each sample, a pause after each, median; bench/harness.py:130-153), per-stage
 HIP-event timings taken inside the timed region, the roofline of the dominant kernel (render_backward)
 against MI355X HBM (8 TB/s), a CPU baseline: the oracle (oracle/hds_oracle.c, OpenMP) running the same
-frame on this host, and the environment (GPU, clocks and power from amd-smi, source digest).
+frame on this host, and the environment (GPU, clocks and power from amd-smi, source digest). After the
+headline it times, on the same GPU, the channel sweep (C = 32, 64, 256, 512 on the
+headline scene) and configs 0, 1 and 4 (their step, fwd / bwd split, blend backward span and per-stage
+means), reported under 'channel_sweep' and 'other_configs'.
 
 Like the reference harness, which times only what agrees with its comparison (harness.py:196-208), it
 first checks one fwd+bwd step of this frame against the oracle (images and every leaf gradient within
@@ -71,6 +74,10 @@ def parse_args():
                          "includes the loss, none otherwise")
     ap.add_argument("--bwd-slice", type=int, default=None,
                     help="channels per backward work-group (gaussian_splatting.rasterizer.FEATURE_SLICE_WIDTH)")
+    ap.add_argument("--configs", default="auto",
+                    help="comma-separated other BASELINE configs timed after the headline on the same GPU (step, "
+                         "fwd / bwd split, blend backward span, per-stage ms) and reported under 'other_configs'; "
+                         "'auto' = 0,1,4 for config 2 (none under a profiler), none otherwise; 'none' skips them")
     ap.add_argument("--sweep", default="auto",
                     help="comma-separated channel counts of BASELINE config 3 timed after the headline on the same "
                          "scene (fwd / bwd ms, backward roofline) and reported under 'channel_sweep'; 'auto' = "
@@ -116,6 +123,90 @@ def algorithmic_bytes(n: int, n_vis: int, pairs: int, hw: int, c: int) -> dict[s
     }
 
 
+class Frame:
+    """One frame as the timed step runs it (bench/harness.py:33-66, 157-177): the leaves (means,
+    scales, quats, opacities, colours evaluated once from SH under no_grad, features), dL/dimage and
+    dL/dfeature_image ~ U[0, 1], and the step's closures: normalize(quats) -> project_gaussians ->
+    rasterize, then autograd backward, of 0.8 L1 + 0.2 (1 - SSIM) against the U[0, 1] image
+    (main.py:179-182) when loss_mode is "l1-ssim", else of the upstream gradients."""
+
+    def __init__(self, wl, dev, loss_mode: str, rgb_only: bool = False, frozen_features: bool = False):
+        import torch
+
+        from gaussian_splatting.rasterizer import project_gaussians
+        from gaussian_splatting.utils.sh import eval_sh
+        from tests.scenes import upstream, view_dirs
+
+        self.wl, self.rgb_only = wl, rgb_only
+        cam = wl.cam
+        wl_dev = wl.to(dev)
+        self.w2c = wl_dev.world_to_camera.contiguous()
+        with torch.no_grad():
+            _, _, radii0, _ = project_gaussians(wl_dev.means, wl_dev.scales, wl_dev.quats, wl_dev.opacities, self.w2c,
+                                                cam["fx"], cam["fy"], cam["cx"], cam["cy"], wl.width, wl.height)
+            self.colors = eval_sh(wl_dev.sh_dc, wl_dev.sh_rest, view_dirs(wl_dev.means, wl_dev.center), wl.sh_degree,
+                                  radii0, None)
+        self.leaves = {
+            "means": wl_dev.means.clone().requires_grad_(True),
+            "scales": wl_dev.scales.clone().requires_grad_(True),
+            "quats": wl_dev.quats.clone().requires_grad_(True),
+            "opacities": wl_dev.opacities[:, 0].clone().requires_grad_(True),
+            "colors": self.colors.clone().requires_grad_(True),
+            "features": wl_dev.features.clone().requires_grad_(not frozen_features),
+        }
+        if rgb_only:
+            del self.leaves["features"]
+        self.grad_image, self.grad_features = upstream(2, wl.height, wl.width, wl.channels, device=dev)
+        self.target = self.grad_image if loss_mode == "l1-ssim" else None
+        self.state = {}
+
+    def forward(self, retain: bool = False) -> None:
+        import torch.nn.functional as F
+
+        from gaussian_splatting.rasterizer import project_gaussians, rasterize
+
+        leaves, cam, W, H = self.leaves, self.wl.cam, self.wl.width, self.wl.height
+        means2D, depths, radii, conics = project_gaussians(
+            leaves["means"], leaves["scales"], F.normalize(leaves["quats"], dim=-1), leaves["opacities"][:, None],
+            self.w2c, cam["fx"], cam["fy"], cam["cx"], cam["cy"], W, H)
+        if retain:
+            # The rasterizer's own gradients (the agreement gate compares each stage on its inputs).
+            means2D.retain_grad()
+            conics.retain_grad()
+            self.state["means2D"], self.state["conics"] = means2D, conics
+            self.state["projected"] = (means2D, depths, radii, conics)
+        self.state["out"] = rasterize(means2D, depths, radii, conics, leaves["colors"], leaves["opacities"][:, None],
+                                      W, H, features=leaves.get("features"))
+
+    def backward(self) -> None:
+        import torch
+
+        from gaussian_splatting.utils.loss import l1_loss, ssim
+
+        out = self.state["out"]
+        image = out if self.rgb_only else out[0]
+        if self.target is not None:
+            # main.py:179-182: 0.8 L1 + 0.2 (1 - SSIM), the SSIM on the fused HIP kernels.
+            loss = 0.8 * l1_loss(image, self.target) + 0.2 * (1.0 - ssim(image, self.target))
+            if self.rgb_only:
+                loss.backward()
+            else:
+                torch.autograd.backward([loss, out[1]], [None, self.grad_features])
+        elif self.rgb_only:
+            torch.autograd.backward(out, self.grad_image)
+        else:
+            torch.autograd.backward(out, [self.grad_image, self.grad_features])
+
+    def reset(self) -> None:
+        for leaf in self.leaves.values():
+            leaf.grad = None
+
+    def step(self) -> None:
+        self.reset()
+        self.forward()
+        self.backward()
+
+
 def main() -> int:
     args = parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -125,15 +216,12 @@ def main() -> int:
               file=sys.stderr)
         return 2
 
-    import numpy as np
     import torch
     import torch.nn.functional as F
 
-    from gaussian_splatting.rasterizer import _get_rasterizer, project_gaussians, rasterize
+    from gaussian_splatting.rasterizer import _get_rasterizer, project_gaussians
     from gaussian_splatting.rasterizer._native import KernelProfile, StageTimer
-    from gaussian_splatting.utils.loss import l1_loss, ssim
-    from gaussian_splatting.utils.sh import eval_sh
-    from tests.scenes import synthetic_config, upstream, view_dirs
+    from tests.scenes import synthetic_config
 
     if not torch.cuda.is_available():
         print("bench.py needs a HIP GPU", file=sys.stderr)
@@ -147,67 +235,13 @@ def main() -> int:
     cam = wl.cam
     W, H, C, N = wl.width, wl.height, wl.channels, wl.n
     print(f"[bench] {wl.name}: N={N} {W}x{H} C={C}", file=sys.stderr, flush=True)
-    wl_dev = wl.to(dev)
-    w2c = wl_dev.world_to_camera.contiguous()
-
-    # Colours are a leaf computed once under no_grad, as in bench/harness.py:33-56.
-    with torch.no_grad():
-        _, _, radii0, _ = project_gaussians(wl_dev.means, wl_dev.scales, wl_dev.quats, wl_dev.opacities, w2c,
-                                            cam["fx"], cam["fy"], cam["cx"], cam["cy"], W, H)
-        colors = eval_sh(wl_dev.sh_dc, wl_dev.sh_rest, view_dirs(wl_dev.means, wl_dev.center), wl.sh_degree,
-                         radii0, None)
-    leaves = {
-        "means": wl_dev.means.clone().requires_grad_(True),
-        "scales": wl_dev.scales.clone().requires_grad_(True),
-        "quats": wl_dev.quats.clone().requires_grad_(True),
-        "opacities": wl_dev.opacities[:, 0].clone().requires_grad_(True),
-        "colors": colors.clone().requires_grad_(True),
-        "features": wl_dev.features.clone().requires_grad_(not args.frozen_features),
-    }
-    if args.rgb_only:
-        del leaves["features"]
-    grad_image, grad_features = upstream(2, H, W, C, device=dev)
-    # With the loss, the U[0, 1] image drawn above is the target and dL/dimage comes from the loss.
+    # With the loss, the U[0, 1] image drawn as dL/dimage is the target and dL/dimage comes from the loss.
     loss_mode = args.loss if args.loss != "auto" else ("l1-ssim" if args.config in (0, 4) and args.checkpoint is None
                                                         else "none")
-    target = grad_image if loss_mode == "l1-ssim" else None
-    state = {}
-
-    def forward(retain=False):
-        means2D, depths, radii, conics = project_gaussians(
-            leaves["means"], leaves["scales"], F.normalize(leaves["quats"], dim=-1), leaves["opacities"][:, None],
-            w2c, cam["fx"], cam["fy"], cam["cx"], cam["cy"], W, H)
-        if retain:
-            # The rasterizer's own gradients (the agreement gate compares each stage on its inputs).
-            means2D.retain_grad()
-            conics.retain_grad()
-            state["means2D"], state["conics"] = means2D, conics
-            state["projected"] = (means2D, depths, radii, conics)
-        state["out"] = rasterize(means2D, depths, radii, conics, leaves["colors"], leaves["opacities"][:, None],
-                                 W, H, features=leaves.get("features"))
-
-    def backward():
-        image = state["out"] if args.rgb_only else state["out"][0]
-        if target is not None:
-            # main.py:179-182: 0.8 L1 + 0.2 (1 - SSIM), the SSIM on the fused HIP kernels.
-            loss = 0.8 * l1_loss(image, target) + 0.2 * (1.0 - ssim(image, target))
-            if args.rgb_only:
-                loss.backward()
-            else:
-                torch.autograd.backward([loss, state["out"][1]], [None, grad_features])
-        elif args.rgb_only:
-            torch.autograd.backward(state["out"], grad_image)
-        else:
-            torch.autograd.backward(state["out"], [grad_image, grad_features])
-
-    def reset():
-        for leaf in leaves.values():
-            leaf.grad = None
-
-    def step():
-        reset()
-        forward()
-        backward()
+    frame = Frame(wl, dev, loss_mode, rgb_only=args.rgb_only, frozen_features=args.frozen_features)
+    leaves, state, w2c = frame.leaves, frame.state, frame.w2c
+    colors, grad_image, grad_features, target = frame.colors, frame.grad_image, frame.grad_features, frame.target
+    forward, backward, reset, step = frame.forward, frame.backward, frame.reset, frame.step
 
     if args.bwd_slice:
         import gaussian_splatting.rasterizer as rasterizer_module
@@ -326,8 +360,18 @@ def main() -> int:
         leaves.pop("features", None)
         state.clear()
         del grad_features
+        frame.grad_features = None
         torch.cuda.empty_cache()
         channel_sweep = measure_sweep(wl, leaves, w2c, sweep_channels, n_vis, pairs, args)
+
+    # Under a profiler "auto" times no other config, so a trace or counter run covers the headline only.
+    other = ([0, 1, 4] if args.config == 2 and args.checkpoint is None and not args.rgb_only
+             and not args.frozen_features and not _profiled() else []) if args.configs == "auto" else (
+        [] if args.configs == "none" else [int(c) for c in args.configs.split(",")])
+    other_configs = None
+    if other:
+        torch.cuda.empty_cache()
+        other_configs = [measure_config(index, args) for index in other]
 
     line = {
         "metric": METRIC, "value": round(ms_per_step, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps,
@@ -342,7 +386,8 @@ def main() -> int:
         "step_hbm_frac": round(step_frac, 4), "step_algorithmic_MB": round(total_alg / 1e6, 1),
         "roofline": roofline, "breakdown_steps": args.breakdown_steps, "stages": stage_report,
         "kernels": kernel_report, "cpu_baseline": cpu,
-        "agreement": agreement, "channel_sweep": channel_sweep, "environment": environment(),
+        "agreement": agreement, "channel_sweep": channel_sweep, "other_configs": other_configs,
+        "environment": environment(),
     }
     print(json.dumps(line), flush=True)
     if args.calibrate_copy_mib > 0:
@@ -460,6 +505,69 @@ def measure_sweep(wl, leaves: dict, w2c, channels_list, n_vis: int, pairs: int, 
                     "render_backward_GBs": round(gbs, 1), "render_backward_hbm_frac": round(gbs / HBM_PEAK_GBS, 4)})
         del feats, grad_image, grad_features, holder
         torch.cuda.empty_cache()
+    return out
+
+
+def measure_config(index: int, args) -> dict:
+    """Another BASELINE config on the same GPU after the headline (0, 1 and 4 by default): its fwd+bwd
+    step as the headline's runs (with the 0.8 L1 + 0.2 (1 - SSIM) loss for configs 0 and 4, whose
+    BASELINE definition includes it), timed the same way, the harness fwd / bwd split, the blend
+    backward's span and HBM fraction, and the per-stage means of a short breakdown pass. It has no
+    oracle gate of its own: the -m gpu tests compare these configs with the oracle."""
+    import torch
+
+    from gaussian_splatting.rasterizer import _get_rasterizer
+    from gaussian_splatting.rasterizer._native import KernelProfile, StageTimer
+    from tests.scenes import synthetic_config
+
+    dev = torch.device("cuda:0")
+    wl = synthetic_config(index)
+    print(f"[bench] config {index}: {wl.name}", file=sys.stderr, flush=True)
+    frame = Frame(wl, dev, "l1-ssim" if index in (0, 4) else "none")
+    for _ in range(3):
+        frame.step()
+    steps = min(args.steps, 20)
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    torch.cuda.synchronize()
+    with KernelProfile(only=BACKWARD_KERNELS) as kprof:
+        for start, end in events:
+            start.record()
+            frame.step()
+            end.record()
+        torch.cuda.synchronize()
+    step_ms = [s.elapsed_time(e) for s, e in events]
+    _, bwd_ms = backward_span(kprof.summary(), kprof.timeline)
+    ext = _get_rasterizer()
+    timer = StageTimer()
+    ext.timer = timer
+    for _ in range(5):
+        frame.step()
+    ext.timer = None
+    stages = {name: round(row["mean_ms"], 4) for name, row in timer.summary().items()}
+    split = harness_split(frame.forward, frame.backward, frame.reset, min(args.steps, 10))
+    # Visible gaussians and pairs of this frame, for the backward's algorithmic bytes.
+    import torch.nn.functional as F
+
+    from gaussian_splatting.rasterizer import project_gaussians
+
+    with torch.no_grad():
+        lv, cam = frame.leaves, wl.cam
+        m2, d, r, c = project_gaussians(lv["means"], lv["scales"], F.normalize(lv["quats"], dim=-1),
+                                        lv["opacities"][:, None], frame.w2c, cam["fx"], cam["fy"], cam["cx"],
+                                        cam["cy"], wl.width, wl.height)
+        n_vis = int((r > 0).sum())
+        pairs = int(ext.bin(m2, d, r, c, None, lv["opacities"][:, None], wl.width, wl.height)[0].numel())
+    alg = algorithmic_bytes(wl.n, n_vis, pairs, wl.width * wl.height, wl.channels)["render_backward"]
+    gbs = alg / (bwd_ms * 1e-3) / 1e9
+    out = {"config": index, "workload": wl.name, "gaussians": wl.n, "width": wl.width, "height": wl.height,
+           "channels": wl.channels, "visible": n_vis, "pairs": pairs,
+           "loss": "0.8 L1 + 0.2 (1 - SSIM)" if frame.target is not None else "none (dL/dimage U[0, 1])",
+           "step_ms_median": round(statistics.median(step_ms), 4), "fwd_ms_median": split["fwd_ms_median"],
+           "bwd_ms_median": split["bwd_ms_median"], "render_backward_ms": round(bwd_ms, 4),
+           "render_backward_GBs": round(gbs, 1), "render_backward_hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+           "stages_ms": stages}
+    del frame
+    torch.cuda.empty_cache()
     return out
 
 
