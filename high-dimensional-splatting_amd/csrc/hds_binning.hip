@@ -202,11 +202,10 @@ __device__ inline uint32_t block_exclusive_scan(uint32_t v, uint32_t* s_wave, ui
 }
 
 // Lanes of this wave (among `active`) whose digit equals ours.
-__device__ inline uint64_t match_digit(uint32_t d, uint64_t active, int bits = kRadixBits) {
+__device__ inline uint64_t match_digit(uint32_t d, uint64_t active) {
 	uint64_t peers = active;
 #pragma unroll
 	for (int b = 0; b < kRadixBits; b++) {
-		if (b >= bits) break;
 		const bool bit = (d >> b) & 1u;
 		const uint64_t m = hds_ballot(bit);
 		peers &= bit ? m : ~m;
@@ -214,16 +213,12 @@ __device__ inline uint64_t match_digit(uint32_t d, uint64_t active, int bits = k
 	return peers;
 }
 
-// Adds this row's keys (lanes in `active`) to the work-group's LDS digit histograms, one per pass.
-__device__ inline void count_digits(uint32_t key, bool valid, int passes, uint32_t (*s_hist)[kRadix],
-								 int key_bits = 32) {
-	const uint64_t active = hds_ballot(valid);
-	if (active == 0) return;
-	for (int p = 0; p < passes; p++) {
-		const uint32_t d = (key >> (p * kRadixBits)) & (kRadix - 1);
-		const uint64_t peers = match_digit(d, active, key_bits - p * kRadixBits);
-		if (valid && hds_rank_below(peers) == 0) atomicAdd(&s_hist[p][d], (uint32_t)__popcll(peers));
-	}
+// Adds a valid key to the work-group's LDS digit histograms, one per pass: one LDS atomic per lane
+// and pass. Lanes that share a digit serialise in the LDS, which still costs less than grouping them
+// with ballots first (measured on the depth keys and on the tile keys of the stress scene).
+__device__ inline void count_digits(uint32_t key, bool valid, int passes, uint32_t (*s_hist)[kRadix]) {
+	if (!valid) return;
+	for (int p = 0; p < passes; p++) atomicAdd(&s_hist[p][(key >> (p * kRadixBits)) & (kRadix - 1)], 1u);
 }
 
 // hist = [pass][kHistCopies][kRadix]; this work-group adds into copy blockIdx.x % kHistCopies.
@@ -543,7 +538,7 @@ __global__ __launch_bounds__(kThreads) void emit_kernel(int64_t n, int64_t num_p
 														 const uint32_t* __restrict__ offsets,
 														 const uint32_t* __restrict__ order,
 														 const uint2* __restrict__ rects_sorted, int tiles_x,
-														 int passes, int key_bits, uint32_t* __restrict__ tile_keys,
+														 int passes, uint32_t* __restrict__ tile_keys,
 														 uint32_t* __restrict__ gids, uint32_t* __restrict__ hist) {
 	__shared__ uint32_t s_off[kWaves][HDS_WAVE];
 	__shared__ uint32_t s_hist[kMaxPasses][kRadix];
@@ -596,7 +591,7 @@ __global__ __launch_bounds__(kThreads) void emit_kernel(int64_t n, int64_t num_p
 			tile_keys[p] = key;
 			gids[p] = jgid;
 		}
-		count_digits(key, valid_pair, passes, s_hist, key_bits);
+		count_digits(key, valid_pair, passes, s_hist);
 	}
 	flush_digits(passes, s_hist, hist);
 }
@@ -859,7 +854,7 @@ int bin_emit_launch(int64_t n, int64_t num_pairs, bool exact, int width, int hei
 	HDS_LAUNCH_CHECK("zero_sort_control", s);
 	HdsKernelTimer timer2("emit_kernel", s);
 	emit_kernel<<<hds_blocks(n, kThreads), kThreads, 0, s>>>(n, num_pairs, total, offsets, order, rects_sorted,
-																	tiles_x, passes, tile_bits(num_tiles), keys_a, vals_a, ctrl->hist);
+																	tiles_x, passes, keys_a, vals_a, ctrl->hist);
 	timer2.stop();
 	HDS_LAUNCH_CHECK("emit_pairs", s);
 	int st = onesweep_sort(keys_a, vals_a, keys_b, vals_b, num_pairs, total, passes, ctrl->hist, status,
