@@ -885,3 +885,17 @@ int render_backward(bool zero_outputs, int64_t n, int width, int height, int cha
 extern "C" int hds_render_backward(HDS_BACKWARD_ARGS) { return render_backward(true, HDS_BACKWARD_PASS); }
 
 extern "C" int hds_render_backward_accumulate(HDS_BACKWARD_ARGS) { return render_backward(false, HDS_BACKWARD_PASS); }
+
+extern "C" int hds_zero_async(float* p, int64_t count, int max_workgroups, hds_stream_t stream) {
+	HDS_REQUIRE(count >= 0 && max_workgroups >= 0, "zero_async: negative count or work-group limit");
+	if (count == 0) return HDS_OK;
+	HDS_REQUIRE(p && aligned16(p) && count % 4 == 0, "zero_async: needs a 16-byte aligned range of a multiple of 4 floats");
+	const int64_t count4 = count / 4;
+	int64_t blocks = std::min<int64_t>(hds_blocks(count4, 256), 8192);
+	if (max_workgroups > 0) blocks = std::min<int64_t>(blocks, max_workgroups);
+	hipStream_t s = (hipStream_t)stream;
+	HdsKernelTimer timer("zero4_kernel", s);
+	zero4_kernel<<<(unsigned)blocks, 256, 0, s>>>(reinterpret_cast<float4*>(p), count4);
+	timer.stop();
+	return hds_check_launch("zero_async", s);
+}

@@ -14,7 +14,7 @@ from typing import Any
 
 import torch
 
-from gaussian_splatting.rasterizer._native import HipRasterizer, default_slice_width
+from gaussian_splatting.rasterizer._native import HipRasterizer, black_background, default_slice_width
 from gaussian_splatting.rasterizer.projection import project_gaussians  # noqa: F401
 
 _rasterizer_module: Any | None = None
@@ -149,7 +149,7 @@ def rasterize(
     assert conics.shape == (n, 3) and colors.shape == (n, 3)
     assert opacities.shape == (n, 1)
     if background is None:
-        background = torch.zeros(3, device=means2D.device, dtype=means2D.dtype)
+        background = black_background(means2D.device) if means2D.is_cuda else torch.zeros(3, dtype=means2D.dtype)
     assert background.shape == (3,)
     assert features is None or (features.ndim == 2 and features.shape[0] == n)
     return RasterizeGaussians.apply(means2D, depths, radii, conics, colors, opacities, background, features,

@@ -33,6 +33,7 @@ _CAMERA = [_f32, _f32, _f32, _f32, _i32, _i32, _f32, _f32, _f32]
 PROTOTYPES = {
     "hds_last_error": (ctypes.c_char_p, []),
     "hds_abi_version": (_i32, []),
+    "hds_zero_async": (_i32, [_vp, _i64, _i32, _vp]),
     "hds_project_gaussians": (_i32, [_i64, _vp, _vp, _vp, _vp, _vp] + _CAMERA + [_vp, _vp, _vp, _vp, _vp]),
     "hds_project_gaussians_backward": (_i32, [_i64, _vp, _vp, _vp, _vp, _vp, _vp] + _CAMERA + [_vp, _vp, _vp, _vp]),
     "hds_eval_sh": (_i32, [_i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
@@ -141,6 +142,20 @@ def _stream(device: torch.device):
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
 
+_BLACK: dict[int, torch.Tensor] = {}
+
+
+def black_background(device: torch.device) -> torch.Tensor:
+    """The default background (0, 0, 0) on `device`, made once per device: a fresh torch.zeros(3) in
+    every call was one more fill kernel in every step. Read-only: nothing writes it."""
+    index = torch.device(device).index
+    index = torch.cuda.current_device() if index is None else index
+    black = _BLACK.get(index)
+    if black is None:
+        black = _BLACK[index] = torch.zeros(3, device=torch.device("cuda", index), dtype=torch.float32)
+    return black
+
+
 def _dev(t: torch.Tensor, name: str) -> torch.Tensor:
     """The reference's TORCH_CHECK(is_cuda / is_contiguous), plus float32 and 16-byte alignment."""
     if not t.is_cuda:
@@ -235,6 +250,8 @@ class HipRasterizer:
         self.timer: StageTimer | None = None
         self._pair_capacity: dict[int, int] = {}
         self._zero_streams: dict[int, torch.cuda.Stream] = {}
+        # Work-groups of the pre-zeroing fill beside the binning (0: as many as fill the device).
+        self.zero_fill_workgroups = 0
 
     def prezeroed_gradients(self, n: int, channels: int, device: torch.device):
         """Zeroed output buffers for a later render_backward (grad_means2D [N,2], grad_conics [N,3],
@@ -246,14 +263,20 @@ class HipRasterizer:
         side = self._zero_streams.get(device.index)
         if side is None:
             side = self._zero_streams[device.index] = torch.cuda.Stream(device=device)
-        f32 = dict(device=device, dtype=torch.float32)
-        buffers = (torch.empty((n, 2), **f32), torch.empty((n, 3), **f32), torch.empty((n, 3), **f32),
-                   torch.empty((n, 1), **f32), torch.empty((n, channels), **f32))
+        # One allocation for the five buffers, each view starting on a 256-byte boundary, cleared by
+        # one fill that takes at most zero_fill_workgroups work-groups, so the binning's small
+        # kernels beside it keep most of the CUs.
+        shapes = ((n, 2), (n, 3), (n, 3), (n, 1), (n, channels))
+        offsets, total = [], 0
+        for shape in shapes:
+            offsets.append(total)
+            total += (math.prod(shape) + 63) // 64 * 64
+        storage = torch.empty((total,), device=device, dtype=torch.float32)
+        buffers = tuple(storage[o:o + math.prod(shape)].view(shape) for o, shape in zip(offsets, shapes))
         side.wait_stream(current)
-        with torch.cuda.stream(side):
-            torch._foreach_zero_(list(buffers))
-            for b in buffers:
-                b.record_stream(side)
+        with torch.cuda.device(device), torch.cuda.stream(side):
+            _check(self.lib.hds_zero_async(_ptr(storage), total, self.zero_fill_workgroups, _stream(device)))
+            storage.record_stream(side)
             event = torch.cuda.Event()
             event.record(side)
         return buffers, event
@@ -474,7 +497,7 @@ class HipRasterizer:
         final_T = torch.empty((height, width), device=dev, dtype=torch.float32)
         n_contrib = torch.empty((height, width), device=dev, dtype=torch.int32)
         if rgb and background is None:
-            background = torch.zeros(3, device=dev, dtype=torch.float32)
+            background = black_background(dev)
         with torch.cuda.device(dev):
             self._run("render", lambda: self.lib.hds_render(
                 means2D.shape[0], width, height, channels, _ptr(tile_ranges), _ptr(values_sorted),
@@ -504,7 +527,7 @@ class HipRasterizer:
         if grad_image is not None:
             grad_image = _dev(grad_image, "grad_image")
             if background is None:
-                background = torch.zeros(3, device=dev, dtype=torch.float32)
+                background = black_background(dev)
         want_feat = features is not None and want_feature_grad
         if prezeroed is not None:
             (g_means, g_conics, g_colors, g_opac, g_feat), event = prezeroed

@@ -210,6 +210,13 @@ HDS_API int hds_render_backward_accumulate(
 	const float* grad_image, const float* features, const float* grad_feature_image, float* grad_means2D,
 	float* grad_conics, float* grad_colors, float* grad_opacities, float* grad_features, hds_stream_t stream);
 
+/* Zeroes `count` floats at p (16-byte aligned, count a multiple of 4) on `stream` with at most
+ * `max_workgroups` work-groups of 256 threads (0: as many as fill the device), so that a large fill
+ * enqueued beside latency-bound kernels takes only part of the CUs. The zero-initialised buffers of
+ * hds_render_backward_accumulate; the reference zeroes its gradient outputs where it allocates them
+ * (torch::zeros in backward.cu:166-226, features.cu:561-616). */
+HDS_API int hds_zero_async(float* p, int64_t count, int max_workgroups, hds_stream_t stream);
+
 /* ---- SSIM: replaces ssim_forward / ssim_backward ------------------------------------------- */
 
 /* ssim.cu:116-148. rendered, gt [H,W,3] -> ssim_map, d_mu, d_aa, d_ab [H,W,3]. */
