@@ -50,3 +50,21 @@ def test_bench_times_a_checkpoint_frame_that_agrees_with_the_oracle(tmp_path, mo
     assert cfg["workload"].startswith("checkpoint-model-turned")
     assert 0 < cfg["visible"] <= n and cfg["pairs"] > 0
     assert line["value"] > 0
+
+
+def test_bench_times_another_config_with_its_loss():
+    """bench.py's other-config pass (configs 0, 1 and 4 after the headline): config 0 runs its step with
+    the L1 + SSIM loss and reports the step, the harness split, the blend backward and the stages."""
+    import argparse
+
+    import bench
+
+    print("[test] bench.measure_config(0)", file=sys.stderr, flush=True)
+    out = bench.measure_config(0, argparse.Namespace(steps=3))
+    assert out["config"] == 0 and out["workload"].startswith("cpu-plumbing-10k")
+    assert out["loss"].startswith("0.8 L1")
+    assert out["gaussians"] == 10_000 and out["channels"] == 32
+    assert 0 < out["visible"] <= out["gaussians"] and out["pairs"] > 0
+    for key in ("step_ms_median", "fwd_ms_median", "bwd_ms_median", "render_backward_ms"):
+        assert out[key] > 0, key
+    assert {"bin_count", "bin_emit", "render", "render_backward", "ssim_forward", "ssim_backward"} <= set(out["stages_ms"])
