@@ -97,6 +97,14 @@ def test_bad_slice_width_is_rejected_before_launch(lib):
     assert status == 1 and b"slices of 48" in lib.hds_last_error()
 
 
+def test_zero_fill_rejects_bad_ranges_before_launch(lib):
+    assert lib.hds_zero_async(None, -4, 0, None) == 1 and b"negative" in lib.hds_last_error()
+    assert lib.hds_zero_async(ctypes.c_void_p(16), 8, -1, None) == 1 and b"negative" in lib.hds_last_error()
+    assert lib.hds_zero_async(ctypes.c_void_p(20), 8, 0, None) == 1 and b"16-byte aligned" in lib.hds_last_error()
+    assert lib.hds_zero_async(ctypes.c_void_p(16), 6, 0, None) == 1 and b"multiple of 4" in lib.hds_last_error()
+    assert lib.hds_zero_async(None, 0, 0, None) == 0  # nothing to clear, nothing enqueued
+
+
 def test_bad_image_size_and_sh_degree_are_rejected(lib):
     status = lib.hds_eval_sh(10, 4, None, None, None, None, None, None)
     assert status == 1 and b"degree 4" in lib.hds_last_error()

@@ -6,6 +6,7 @@ tolerances (test_render.py:29-58: RGB max 2e-3 / p99 1e-4, features max 1e-3 / p
 within assert_grads_close (rtol 1e-3, atol 1e-4 * max|want|, < 0.1% outside, max error 2e-3 * max).
 """
 import math
+import sys
 
 import numpy as np
 import pytest
@@ -292,6 +293,22 @@ def test_gradient_buffers_are_zeroed_ahead_only_when_a_graph_is_recorded(monkeyp
                               slice_width=32)[4]
     scale = own.abs().max().item()
     assert (ahead - own).abs().max().item() <= 1e-5 * scale
+
+
+@pytest.mark.parametrize("workgroups", [0, 3])
+def test_zero_fill_clears_exactly_its_range(workgroups):
+    """hds_zero_async (the pre-zeroed gradients' fill) clears count floats from p, with as many
+    work-groups as fill the device or only three (each then strides over the range), and nothing past
+    it."""
+    from gaussian_splatting.rasterizer._native import _ptr, _stream, load_library
+
+    lib = load_library()
+    buf = torch.full((1_000_064,), 7.0, device=DEV)
+    print(f"[test] zero fill, {workgroups} work-groups", file=sys.stderr, flush=True)
+    assert lib.hds_zero_async(_ptr(buf), 1_000_000, workgroups, _stream(buf.device)) == 0
+    torch.cuda.synchronize()
+    assert int((buf[:1_000_000] != 0).sum()) == 0
+    assert bool((buf[1_000_000:] == 7.0).all())
 
 
 def test_rasterize_is_identical_with_and_without_the_pair_count_read():
