@@ -8,6 +8,7 @@
 // gradient where Adam consumes it (eval_sh_backward_adam_kernel). The basis constants are the real
 // SH of the 3DGS convention, sh.cu:9-15 / test_sh.py:27-47.
 #include "hds_internal.h"
+#include "hds_stage.h"
 #include "hds_rasterizer.h"
 
 namespace {
@@ -47,20 +48,50 @@ __device__ inline float sh_weight(const float* dc, const float* rest, int j, int
 }
 
 constexpr int kShEvalBlock = 256;
+constexpr int kShRestRow = 45;  // floats of sh_rest per gaussian (15 coefficients x 3 channels)
+
+// Copies the run of count consecutive 45-float sh_rest rows that starts at src into LDS and waits
+// for it (and for every earlier vector-memory read of the calling wave); the caller's barrier then
+// publishes it. When src is 16-byte aligned (a work-group's run is count * 180 bytes, so a
+// 256-gaussian run starts aligned when the tensor does) the run goes HBM -> LDS by
+// global_load_lds_dwordx4, one contiguous 1 KB block per wave instruction and all of them in flight
+// at once with no registers held; the last len % 4 floats, or the whole run when src is not
+// aligned, are copied with 4-byte loads.
+__device__ inline void stage_rest_rows(float* dst, const float* src, int count, bool vec) {
+	const int len = count * kShRestRow;
+	int done = 0;
+	if (vec) {
+		constexpr int kWaves = kShEvalBlock / 64;
+		constexpr int kOpsMax = (kShEvalBlock * kShRestRow / 4 + 63) / 64;  // 1 KB blocks of a full run: 45
+		const int len4 = len / 4;
+		const int ops = (len4 + 63) / 64;
+		const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+		for (int j = 0; j < (kOpsMax + kWaves - 1) / kWaves; j++) {
+			const int op = wave + j * kWaves;
+			const int e4 = op * 64 + lane;
+			if (op < ops && e4 < len4)
+				__builtin_amdgcn_global_load_lds(src + 4 * e4, (hds_lds_void*)(dst + op * 256), 16, 0, 0);
+		}
+		done = 4 * len4;
+	}
+	for (int e = done + (int)threadIdx.x; e < len; e += kShEvalBlock) dst[e] = src[e];
+	hds_wait_vmem();
+}
 
 __global__ __launch_bounds__(kShEvalBlock) void eval_sh_kernel(int64_t n, int k, const float* __restrict__ sh_dc,
 													  const float* __restrict__ sh_rest, const float* __restrict__ dirs,
-													  const float* __restrict__ radii, float* __restrict__ rgb) {
+													  const float* __restrict__ radii, float* __restrict__ rgb,
+													  bool vec) {
 	// The block's higher-order rows are one contiguous run of count * 45 floats: read it coalesced
 	// into LDS (a thread's own row, read directly, puts 64 cache lines under every load). Row
 	// stride 45 is odd, so the per-thread LDS reads hit 64 different banks.
-	__shared__ float s_rest[kShEvalBlock * 45];
+	__shared__ __attribute__((aligned(16))) float s_rest[kShEvalBlock * kShRestRow];
 	const int64_t first = (int64_t)blockIdx.x * kShEvalBlock;
 	const int64_t i = first + threadIdx.x;
 	if (k > 1) {
 		const int count = (int)(n - first < kShEvalBlock ? n - first : kShEvalBlock);
-		const float* src = sh_rest + first * 45;
-		for (int e = threadIdx.x; e < count * 45; e += kShEvalBlock) s_rest[e] = src[e];
+		stage_rest_rows(s_rest, sh_rest + first * kShRestRow, count, vec);
 		__syncthreads();
 	}
 	if (i >= n) return;
@@ -71,7 +102,7 @@ __global__ __launch_bounds__(kShEvalBlock) void eval_sh_kernel(int64_t n, int k,
 	float b[16];
 	sh_basis(dirs[i * 3], dirs[i * 3 + 1], dirs[i * 3 + 2], k, b);
 	const float* dc = sh_dc + i * 3;
-	const float* rest = s_rest + threadIdx.x * 45;
+	const float* rest = s_rest + threadIdx.x * kShRestRow;
 	for (int c = 0; c < 3; c++) {
 		float value = 0.5f;
 		for (int j = 0; j < k; j++) value += b[j] * sh_weight(dc, rest, j, c);
@@ -135,43 +166,61 @@ struct AdamArgs {
 	float lr_dc, lr_rest, beta1, beta2, one_minus_beta1, one_minus_beta2, eps;
 };
 
-constexpr int kShAdamBlock = 256;  // gaussians (and threads) per work-group
-constexpr int kWRow = 49;          // LDS words per gaussian: 48 weights, odd stride for conflict-free rows
-constexpr int kBRow = 17;          // basis values per gaussian (16, odd stride)
+constexpr int kShAdamBlock = kShEvalBlock;  // gaussians (and threads) per work-group
+constexpr int kBRow = 17;                    // basis values per gaussian (16, odd stride)
 
 // One work-group owns kShAdamBlock consecutive gaussians, i.e. one contiguous run of 3 * count sh_dc
 // and 45 * count sh_rest parameters and of their moments.
-//  1. The run's weights are read coalesced into LDS rows (row = gaussian: dc, then rest).
+//  1. The run's weights are read into LDS (sh_rest as 16-byte loads, all in flight at once).
 //  2. Thread = gaussian: basis of its direction, colour per channel, the clamp mask (max(., 0) passes
 //     no gradient where it clipped), g_c = masked dL/drgb_c, the direction gradient from the colour
 //     polynomial, and (b_j, g_c) into LDS. Culled gaussians get b = g = 0.
-//  3. Thread = parameter: the whole run is stepped with coalesced 16-byte moment reads and writes,
-//     each coefficient's gradient formed on the fly as b_j g_c of its gaussian and channel (no
-//     gradient array is ever materialised) and its current value taken from the LDS copy. Culled
-//     gaussians and coefficients above the degree get a zero gradient and are still stepped, as an
-//     optimizer step over the whole tensors does.
+//  3. Thread = parameter: the whole run is stepped with 16-byte moment reads and writes, all of a
+//     thread's reads issued before its first update, each coefficient's gradient formed on the fly
+//     as b_j g_c of its gaussian and channel (no gradient array is ever materialised) and its
+//     current value taken from the LDS copy. Culled gaussians and coefficients above the degree get
+//     a zero gradient and are still stepped, as an optimizer step over the whole tensors does.
 __global__ __launch_bounds__(kShAdamBlock) void eval_sh_backward_adam_kernel(
 	int64_t n, int k, const float* __restrict__ grad_rgb, float* __restrict__ sh_dc, float* __restrict__ sh_rest,
 	const float* __restrict__ dirs, const float* __restrict__ radii, float* __restrict__ m_dc,
 	float* __restrict__ v_dc, float* __restrict__ m_rest, float* __restrict__ v_rest,
 	const float* __restrict__ step_dc, const float* __restrict__ step_rest, AdamArgs args,
-	float* __restrict__ grad_dirs) {
-	__shared__ float s_w[kShAdamBlock * kWRow];
+	float* __restrict__ grad_dirs, bool vec) {
+	__shared__ __attribute__((aligned(16))) float s_rest[kShAdamBlock * kShRestRow];
+	__shared__ float s_dc[kShAdamBlock * 3];
 	__shared__ float s_b[kShAdamBlock * kBRow];
 	__shared__ float s_g[kShAdamBlock * 4];
 	const int64_t first = (int64_t)blockIdx.x * kShAdamBlock;
 	const int count = (int)min((int64_t)kShAdamBlock, n - first);
 	const int tid = threadIdx.x;
 
-	const float* dc_run = sh_dc + first * 3;
-	const float* rest_run = sh_rest + first * 45;
-	for (int e = tid; e < count * 3; e += kShAdamBlock) s_w[(e / 3) * kWRow + e % 3] = dc_run[e];
-	for (int e = tid; e < count * 45; e += kShAdamBlock) s_w[(e / 45) * kWRow + 3 + e % 45] = rest_run[e];
+	float* const dc_run = sh_dc + first * 3;
+	float* const rest_run = sh_rest + first * kShRestRow;
+	float* const mr = m_rest + first * kShRestRow;
+	float* const vr = v_rest + first * kShRestRow;
+	const int len = count * kShRestRow;
+	const int len4 = len / 4;
+	// The sh_rest moments are read first, four consecutive elements per thread and step, so that
+	// they are in flight with the weights and stay in registers through the gradient phase
+	// (clamped indices: every lane loads, only the updates are guarded).
+	constexpr int kIters = (kShAdamBlock * kShRestRow / 4 + kShAdamBlock - 1) / kShAdamBlock;
+	float4 m4[kIters], v4[kIters];
+	if (vec) {
+#pragma unroll
+		for (int r = 0; r < kIters; r++) {
+			const int e4 = min(tid + r * kShAdamBlock, len4 - 1);
+			m4[r] = reinterpret_cast<const float4*>(mr)[e4];
+			v4[r] = reinterpret_cast<const float4*>(vr)[e4];
+		}
+	}
+	for (int e = tid; e < count * 3; e += kShAdamBlock) s_dc[e] = dc_run[e];
+	stage_rest_rows(s_rest, rest_run, count, vec);
 	__syncthreads();
 
 	if (tid < count) {
 		const int64_t i = first + tid;
-		const float* w = s_w + tid * kWRow;  // w[3 j + c]
+		// w(j, c): coefficient j of channel c of this thread's gaussian.
+		auto w = [&](int j, int c) { return j == 0 ? s_dc[tid * 3 + c] : s_rest[tid * kShRestRow + 3 * (j - 1) + c]; };
 		float b[16];
 		float g[3] = {0.0f, 0.0f, 0.0f};
 		float gd[3] = {0.0f, 0.0f, 0.0f};
@@ -183,12 +232,12 @@ __global__ __launch_bounds__(kShAdamBlock) void eval_sh_backward_adam_kernel(
 #pragma unroll
 			for (int c = 0; c < 3; c++) {
 				float value = 0.5f;
-				for (int j = 0; j < k; j++) value += b[j] * w[3 * j + c];
+				for (int j = 0; j < k; j++) value += b[j] * w(j, c);
 				g[c] = value > 0.0f ? grad_rgb[i * 3 + c] : 0.0f;
 			}
 			float t[16];
 #pragma unroll
-			for (int j = 0; j < 16; j++) t[j] = j < k ? w[3 * j] * g[0] + w[3 * j + 1] * g[1] + w[3 * j + 2] * g[2] : 0.0f;
+			for (int j = 0; j < 16; j++) t[j] = j < k ? w(j, 0) * g[0] + w(j, 1) * g[1] + w(j, 2) * g[2] : 0.0f;
 			sh_poly_grad(x, y, z, k, t, gd[0], gd[1], gd[2]);
 #pragma unroll
 			for (int j = 0; j < 16; j++)
@@ -212,51 +261,36 @@ __global__ __launch_bounds__(kShAdamBlock) void eval_sh_backward_adam_kernel(
 		const int r = e / 3, c = e % 3;
 		const float grad = s_b[r * kBRow] * s_g[r * 4 + c];
 		float m = m_dc[first * 3 + e], v = v_dc[first * 3 + e];
-		sh_dc[first * 3 + e] = adam_update(s_w[r * kWRow + c], m, v, grad, a_dc);
+		dc_run[e] = adam_update(s_dc[e], m, v, grad, a_dc);
 		m_dc[first * 3 + e] = m;
 		v_dc[first * 3 + e] = v;
 	}
-	// sh_rest: element e is coefficient 1 + (e % 45) / 3 of gaussian e / 45, channel e % 3; four
-	// consecutive elements per thread and step, the moments as 16-byte accesses when aligned.
-	float* pr = sh_rest + first * 45;
-	float* mr = m_rest + first * 45;
-	float* vr = v_rest + first * 45;
-	const int len = count * 45;
-	const bool vec = ((reinterpret_cast<uintptr_t>(pr) | reinterpret_cast<uintptr_t>(mr) |
-					   reinterpret_cast<uintptr_t>(vr)) & 15u) == 0;
-	for (int e0 = 4 * tid; e0 < len; e0 += 4 * kShAdamBlock) {
-		float m[4], v[4], p[4];
-		const int lanes = min(4, len - e0);
-		if (vec && lanes == 4) {
-			const float4 m4 = *reinterpret_cast<const float4*>(mr + e0);
-			const float4 v4 = *reinterpret_cast<const float4*>(vr + e0);
-			m[0] = m4.x; m[1] = m4.y; m[2] = m4.z; m[3] = m4.w;
-			v[0] = v4.x; v[1] = v4.y; v[2] = v4.z; v[3] = v4.w;
-		} else {
-			for (int u = 0; u < lanes; u++) {
-				m[u] = mr[e0 + u];
-				v[u] = vr[e0 + u];
-			}
-		}
+	// sh_rest: element e of the run is coefficient 1 + (e % 45) / 3 of gaussian e / 45, channel e % 3.
+	auto rest_grad = [&](int e) {
+		const int r = e / kShRestRow, q = e - r * kShRestRow;
+		return s_b[r * kBRow + 1 + q / 3] * s_g[r * 4 + q % 3];
+	};
+	int done = 0;
+	if (vec) {
 #pragma unroll
-		for (int u = 0; u < 4; u++) {
-			if (u < lanes) {
-				const int e = e0 + u, r = e / 45, q = e % 45;
-				const float grad = s_b[r * kBRow + 1 + q / 3] * s_g[r * 4 + q % 3];
-				p[u] = adam_update(s_w[r * kWRow + 3 + q], m[u], v[u], grad, a_rest);
+		for (int r = 0; r < kIters; r++) {
+			const int e4 = tid + r * kShAdamBlock;
+			if (e4 < len4) {
+				float m[4] = {m4[r].x, m4[r].y, m4[r].z, m4[r].w}, v[4] = {v4[r].x, v4[r].y, v4[r].z, v4[r].w}, p[4];
+#pragma unroll
+				for (int u = 0; u < 4; u++) p[u] = adam_update(s_rest[4 * e4 + u], m[u], v[u], rest_grad(4 * e4 + u), a_rest);
+				reinterpret_cast<float4*>(rest_run)[e4] = make_float4(p[0], p[1], p[2], p[3]);
+				reinterpret_cast<float4*>(mr)[e4] = make_float4(m[0], m[1], m[2], m[3]);
+				reinterpret_cast<float4*>(vr)[e4] = make_float4(v[0], v[1], v[2], v[3]);
 			}
 		}
-		if (vec && lanes == 4) {
-			*reinterpret_cast<float4*>(pr + e0) = make_float4(p[0], p[1], p[2], p[3]);
-			*reinterpret_cast<float4*>(mr + e0) = make_float4(m[0], m[1], m[2], m[3]);
-			*reinterpret_cast<float4*>(vr + e0) = make_float4(v[0], v[1], v[2], v[3]);
-		} else {
-			for (int u = 0; u < lanes; u++) {
-				pr[e0 + u] = p[u];
-				mr[e0 + u] = m[u];
-				vr[e0 + u] = v[u];
-			}
-		}
+		done = 4 * len4;
+	}
+	for (int e = done + tid; e < len; e += kShAdamBlock) {
+		float m = mr[e], v = vr[e];
+		rest_run[e] = adam_update(s_rest[e], m, v, rest_grad(e), a_rest);
+		mr[e] = m;
+		vr[e] = v;
 	}
 }
 
@@ -270,7 +304,9 @@ extern "C" int hds_eval_sh(int64_t n, int degree, const float* sh_dc, const floa
 	HDS_REQUIRE(sh_dc && sh_rest && dirs && radii && rgb, "eval_sh: null pointer argument");
 	hipStream_t s = (hipStream_t)stream;
 	HdsKernelTimer timer1("eval_sh_kernel", s);
-	eval_sh_kernel<<<hds_blocks(n, kShEvalBlock), kShEvalBlock, 0, s>>>(n, (degree + 1) * (degree + 1), sh_dc, sh_rest, dirs, radii, rgb);
+	const bool vec = (reinterpret_cast<uintptr_t>(sh_rest) & 15u) == 0;
+	eval_sh_kernel<<<hds_blocks(n, kShEvalBlock), kShEvalBlock, 0, s>>>(n, (degree + 1) * (degree + 1), sh_dc, sh_rest, dirs,
+																	   radii, rgb, vec);
 	timer1.stop();
 	HDS_LAUNCH_CHECK("eval_sh_forward", s);
 	return HDS_OK;
@@ -292,9 +328,13 @@ extern "C" int hds_eval_sh_backward_adam(int64_t n, int degree, const float* gra
 	AdamArgs a{(float)lr_dc, (float)lr_rest, (float)beta1, (float)beta2, (float)(1.0 - beta1), (float)(1.0 - beta2),
 			   (float)eps};
 	HdsKernelTimer timer2("eval_sh_backward_adam_kernel", s);
+	// 16-byte accesses to the sh_rest run and its moments (each work-group's run starts 16-byte aligned
+	// when the tensors do).
+	const bool vec = ((reinterpret_cast<uintptr_t>(sh_rest) | reinterpret_cast<uintptr_t>(m_rest) |
+					   reinterpret_cast<uintptr_t>(v_rest)) & 15u) == 0;
 	eval_sh_backward_adam_kernel<<<hds_blocks(n, kShAdamBlock), kShAdamBlock, 0, s>>>(
 		n, (degree + 1) * (degree + 1), grad_rgb, sh_dc, sh_rest, dirs, radii, m_dc, v_dc, m_rest, v_rest, step_dc,
-		step_rest, a, grad_dirs);
+		step_rest, a, grad_dirs, vec);
 	timer2.stop();
 	HDS_LAUNCH_CHECK("eval_sh_backward_adam", s);
 	return HDS_OK;
