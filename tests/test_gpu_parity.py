@@ -651,3 +651,58 @@ def test_sh_backward_adam_matches_oracle(degree):
     np.testing.assert_allclose(np_(gd), want_gd, rtol=1e-4, atol=1e-5)
     for a, b in zip(dev, host):
         np.testing.assert_allclose(np_(a), b, rtol=1e-5, atol=1e-7)
+
+
+def _offset_copy(t, offset):
+    """A contiguous device copy of t whose data starts `offset` floats into a larger buffer (offset 1:
+    4-byte aligned only)."""
+    buf = torch.zeros(t.numel() + offset, device=DEV)
+    view = buf[offset:].view(t.shape)
+    view.copy_(t.to(DEV))
+    return view
+
+
+@pytest.mark.parametrize("offset", [0, 1])
+def test_sh_kernels_take_partial_blocks_and_unaligned_runs(offset):
+    """eval_sh and the SH backward + Adam step through the C ABI with 5001 gaussians (the last
+    256-gaussian block holds 137, so its 45-float coefficient run ends in a 1-float tail after the
+    16-byte copies) and, with offset 1, sh_rest and the sh_rest moments 4 bytes off a 16-byte
+    boundary (the 4-byte copy path); both against the oracle."""
+    from gaussian_splatting.rasterizer._native import _ptr, _stream, load_library
+
+    lib = load_library()
+    g = torch.Generator().manual_seed(77)
+    n, degree = 5001, 3
+    sh = torch.randn(n, 16, 3, generator=g) * 0.5
+    dirs = torch.nn.functional.normalize(torch.randn(n, 3, generator=g), dim=-1)
+    radii = (torch.rand(n, generator=g) > 0.1).float()
+    grad_rgb = torch.randn(n, 3, generator=g)
+    dc, rest = sh[:, :1].contiguous(), sh[:, 1:].contiguous()
+    state = [torch.rand(n, 1, 3, generator=g) * 0.01, torch.rand(n, 1, 3, generator=g) * 1e-4,
+             torch.rand(n, 15, 3, generator=g) * 0.01, torch.rand(n, 15, 3, generator=g) * 1e-4]
+    print(f"[test] SH kernels, n {n}, offset {offset}", file=sys.stderr, flush=True)
+    d_dc, d_rest = dc.to(DEV), _offset_copy(rest, offset)
+    d_dirs, d_radii, d_grad = dirs.to(DEV), radii.to(DEV), grad_rgb.to(DEV)
+    assert (d_rest.data_ptr() % 16 == 0) == (offset == 0)
+    rgb = torch.empty(n, 3, device=DEV)
+    assert lib.hds_eval_sh(n, degree, _ptr(d_dc), _ptr(d_rest), _ptr(d_dirs), _ptr(d_radii), _ptr(rgb),
+                           _stream(rgb.device)) == 0
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(np_(rgb), oracle.eval_sh(np_(dc), np_(rest), np_(dirs), degree, np_(radii)),
+                               rtol=1e-6, atol=1e-6)
+
+    m_dc, v_dc = state[0].to(DEV), state[1].to(DEV)
+    m_rest, v_rest = _offset_copy(state[2], offset), _offset_copy(state[3], offset)
+    step = torch.tensor(3.0, device=DEV)
+    grad_dirs = torch.empty(n, 3, device=DEV)
+    assert lib.hds_eval_sh_backward_adam(n, degree, _ptr(d_grad), _ptr(d_dc), _ptr(d_rest), _ptr(d_dirs),
+                                         _ptr(d_radii), _ptr(m_dc), _ptr(v_dc), _ptr(m_rest), _ptr(v_rest), _ptr(step),
+                                         _ptr(step), 0.0025, 0.0025 / 20, 0.9, 0.999, 1e-15, _ptr(grad_dirs),
+                                         _stream(step.device)) == 0
+    torch.cuda.synchronize()
+    host = [np_(t).copy() for t in (dc, rest, *state)]
+    want_gd = oracle.eval_sh_backward_adam(np_(grad_rgb), host[0], host[1], np_(dirs), degree, np_(radii), host[2],
+                                           host[3], host[4], host[5], 3.0, 3.0, 0.0025, 0.0025 / 20, 0.9, 0.999, 1e-15)
+    np.testing.assert_allclose(np_(grad_dirs), want_gd, rtol=1e-4, atol=1e-5)
+    for a, b in zip((d_dc, d_rest, m_dc, v_dc, m_rest, v_rest), host):
+        np.testing.assert_allclose(np_(a), b, rtol=1e-5, atol=1e-7)
