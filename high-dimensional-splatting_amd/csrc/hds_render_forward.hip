@@ -46,6 +46,8 @@ struct RenderArgs {
 	float* final_T;
 	int* n_contrib;
 	float* feature_image;
+	float4* clear;   // hds_render_clear's range (clear4 16-byte words), or null
+	int64_t clear4;
 };
 
 // acc[m][cb] += F^T W for one group. w_hi / w_lo hold this lane's pixel's packed weights for
@@ -122,6 +124,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S >= 128 ? 
 
 	const int tile = hds_xcd_tile(blockIdx.x, a.tiles_x, a.num_tiles);
 	if (tile < 0) return;
+	// hds_render_clear: every (tile, slice) work-group zeroes one contiguous share of the caller's
+	// range before its walk. The walk leaves most of the HBM bandwidth unused, so the 16-byte stores
+	// drain beside it instead of in a fill launch of their own.
+	if (a.clear4 > 0) {
+		const int64_t parts = (int64_t)a.num_tiles * gridDim.y;
+		const int64_t per = (a.clear4 + parts - 1) / parts;
+		const int64_t begin = ((int64_t)tile * gridDim.y + blockIdx.y) * per;
+		const int64_t end = min(a.clear4, begin + per);
+		for (int64_t e = begin + threadIdx.x; e < end; e += blockDim.x) a.clear[e] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+	}
 	const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 	const int slice = blockIdx.y;
 	const int tx0 = (tile % a.tiles_x) * HDS_TILE, ty0 = (tile / a.tiles_x) * HDS_TILE;
@@ -303,12 +315,13 @@ int launch(const RenderArgs& a, int num_tiles, int slices, hipStream_t s) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-}  // namespace
-
-extern "C" int hds_render(int64_t n, int width, int height, int channels, const int32_t* tile_ranges,
-						  const int32_t* values_sorted, int64_t num_pairs, const float* means2D, const float* conic4,
-						  const float* color_opacity4, const float* background, const float* features, float* image,
-						  float* final_T, int32_t* n_contrib, float* feature_image, hds_stream_t stream) {
+int render(int width, int height, int channels, const int32_t* tile_ranges, const int32_t* values_sorted,
+		   int64_t num_pairs, const float* means2D, const float* conic4, const float* color_opacity4,
+		   const float* background, const float* features, float* image, float* final_T, int32_t* n_contrib,
+		   float* feature_image, float* clear, int64_t clear_count, hds_stream_t stream) {
+	HDS_REQUIRE(clear_count >= 0, "render_clear: negative clear count");
+	HDS_REQUIRE(clear_count == 0 || (clear && aligned16(clear) && clear_count % 4 == 0),
+				"render_clear: needs a 16-byte aligned range of a multiple of 4 floats");
 	HDS_REQUIRE(width > 0 && height > 0, "render: image size %dx%d must be positive", width, height);
 	HDS_REQUIRE(tile_ranges && final_T && n_contrib, "render: null tile_ranges / final_T / n_contrib");
 	const bool rgb = image != nullptr;
@@ -323,7 +336,6 @@ extern "C" int hds_render(int64_t n, int width, int height, int channels, const 
 					(!feature_image || aligned16(feature_image)) && (reinterpret_cast<uintptr_t>(means2D) & 7u) == 0 &&
 					(reinterpret_cast<uintptr_t>(tile_ranges) & 7u) == 0,
 				"render: misaligned buffer (conic4, color_opacity4, features, feature_image need 16 bytes)");
-	(void)n;
 	const int tiles_x = (width + HDS_TILE - 1) / HDS_TILE, tiles_y = (height + HDS_TILE - 1) / HDS_TILE;
 	const int num_tiles = tiles_x * tiles_y;
 	RenderArgs a{width,
@@ -341,7 +353,9 @@ extern "C" int hds_render(int64_t n, int width, int height, int channels, const 
 				 image,
 				 final_T,
 				 n_contrib,
-				 feature_image};
+				 feature_image,
+				 reinterpret_cast<float4*>(clear),
+				 clear_count / 4};
 	hipStream_t s = (hipStream_t)stream;
 	if (!feats) {
 		HDS_REQUIRE(rgb, "render: nothing to render (no image and no features)");
@@ -360,4 +374,25 @@ extern "C" int hds_render(int64_t n, int width, int height, int channels, const 
 		case 64: return rgb ? launch<64, true>(a, num_tiles, slices, s) : launch<64, false>(a, num_tiles, slices, s);
 		default: return rgb ? launch<128, true>(a, num_tiles, slices, s) : launch<128, false>(a, num_tiles, slices, s);
 	}
+}
+
+}  // namespace
+
+extern "C" int hds_render(int64_t n, int width, int height, int channels, const int32_t* tile_ranges,
+						  const int32_t* values_sorted, int64_t num_pairs, const float* means2D, const float* conic4,
+						  const float* color_opacity4, const float* background, const float* features, float* image,
+						  float* final_T, int32_t* n_contrib, float* feature_image, hds_stream_t stream) {
+	(void)n;
+	return render(width, height, channels, tile_ranges, values_sorted, num_pairs, means2D, conic4, color_opacity4,
+				  background, features, image, final_T, n_contrib, feature_image, nullptr, 0, stream);
+}
+
+extern "C" int hds_render_clear(int64_t n, int width, int height, int channels, const int32_t* tile_ranges,
+								const int32_t* values_sorted, int64_t num_pairs, const float* means2D,
+								const float* conic4, const float* color_opacity4, const float* background,
+								const float* features, float* image, float* final_T, int32_t* n_contrib,
+								float* feature_image, float* clear, int64_t clear_count, hds_stream_t stream) {
+	(void)n;
+	return render(width, height, channels, tile_ranges, values_sorted, num_pairs, means2D, conic4, color_opacity4,
+				  background, features, image, final_T, n_contrib, feature_image, clear, clear_count, stream);
 }

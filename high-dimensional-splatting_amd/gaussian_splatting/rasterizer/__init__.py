@@ -55,12 +55,12 @@ class RasterizeGaussians(torch.autograd.Function):
         ext = _get_rasterizer()
         width, height = int(image_width), int(image_height)
         means2D = means2D.contiguous()
-        # Training (features need a gradient and the caller records a graph): the gradient buffers are
-        # zeroed beside the binning. Inside forward grad mode is always off, so the caller's mode
-        # comes in as grad_enabled.
-        ctx.prezeroed = None
+        # Training (features need a gradient and the caller records a graph): the render's work-groups
+        # zero the backward's gradient buffers beside their walk. Inside forward grad mode is always
+        # off, so the caller's mode comes in as grad_enabled.
+        ctx.prezeroed, clear = None, None
         if features is not None and ctx.needs_input_grad[7] and grad_enabled:
-            ctx.prezeroed = ext.prezeroed_gradients(means2D.shape[0], int(features.shape[1]), means2D.device)
+            clear, ctx.prezeroed = ext.gradient_buffers(means2D.shape[0], int(features.shape[1]), means2D.device)
         # The render is enqueued before the host reads the pair count (the reference's one
         # blocking read, forward.cu:321-325), so the GPU does not idle during that read.
         bins = ext.bin_async(means2D, depths.contiguous(), radii.contiguous(), conics.contiguous(),
@@ -70,7 +70,9 @@ class RasterizeGaussians(torch.autograd.Function):
         background = background.contiguous()
         conic, color_opacity, tile_ranges = bins.conic4, bins.color_opacity4, bins.tile_ranges
         image, feature_image, final_T, n_contrib = ext.render(
-            means2D, conic, color_opacity, bins.values, tile_ranges, width, height, background, features)
+            means2D, conic, color_opacity, bins.values, tile_ranges, width, height, background, features,
+            clear=clear)
+        # A render again after a rebin: the buffers were already cleared (on this stream) by the first.
         if ext.resolve(bins):
             image, feature_image, final_T, n_contrib = ext.render(
                 means2D, conic, color_opacity, bins.values, tile_ranges, width, height, background, features)

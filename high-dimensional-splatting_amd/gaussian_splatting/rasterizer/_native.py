@@ -51,6 +51,8 @@ PROTOTYPES = {
     "hds_bin_static": (_i32, [_i64, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _vp, _vp, _i64, _vp, _vp, _vp, _vp]),
     "hds_render": (_i32, [_i64, _i32, _i32, _i32, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                           _vp]),
+    "hds_render_clear": (_i32, [_i64, _i32, _i32, _i32, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                _vp, _vp, _i64, _vp]),
     "hds_render_backward": (_i32, [_i64, _i32, _i32, _i32, _i32, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp,
                                    _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "hds_render_backward_accumulate": (_i32, [_i64, _i32, _i32, _i32, _i32, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp,
@@ -249,37 +251,19 @@ class HipRasterizer:
         self.lib = load_library()
         self.timer: StageTimer | None = None
         self._pair_capacity: dict[int, int] = {}
-        self._zero_streams: dict[int, torch.cuda.Stream] = {}
-        # Work-groups of the pre-zeroing fill beside the binning (0: as many as fill the device).
-        self.zero_fill_workgroups = 0
 
-    def prezeroed_gradients(self, n: int, channels: int, device: torch.device):
-        """Zeroed output buffers for a later render_backward (grad_means2D [N,2], grad_conics [N,3],
-        grad_colors [N,3], grad_opacities [N,1], grad_features [N,C]), cleared on a side stream
-        (default priority) that starts after the work queued so far, so the fill runs beside the
-        forward's binning instead of at the head of the backward. Returns (buffers, event); pass both
-        to render_backward."""
-        current = torch.cuda.current_stream(device)
-        side = self._zero_streams.get(device.index)
-        if side is None:
-            side = self._zero_streams[device.index] = torch.cuda.Stream(device=device)
-        # One allocation for the five buffers, each view starting on a 256-byte boundary, cleared by
-        # one fill that takes at most zero_fill_workgroups work-groups, so the binning's small
-        # kernels beside it keep most of the CUs.
+    def gradient_buffers(self, n: int, channels: int, device: torch.device):
+        """Output buffers for a later render_backward (grad_means2D [N,2], grad_conics [N,3],
+        grad_colors [N,3], grad_opacities [N,1], grad_features [N,C]) as views of one allocation, each
+        starting on a 256-byte boundary. Returns (storage, buffers): pass storage to render(clear=...),
+        which zeroes it, and the buffers to render_backward(prezeroed=...)."""
         shapes = ((n, 2), (n, 3), (n, 3), (n, 1), (n, channels))
         offsets, total = [], 0
         for shape in shapes:
             offsets.append(total)
             total += (math.prod(shape) + 63) // 64 * 64
         storage = torch.empty((total,), device=device, dtype=torch.float32)
-        buffers = tuple(storage[o:o + math.prod(shape)].view(shape) for o, shape in zip(offsets, shapes))
-        side.wait_stream(current)
-        with torch.cuda.device(device), torch.cuda.stream(side):
-            _check(self.lib.hds_zero_async(_ptr(storage), total, self.zero_fill_workgroups, _stream(device)))
-            storage.record_stream(side)
-            event = torch.cuda.Event()
-            event.record(side)
-        return buffers, event
+        return storage, tuple(storage[o:o + math.prod(shape)].view(shape) for o, shape in zip(offsets, shapes))
 
     def _run(self, stage: str, fn) -> None:
         """Runs one C call (raising on error), inside the stage timer when one is installed."""
@@ -475,8 +459,9 @@ class HipRasterizer:
         self._pair_capacity[dev.index] = (int(pairs * self.PAIR_HEADROOM) + 2 * chunk) // chunk * chunk
 
     def render(self, means2D, conic4, color_opacity4, values_sorted, tile_ranges, width, height, background=None,
-               features=None, rgb=True):
-        """One front-to-back tile walk (forward.cu:141-237 + features.cu:116-282).
+               features=None, rgb=True, clear=None):
+        """One front-to-back tile walk (forward.cu:141-237 + features.cu:116-282). With `clear` (a float32
+        tensor from gradient_buffers), the walk's work-groups also zero it (hds_render_clear).
 
         Returns (image [H,W,3] or None, feature_image [H,W,C] or None, final_T [H,W], n_contrib [H,W]).
         """
@@ -498,21 +483,28 @@ class HipRasterizer:
         n_contrib = torch.empty((height, width), device=dev, dtype=torch.int32)
         if rgb and background is None:
             background = black_background(dev)
-        with torch.cuda.device(dev):
-            self._run("render", lambda: self.lib.hds_render(
-                means2D.shape[0], width, height, channels, _ptr(tile_ranges), _ptr(values_sorted),
+        args = (means2D.shape[0], width, height, channels, _ptr(tile_ranges), _ptr(values_sorted),
                 values_sorted.numel(), _ptr(means2D), _ptr(conic4), _ptr(color_opacity4) if rgb else None,
                 _ptr(background) if rgb else None, _ptr(features), _ptr(image), _ptr(final_T), _ptr(n_contrib),
-                _ptr(feature_image), _stream(dev)))
+                _ptr(feature_image))
+        if clear is not None and not (clear.is_cuda and clear.is_contiguous() and clear.dtype == torch.float32
+                                      and clear.device == dev):
+            raise RuntimeError("clear must be a contiguous float32 tensor on the render's device")
+        with torch.cuda.device(dev):
+            if clear is None:
+                self._run("render", lambda: self.lib.hds_render(*args, _stream(dev)))
+            else:
+                self._run("render", lambda: self.lib.hds_render_clear(*args, _ptr(clear), clear.numel(),
+                                                                      _stream(dev)))
         return image, feature_image, final_T, n_contrib
 
     def render_backward(self, means2D, conic4, color_opacity4, values_sorted, tile_ranges, final_T, n_contrib,
                         width, height, grad_image=None, background=None, features=None, grad_feature_image=None,
                         slice_width=None, want_feature_grad=True, prezeroed=None):
         """The blend backward (backward.cu:7-164 + features.cu:350-542): geometry gradients from a
-        back-to-front replay, feature gradients from a front-to-back replay beside it. `prezeroed` is a
-        (buffers, event) pair from prezeroed_gradients: the gradients are then added into those
-        buffers once the event has passed, instead of into buffers zeroed here.
+        back-to-front replay, feature gradients from a front-to-back replay beside it. `prezeroed` is the
+        buffers of gradient_buffers, zeroed by earlier work on the current stream (render(clear=...)):
+        the gradients are then added into those buffers instead of into buffers zeroed here.
 
         Returns (grad_means2D [N,2], grad_conics [N,3], grad_colors [N,3] or None, grad_opacities [N,1],
         grad_features [N,C] or None).
@@ -530,14 +522,13 @@ class HipRasterizer:
                 background = black_background(dev)
         want_feat = features is not None and want_feature_grad
         if prezeroed is not None:
-            (g_means, g_conics, g_colors, g_opac, g_feat), event = prezeroed
+            g_means, g_conics, g_colors, g_opac, g_feat = prezeroed
             if grad_image is None:
                 g_colors = None
             if not want_feat:
                 g_feat = None
             elif g_feat.shape != (n, channels):
                 raise RuntimeError(f"prezeroed grad_features {tuple(g_feat.shape)} != ({n}, {channels})")
-            torch.cuda.current_stream(dev).wait_event(event)
             entry = self.lib.hds_render_backward_accumulate
         else:
             # hds_render_backward zeroes the outputs itself before its atomics add into them.

@@ -184,6 +184,18 @@ HDS_API int hds_render(int64_t n, int width, int height, int channels, const int
 			   const float* features, float* image, float* final_T, int32_t* n_contrib,
 			   float* feature_image, hds_stream_t stream);
 
+/* hds_render that also zeroes `clear_count` floats at `clear` (16-byte aligned, a multiple of 4;
+ * 0 clears nothing), each tile's work-group one share before its walk: the zero-initialised
+ * gradient buffers of a following hds_render_backward_accumulate, cleared in the bandwidth the
+ * walk leaves unused instead of by a fill of their own. The same results as hds_render followed by
+ * hds_zero_async over the range. No counterpart in the reference, which allocates its gradient
+ * outputs with torch::zeros in the backward (backward.cu:166-226, features.cu:561-616). */
+HDS_API int hds_render_clear(int64_t n, int width, int height, int channels, const int32_t* tile_ranges,
+				 const int32_t* values_sorted, int64_t num_pairs, const float* means2D,
+				 const float* conic4, const float* color_opacity4, const float* background,
+				 const float* features, float* image, float* final_T, int32_t* n_contrib,
+				 float* feature_image, float* clear, int64_t clear_count, hds_stream_t stream);
+
 /* ---- blend backward: replaces rasterize_backward (backward.cu:166-226) and
  *      rasterize_features_backward (features.cu:561-616) with one back-to-front walk ----------- */
 

@@ -105,6 +105,24 @@ def test_zero_fill_rejects_bad_ranges_before_launch(lib):
     assert lib.hds_zero_async(None, 0, 0, None) == 0  # nothing to clear, nothing enqueued
 
 
+def test_render_clear_rejects_bad_ranges_before_launch(lib):
+    fake = ctypes.c_void_p(16)
+
+    def call(clear, count):
+        # A valid-looking RGB render of 10 pairs; the range checks come first.
+        return lib.hds_render_clear(10, 32, 32, 0, fake, fake, 10, fake, fake, fake, fake, None, fake, fake, fake,
+                                    None, clear, count, None)
+
+    assert call(fake, -4) == 1 and b"negative" in lib.hds_last_error()
+    assert call(None, 8) == 1 and b"16-byte aligned" in lib.hds_last_error()
+    assert call(ctypes.c_void_p(20), 8) == 1 and b"16-byte aligned" in lib.hds_last_error()
+    assert call(fake, 6) == 1 and b"multiple of 4" in lib.hds_last_error()
+    # Past the range checks, the render's own checks still apply.
+    status = lib.hds_render_clear(10, 0, 32, 0, fake, fake, 10, fake, fake, fake, fake, None, fake, fake, fake, None,
+                                  fake, 8, None)
+    assert status == 1 and b"must be positive" in lib.hds_last_error()
+
+
 def test_bad_image_size_and_sh_degree_are_rejected(lib):
     status = lib.hds_eval_sh(10, 4, None, None, None, None, None, None)
     assert status == 1 and b"degree 4" in lib.hds_last_error()

@@ -262,9 +262,9 @@ def test_async_binning_of_a_scene_with_no_pairs():
 
 
 def test_gradient_buffers_are_zeroed_ahead_only_when_a_graph_is_recorded(monkeypatch):
-    """The forward zeroes the backward's gradient buffers on a side stream only when the caller records
-    a graph (not under torch.no_grad(), where no backward can follow), and the backward then gives the
-    same gradients as one that zeroes its own buffers."""
+    """The forward's render zeroes the backward's gradient buffers only when the caller records a graph
+    (not under torch.no_grad(), where no backward can follow), and the backward then gives the same
+    gradients as one that zeroes its own buffers."""
     wl = synthetic_config(0, n=6000)
     (m2, d, r, c), _ = project_both(wl.means, wl.scales, wl.quats, wl.opacities, wl.cam)
     colors = torch.rand(wl.n, 3, generator=torch.Generator().manual_seed(3)).to(DEV)
@@ -272,8 +272,8 @@ def test_gradient_buffers_are_zeroed_ahead_only_when_a_graph_is_recorded(monkeyp
     opac = wl.opacities.to(DEV)
     ext = _get_rasterizer()
     calls = []
-    original = ext.prezeroed_gradients
-    monkeypatch.setattr(ext, "prezeroed_gradients", lambda *args: calls.append(args) or original(*args))
+    original = ext.gradient_buffers
+    monkeypatch.setattr(ext, "gradient_buffers", lambda *args: calls.append(args) or original(*args))
     with torch.no_grad():
         rasterize(m2, d, r, c, colors, opac, wl.width, wl.height, features=feats)
     assert not calls
@@ -309,6 +309,33 @@ def test_zero_fill_clears_exactly_its_range(workgroups):
     torch.cuda.synchronize()
     assert int((buf[:1_000_000] != 0).sum()) == 0
     assert bool((buf[1_000_000:] == 7.0).all())
+
+
+@pytest.mark.parametrize("channels,count", [(0, 1_000_004), (256, 2_000_000), (64, 4)])
+def test_render_clear_renders_the_same_and_clears_exactly_its_range(channels, count):
+    """hds_render_clear gives hds_render's outputs bit for bit and zeroes exactly `count` floats: a range
+    that does not divide evenly over the (tile, slice) work-groups, one spread over two 128-channel
+    slices, and one smaller than the work-group count (most shares empty)."""
+    wl = synthetic_config(0, n=6000)
+    (m2, d, r, c), _ = project_both(wl.means, wl.scales, wl.quats, wl.opacities, wl.cam)
+    colors = torch.rand(wl.n, 3, generator=torch.Generator().manual_seed(3)).to(DEV)
+    opac = wl.opacities.to(DEV)
+    feats = (torch.randn(wl.n, channels, generator=torch.Generator().manual_seed(4)).to(DEV)
+             if channels else None)
+    ext = _get_rasterizer()
+    values, ranges, conic4, color4 = ext.bin(m2, d, r, c, colors, opac, wl.width, wl.height)
+    bg = torch.zeros(3, device=DEV)
+    print(f"[test] render_clear, C {channels}, count {count}", file=sys.stderr, flush=True)
+    want = ext.render(m2, conic4, color4, values, ranges, wl.width, wl.height, bg, feats)
+    buf = torch.full((count + 64,), 7.0, device=DEV)
+    got = ext.render(m2, conic4, color4, values, ranges, wl.width, wl.height, bg, feats, clear=buf[:count])
+    torch.cuda.synchronize()
+    assert int((buf[:count] != 0).sum()) == 0
+    assert bool((buf[count:] == 7.0).all())
+    for a, b in zip(got, want):
+        assert (a is None) == (b is None)
+        if a is not None:
+            assert torch.equal(a, b)
 
 
 def test_rasterize_is_identical_with_and_without_the_pair_count_read():
