@@ -188,7 +188,8 @@ HDS_API int hds_render(int64_t n, int width, int height, int channels, const int
  * 0 clears nothing), each tile's work-group one share before its walk: the zero-initialised
  * gradient buffers of a following hds_render_backward_accumulate, cleared in the bandwidth the
  * walk leaves unused instead of by a fill of their own. The same results as hds_render followed by
- * hds_zero_async over the range. No counterpart in the reference, which allocates its gradient
+ * hds_zero_async over the range; the range must not overlap the render's inputs or outputs. No
+ * counterpart in the reference, which allocates its gradient
  * outputs with torch::zeros in the backward (backward.cu:166-226, features.cu:561-616). */
 HDS_API int hds_render_clear(int64_t n, int width, int height, int channels, const int32_t* tile_ranges,
 				 const int32_t* values_sorted, int64_t num_pairs, const float* means2D,
