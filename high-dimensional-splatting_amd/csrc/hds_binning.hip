@@ -5,7 +5,7 @@
 // order is built in two cheaper steps:
 //   1. stable radix sort of the N gaussians by the 32-bit depth key (ties keep index order),
 //   2. pairs emitted in that depth order, then stable radix sort of the P pairs by tile id alone
-//      (ceil(log2 T) bits: 12 at 979x546, so 2 passes of 8 bits instead of 6).
+//      (ceil(log2 T) bits: 12 at 979x546, so 2 passes of 6 bits instead of 6 passes of 8).
 // Stability of both sorts gives exactly the reference's (tile, depth bits, index) order, so
 // values_sorted and tile_ranges equal the CPU oracle's bit for bit, and the pair sort moves
 // 8 B per pair and pass instead of 12. Everything is integer work; the only floating point is the
@@ -201,7 +201,8 @@ __device__ inline uint32_t block_exclusive_scan(uint32_t v, uint32_t* s_wave, ui
 	return before + x - v;
 }
 
-// Lanes of this wave (among `active`) whose digit equals ours.
+// Lanes of this wave (among `active`) whose digit equals ours. Digits narrower than 8 bits have
+// zero high bits in every lane, whose ballots then change nothing.
 __device__ inline uint64_t match_digit(uint32_t d, uint64_t active) {
 	uint64_t peers = active;
 #pragma unroll
@@ -216,9 +217,10 @@ __device__ inline uint64_t match_digit(uint32_t d, uint64_t active) {
 // Adds a valid key to the work-group's LDS digit histograms, one per pass: one LDS atomic per lane
 // and pass. Lanes that share a digit serialise in the LDS, which still costs less than grouping them
 // with ballots first (measured on the depth keys and on the tile keys of the stress scene).
-__device__ inline void count_digits(uint32_t key, bool valid, int passes, uint32_t (*s_hist)[kRadix]) {
+__device__ inline void count_digits(uint32_t key, bool valid, int passes, int bits, uint32_t (*s_hist)[kRadix]) {
 	if (!valid) return;
-	for (int p = 0; p < passes; p++) atomicAdd(&s_hist[p][(key >> (p * kRadixBits)) & (kRadix - 1)], 1u);
+	const uint32_t mask = (1u << bits) - 1u;
+	for (int p = 0; p < passes; p++) atomicAdd(&s_hist[p][(key >> (p * bits)) & mask], 1u);
 }
 
 // hist = [pass][kHistCopies][kRadix]; this work-group adds into copy blockIdx.x % kHistCopies.
@@ -232,7 +234,7 @@ __device__ inline void flush_digits(int passes, uint32_t (*s_hist)[kRadix], uint
 }
 
 // ---------------------------------------------------------------------------------------------
-// One stable LSD radix pass over 8 bits, single launch.
+// One stable LSD radix pass over a digit of at most 8 bits, single launch.
 // ---------------------------------------------------------------------------------------------
 
 // digit_hist = this pass's kHistCopies digit histograms; status = [partitions][kRadix] look-back
@@ -244,7 +246,7 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __re
 															 const uint32_t* __restrict__ vals_in,
 															 uint32_t* __restrict__ keys_out,
 															 uint32_t* __restrict__ vals_out, int64_t n,
-															 const uint64_t* __restrict__ n_total, int pass,
+															 const uint64_t* __restrict__ n_total, int pass, int bits,
 															 const uint32_t* __restrict__ digit_hist,
 															 uint64_t* status, uint32_t* ticket, uint32_t* error,
 															 uint32_t spin_limit, const uint2* __restrict__ table,
@@ -259,7 +261,10 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __re
 	__shared__ uint32_t s_wave[kWaves];
 	__shared__ int64_t s_part;
 	const int t = threadIdx.x, lane = t & (HDS_WAVE - 1), wave = t / HDS_WAVE;
-	const int shift = pass * kRadixBits;
+	// Digit p of a key is bits [p * bits, (p + 1) * bits): every pass of a sort has the same width,
+	// at most 8 bits; digits above 2^bits never occur.
+	const int shift = pass * bits;
+	const uint32_t mask = (1u << bits) - 1u;
 #pragma unroll
 	for (int w = 0; w < kWaves; w++) s_cnt[w][t] = 0;
 	const int64_t part = take_ticket(ticket, &s_part);
@@ -284,7 +289,7 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __re
 #pragma unroll
 	for (int r = 0; r < kIPT; r++) {
 		const bool valid = wbase + r * HDS_WAVE + lane < n;
-		const uint32_t d = (key[r] >> shift) & (kRadix - 1);
+		const uint32_t d = (key[r] >> shift) & mask;
 		const uint64_t peers = match_digit(d, hds_ballot(valid));
 		const uint32_t below = (uint32_t)hds_rank_below(peers);
 		const uint32_t before = s_cnt[wave][d];
@@ -301,8 +306,10 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __re
 		s_cnt[w][t] = count;
 		count += c;
 	}
+	// Digits that cannot occur (t > mask) have no count to publish and no predecessors to wait for.
+	const bool digit_used = (uint32_t)t <= mask;
 	uint64_t* mine = status + part * kRadix + t;
-	status_store(mine, status_word(part == 0 ? 2 * pass + 2 : 2 * pass + 1, count));
+	if (digit_used) status_store(mine, status_word(part == 0 ? 2 * pass + 2 : 2 * pass + 1, count));
 	uint32_t digit_total = 0;
 #pragma unroll
 	for (int c = 0; c < kHistCopies; c++) digit_total += digit_hist[c * kRadix + t];
@@ -310,7 +317,7 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __re
 	const uint32_t digit_start = block_exclusive_scan(digit_total, s_wave, unused);
 	const uint32_t local_start = block_exclusive_scan(count, s_wave, unused);
 	uint64_t before = 0;
-	if (part > 0) {
+	if (part > 0 && digit_used) {
 		before = lookback<8>(status + t, kRadix, part, (uint32_t)pass, error, spin_limit);
 		status_store(mine, status_word(2 * pass + 2, before + count));
 	}
@@ -323,7 +330,7 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __re
 #pragma unroll
 	for (int r = 0; r < kIPT; r++) {
 		if (wbase + r * HDS_WAVE + lane < n) {
-			const uint32_t d = (key[r] >> shift) & (kRadix - 1);
+			const uint32_t d = (key[r] >> shift) & mask;
 			const uint32_t slot = s_local[d] + s_cnt[wave][d] + rank[r];
 			s_keys[slot] = key[r];
 			s_vals[slot] = val[r];
@@ -336,7 +343,7 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __re
 		const int j = r * kThreads + t;
 		if (j < items) {
 			const uint32_t k = s_keys[j];
-			const uint32_t pos = s_adj[(k >> shift) & (kRadix - 1)] + (uint32_t)j;
+			const uint32_t pos = s_adj[(k >> shift) & mask] + (uint32_t)j;
 			// Always in range when the digit counts are right; the test keeps a failed look-back
 			// (error flag raised) from writing outside the buffers.
 			if (pos < n) {
@@ -351,12 +358,12 @@ __global__ __launch_bounds__(kThreads) void onesweep_kernel(const uint32_t* __re
 	}
 }
 
-// Sorts (keys, vals) on `passes` 8-bit digits through the buffers a (input) and b; the result
+// Sorts (keys, vals) on `passes` digits of `bits` bits through the buffers a (input) and b; the result
 // ends in a for an even pass count, else in b. n items, or device_count(n_total, n) with n_total. hist holds every pass's digit histograms (filled by
 // the producer of the keys); status/tickets are zeroed. Keys of the last pass are written only
 // if keys_final_needed; with table, the last pass also writes gathered[i] = table[vals[i]].
 int onesweep_sort(uint32_t* keys_a, uint32_t* vals_a, uint32_t* keys_b, uint32_t* vals_b, int64_t n,
-				  const uint64_t* n_total, int passes, const uint32_t* hist, uint64_t* status, uint32_t* tickets, uint32_t* error, bool keys_final_needed,
+				  const uint64_t* n_total, int passes, int bits, const uint32_t* hist, uint64_t* status, uint32_t* tickets, uint32_t* error, bool keys_final_needed,
 				  const uint2* table, uint2* gathered, hipStream_t s) {
 	// Passes over more than 16M items take 8192-item partitions: half the tickets and look-back
 	// steps (both are paid per partition); smaller ones keep 4096 so that the grid fills the chip.
@@ -369,22 +376,22 @@ int onesweep_sort(uint32_t* keys_a, uint32_t* vals_a, uint32_t* keys_b, uint32_t
 		const uint32_t* h = hist + p * kHistWords;
 		HdsKernelTimer timer("onesweep_kernel", s);
 		if (last && table && large)
-			onesweep_kernel<false, true, 2 * kItemsPerThread><<<parts, kThreads, 0, s>>>(kin, vin, nullptr, vout, n, n_total, p, h,
+			onesweep_kernel<false, true, 2 * kItemsPerThread><<<parts, kThreads, 0, s>>>(kin, vin, nullptr, vout, n, n_total, p, bits, h,
 																						  status, tickets + p, error, g_spin_limit.load(std::memory_order_relaxed), table, gathered);
 		else if (last && table)
-			onesweep_kernel<false, true, kItemsPerThread><<<parts, kThreads, 0, s>>>(kin, vin, nullptr, vout, n, n_total, p, h, status,
+			onesweep_kernel<false, true, kItemsPerThread><<<parts, kThreads, 0, s>>>(kin, vin, nullptr, vout, n, n_total, p, bits, h, status,
 																					  tickets + p, error, g_spin_limit.load(std::memory_order_relaxed), table, gathered);
 		else if (keys_out && large)
-			onesweep_kernel<true, false, 2 * kItemsPerThread><<<parts, kThreads, 0, s>>>(kin, vin, kout, vout, n, n_total, p, h,
+			onesweep_kernel<true, false, 2 * kItemsPerThread><<<parts, kThreads, 0, s>>>(kin, vin, kout, vout, n, n_total, p, bits, h,
 																						  status, tickets + p, error, g_spin_limit.load(std::memory_order_relaxed), nullptr, nullptr);
 		else if (keys_out)
-			onesweep_kernel<true, false, kItemsPerThread><<<parts, kThreads, 0, s>>>(kin, vin, kout, vout, n, n_total, p, h, status,
+			onesweep_kernel<true, false, kItemsPerThread><<<parts, kThreads, 0, s>>>(kin, vin, kout, vout, n, n_total, p, bits, h, status,
 																					  tickets + p, error, g_spin_limit.load(std::memory_order_relaxed), nullptr, nullptr);
 		else if (large)
-			onesweep_kernel<false, false, 2 * kItemsPerThread><<<parts, kThreads, 0, s>>>(kin, vin, nullptr, vout, n, n_total, p, h,
+			onesweep_kernel<false, false, 2 * kItemsPerThread><<<parts, kThreads, 0, s>>>(kin, vin, nullptr, vout, n, n_total, p, bits, h,
 																						   status, tickets + p, error, g_spin_limit.load(std::memory_order_relaxed), nullptr, nullptr);
 		else
-			onesweep_kernel<false, false, kItemsPerThread><<<parts, kThreads, 0, s>>>(kin, vin, nullptr, vout, n, n_total, p, h, status,
+			onesweep_kernel<false, false, kItemsPerThread><<<parts, kThreads, 0, s>>>(kin, vin, nullptr, vout, n, n_total, p, bits, h, status,
 																					   tickets + p, error, g_spin_limit.load(std::memory_order_relaxed), nullptr, nullptr);
 		timer.stop();
 		HDS_LAUNCH_CHECK("onesweep_radix_pass", s);
@@ -499,7 +506,7 @@ __global__ __launch_bounds__(kThreads) void prepare_kernel(
 			depth_keys[i] = key;
 			order[i] = (uint32_t)i;
 		}
-		count_digits(key, valid, kMaxPasses, s_hist);
+		count_digits(key, valid, kMaxPasses, kRadixBits, s_hist);
 	}
 	flush_digits(kMaxPasses, s_hist, hist);
 }
@@ -538,7 +545,7 @@ __global__ __launch_bounds__(kThreads) void emit_kernel(int64_t n, int64_t num_p
 														 const uint32_t* __restrict__ offsets,
 														 const uint32_t* __restrict__ order,
 														 const uint2* __restrict__ rects_sorted, int tiles_x,
-														 int passes, uint32_t* __restrict__ tile_keys,
+														 int passes, int bits, uint32_t* __restrict__ tile_keys,
 														 uint32_t* __restrict__ gids, uint32_t* __restrict__ hist) {
 	__shared__ uint32_t s_off[kWaves][HDS_WAVE];
 	__shared__ uint32_t s_hist[kMaxPasses][kRadix];
@@ -591,7 +598,7 @@ __global__ __launch_bounds__(kThreads) void emit_kernel(int64_t n, int64_t num_p
 			tile_keys[p] = key;
 			gids[p] = jgid;
 		}
-		count_digits(key, valid_pair, passes, s_hist);
+		count_digits(key, valid_pair, passes, bits, s_hist);
 	}
 	flush_digits(passes, s_hist, hist);
 }
@@ -780,7 +787,7 @@ int bin_count_launch(int64_t n, const float* means2D, const float* depths, const
 	HDS_LAUNCH_CHECK("prepare_gaussians", s);
 	// 4 passes: the depth order ends back in (keys_a, vals_a); the last one also writes each
 	// entry's tile rectangle to rects_sorted.
-	int st = onesweep_sort(keys_a, vals_a, keys_b, vals_b, n, nullptr, kMaxPasses, ctrl->hist, status, ctrl->tickets,
+	int st = onesweep_sort(keys_a, vals_a, keys_b, vals_b, n, nullptr, kMaxPasses, kRadixBits, ctrl->hist, status, ctrl->tickets,
 						   &ctrl->error, false, rects, rects_sorted, s);
 	if (st != HDS_OK) return st;
 	HdsKernelTimer timer3("scan_kernel", s);
@@ -841,8 +848,12 @@ int bin_emit_launch(int64_t n, int64_t num_pairs, bool exact, int width, int hei
 	uint64_t* status = at<uint64_t>(pairs_workspace, p.status);
 	uint32_t* out = reinterpret_cast<uint32_t*>(values_sorted);
 
-	// Pick the ping-pong buffers so the last pass lands in values_sorted.
-	const int passes = (tile_bits(num_tiles) + kRadixBits - 1) / kRadixBits;
+	// Pick the ping-pong buffers so the last pass lands in values_sorted. The tile id's bits are
+	// split evenly over the passes (12 bits at 979x546: two 6-bit digits, not 8 + 4), so each
+	// digit's run in a partition's output is longer and its stores more coalesced.
+	const int key_bits = tile_bits(num_tiles);
+	const int passes = (key_bits + kRadixBits - 1) / kRadixBits;
+	const int bits = passes > 0 ? (key_bits + passes - 1) / passes : kRadixBits;
 	uint32_t* vals_a = (passes % 2 == 0) ? out : vals_tmp;
 	uint32_t* vals_b = (passes % 2 == 0) ? vals_tmp : out;
 
@@ -854,10 +865,10 @@ int bin_emit_launch(int64_t n, int64_t num_pairs, bool exact, int width, int hei
 	HDS_LAUNCH_CHECK("zero_sort_control", s);
 	HdsKernelTimer timer2("emit_kernel", s);
 	emit_kernel<<<hds_blocks(n, kThreads), kThreads, 0, s>>>(n, num_pairs, total, offsets, order, rects_sorted,
-																	tiles_x, passes, keys_a, vals_a, ctrl->hist);
+																	tiles_x, passes, bits, keys_a, vals_a, ctrl->hist);
 	timer2.stop();
 	HDS_LAUNCH_CHECK("emit_pairs", s);
-	int st = onesweep_sort(keys_a, vals_a, keys_b, vals_b, num_pairs, total, passes, ctrl->hist, status,
+	int st = onesweep_sort(keys_a, vals_a, keys_b, vals_b, num_pairs, total, passes, bits, ctrl->hist, status,
 						   ctrl->tickets, &ctrl->error, true, nullptr, nullptr, s);
 	if (st != HDS_OK) return st;
 	const uint32_t* keys_sorted = (passes % 2 == 0) ? keys_a : keys_b;
