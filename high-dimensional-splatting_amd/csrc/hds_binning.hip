@@ -477,7 +477,7 @@ __global__ __launch_bounds__(kThreads) void prepare_kernel(
 	const float* __restrict__ conics, const float* __restrict__ colors, const float* __restrict__ opacities,
 	int tiles_x, int tiles_y, float4* __restrict__ conic4, float4* __restrict__ color_opacity4,
 	uint2* __restrict__ rects, uint32_t* __restrict__ depth_keys,
-	uint32_t* __restrict__ order, uint32_t* __restrict__ hist) {
+	uint32_t* __restrict__ order, int passes, uint32_t* __restrict__ hist) {
 	__shared__ uint32_t s_hist[kMaxPasses][kRadix];
 #pragma unroll
 	for (int p = 0; p < kMaxPasses; p++) s_hist[p][threadIdx.x] = 0;
@@ -506,9 +506,9 @@ __global__ __launch_bounds__(kThreads) void prepare_kernel(
 			depth_keys[i] = key;
 			order[i] = (uint32_t)i;
 		}
-		count_digits(key, valid, kMaxPasses, kRadixBits, s_hist);
+		count_digits(key, valid, passes, kRadixBits, s_hist);
 	}
-	flush_digits(kMaxPasses, s_hist, hist);
+	flush_digits(passes, s_hist, hist);
 }
 
 // q = a / b, r = a % b: a float quotient estimate, within one of a / b for a < 2^22, corrected
@@ -657,6 +657,134 @@ __global__ __launch_bounds__(kThreads) void ranges_kernel(int64_t num_pairs, con
 }
 
 // ---------------------------------------------------------------------------------------------
+// Depth order inside each tile (the tile-order binning). The pairs were emitted in gaussian-index
+// order and sorted by tile alone, so every tile's list holds the right gaussians in index order;
+// one work-group per tile sorts it by the key (depth bits << 32 | gaussian id), which is the
+// reference's (tile, depth bits, index) order restricted to the tile. Lists of up to 2048 pairs
+// are sorted by a bitonic network with E = 256..2048 / 256 keys per thread in registers: strides
+// inside a thread's E keys are register swaps, strides inside a wave lane shuffles, and only the
+// strides that cross waves (three stages) go through LDS. Lists of up to kTileSortMax pairs take
+// the same network entirely in LDS; longer ones are left in index order and flagged (bit 1 of
+// *overflow), and the caller bins the frame again with the global depth sort.
+// ---------------------------------------------------------------------------------------------
+
+constexpr int kTileSortRegMax = 2048;
+constexpr int kTileSortMax = 4096;
+
+__device__ inline uint64_t tile_sort_key(const int* vals, int i, int n, const uint32_t* __restrict__ depth_keys,
+										 int64_t n_gaussians) {
+	if (i >= n) return ~0ull;  // padding sorts last
+	const uint32_t g = (uint32_t)vals[i];
+	const uint32_t d = g < (uint64_t)n_gaussians ? depth_keys[g] : 0xffffffffu;
+	return ((uint64_t)d << 32) | g;
+}
+
+__device__ inline uint64_t shfl_xor_u64(uint64_t v, int mask) {
+	const int lo = __shfl_xor((int)(uint32_t)v, mask, HDS_WAVE);
+	const int hi = __shfl_xor((int)(uint32_t)(v >> 32), mask, HDS_WAVE);
+	return ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo;
+}
+
+// The element of a bitonic compare-exchange at index i whose partner holds p: the lower index of
+// the pair keeps the smaller key in an ascending block (i & k == 0), the larger in a descending one.
+__device__ inline uint64_t bitonic_keep(uint64_t v, uint64_t p, int i, int j, int k) {
+	const bool keep_min = ((i & j) == 0) == ((i & k) == 0);
+	return keep_min ? (v < p ? v : p) : (v > p ? v : p);
+}
+
+// n <= 256 * E; thread t holds keys t * E .. t * E + E - 1 (blocked).
+template <int E>
+__device__ void tile_sort_registers(uint64_t* s_keys, int* vals, int n, const uint32_t* __restrict__ depth_keys,
+									int64_t n_gaussians) {
+	constexpr int M = kThreads * E;
+	const int t = threadIdx.x;
+	uint64_t v[E];
+#pragma unroll
+	for (int e = 0; e < E; e++) v[e] = tile_sort_key(vals, t * E + e, n, depth_keys, n_gaussians);
+	for (int k = 2; k <= M; k <<= 1) {
+		for (int j = k >> 1; j >= E; j >>= 1) {
+			if (j >= HDS_WAVE * E) {
+				// The partner sits in another wave.
+				__syncthreads();
+#pragma unroll
+				for (int e = 0; e < E; e++) s_keys[t * E + e] = v[e];
+				__syncthreads();
+#pragma unroll
+				for (int e = 0; e < E; e++) v[e] = bitonic_keep(v[e], s_keys[(t * E + e) ^ j], t * E + e, j, k);
+			} else {
+				// Same slot e of lane t ^ (j / E).
+#pragma unroll
+				for (int e = 0; e < E; e++) v[e] = bitonic_keep(v[e], shfl_xor_u64(v[e], j / E), t * E + e, j, k);
+			}
+		}
+		// Strides below E: both keys in this thread's registers (compile-time indices).
+#pragma unroll
+		for (int jj = E / 2; jj > 0; jj >>= 1) {
+			if (jj < k) {
+#pragma unroll
+				for (int e = 0; e < E; e++) {
+					if ((e & jj) == 0) {
+						const bool ascending = ((t * E + e) & k) == 0;
+						const uint64_t a = v[e], b = v[e | jj];
+						const bool swap = (a > b) == ascending;
+						v[e] = swap ? b : a;
+						v[e | jj] = swap ? a : b;
+					}
+				}
+			}
+		}
+	}
+#pragma unroll
+	for (int e = 0; e < E; e++)
+		if (t * E + e < n) vals[t * E + e] = (int)(uint32_t)v[e];
+}
+
+// n <= kTileSortMax: the network over the next power of two, all in LDS.
+__device__ void tile_sort_lds(uint64_t* s_keys, int* vals, int n, const uint32_t* __restrict__ depth_keys,
+							  int64_t n_gaussians) {
+	int m = kThreads;
+	while (m < n) m <<= 1;
+	for (int i = threadIdx.x; i < m; i += kThreads) s_keys[i] = tile_sort_key(vals, i, n, depth_keys, n_gaussians);
+	__syncthreads();
+	for (int k = 2; k <= m; k <<= 1) {
+		for (int j = k >> 1; j > 0; j >>= 1) {
+			for (int q = threadIdx.x; q < (m >> 1); q += kThreads) {
+				const int i = 2 * j * (q / j) + (q % j);  // lower index of the pair (bit j clear)
+				const uint64_t a = s_keys[i], b = s_keys[i + j];
+				const bool swap = (a > b) == ((i & k) == 0);
+				if (swap) {
+					s_keys[i] = b;
+					s_keys[i + j] = a;
+				}
+			}
+			__syncthreads();
+		}
+	}
+	for (int i = threadIdx.x; i < n; i += kThreads) vals[i] = (int)(uint32_t)s_keys[i];
+}
+
+__global__ __launch_bounds__(kThreads) void tile_sort_kernel(const int2* __restrict__ ranges, int* __restrict__ values,
+															 const uint32_t* __restrict__ depth_keys, int64_t n_gaussians,
+															 int64_t num_tiles, uint32_t* __restrict__ overflow) {
+	__shared__ uint64_t s_keys[kTileSortMax];
+	const int64_t tile = blockIdx.x;
+	if (tile >= num_tiles) return;
+	const int2 r = ranges[tile];
+	const int n = r.y - r.x;
+	if (n <= 1) return;
+	if (n > kTileSortMax) {
+		if (threadIdx.x == 0) atomicOr(overflow, 2u);
+		return;
+	}
+	int* vals = values + r.x;
+	if (n <= 256) tile_sort_registers<1>(s_keys, vals, n, depth_keys, n_gaussians);
+	else if (n <= 512) tile_sort_registers<2>(s_keys, vals, n, depth_keys, n_gaussians);
+	else if (n <= 1024) tile_sort_registers<4>(s_keys, vals, n, depth_keys, n_gaussians);
+	else if (n <= kTileSortRegMax) tile_sort_registers<8>(s_keys, vals, n, depth_keys, n_gaussians);
+	else tile_sort_lds(s_keys, vals, n, depth_keys, n_gaussians);
+}
+
+// ---------------------------------------------------------------------------------------------
 // Workspace layouts. Every region is 256-byte aligned; [ctrl, bytes) is zeroed before use.
 // ---------------------------------------------------------------------------------------------
 
@@ -667,7 +795,8 @@ inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 struct Control {
 	uint64_t total;
 	uint32_t error;       // a look-back of the depth sort or the scan gave up
-	uint32_t pair_error;  // (gaussian workspace) a look-back of the pair sort gave up
+	uint32_t pair_error;  // (gaussian workspace) bit 0: a look-back of the pair sort gave up;
+						  // bit 1: a tile-order binning met a tile beyond kTileSortMax pairs
 	uint32_t tickets[kMaxPasses + 1];  // one per radix pass, then the scan's
 	uint32_t hist[kMaxPasses * kHistWords];
 };
@@ -747,7 +876,8 @@ namespace {
 // false when there was nothing to enqueue (n == 0).
 int bin_count_launch(int64_t n, const float* means2D, const float* depths, const float* radii, const float* conics,
 					 const float* colors, const float* opacities, int width, int height, float* conic4,
-					 float* color_opacity4, void* workspace, size_t workspace_bytes, hipStream_t s, bool* launched) {
+					 float* color_opacity4, void* workspace, size_t workspace_bytes, bool depth_sort, hipStream_t s,
+					 bool* launched) {
 	*launched = false;
 	HDS_REQUIRE(n >= 0 && n < INT32_MAX, "bin_count: gaussian count %lld outside [0, 2^31)", (long long)n);
 	HDS_REQUIRE(width > 0 && height > 0, "bin_count: image size %dx%d must be positive", width, height);
@@ -782,16 +912,20 @@ int bin_count_launch(int64_t n, const float* means2D, const float* depths, const
 	HdsKernelTimer timer2("prepare_kernel", s);
 	prepare_kernel<<<hds_blocks(n, 4 * kThreads), kThreads, 0, s>>>(
 		n, means2D, depths, radii, conics, colors, opacities, tiles_x, tiles_y, reinterpret_cast<float4*>(conic4),
-		reinterpret_cast<float4*>(color_opacity4), rects, keys_a, vals_a, ctrl->hist);
+		reinterpret_cast<float4*>(color_opacity4), rects, keys_a, vals_a, depth_sort ? kMaxPasses : 0, ctrl->hist);
 	timer2.stop();
 	HDS_LAUNCH_CHECK("prepare_gaussians", s);
-	// 4 passes: the depth order ends back in (keys_a, vals_a); the last one also writes each
-	// entry's tile rectangle to rects_sorted.
-	int st = onesweep_sort(keys_a, vals_a, keys_b, vals_b, n, nullptr, kMaxPasses, kRadixBits, ctrl->hist, status, ctrl->tickets,
-						   &ctrl->error, false, rects, rects_sorted, s);
-	if (st != HDS_OK) return st;
+	if (depth_sort) {
+		// 4 passes: the depth order ends back in (keys_a, vals_a); the last one also writes each
+		// entry's tile rectangle to rects_sorted.
+		int st = onesweep_sort(keys_a, vals_a, keys_b, vals_b, n, nullptr, kMaxPasses, kRadixBits, ctrl->hist, status,
+							   ctrl->tickets, &ctrl->error, false, rects, rects_sorted, s);
+		if (st != HDS_OK) return st;
+	}
+	// Without the depth sort (tile order) the entries stay in index order: vals_a = identity,
+	// keys_a = each gaussian's depth key, and the scan and the emit read the rectangles as prepared.
 	HdsKernelTimer timer3("scan_kernel", s);
-	scan_kernel<<<(unsigned)parts_of(n), kThreads, 0, s>>>(rects_sorted, n, offsets, scan_status,
+	scan_kernel<<<(unsigned)parts_of(n), kThreads, 0, s>>>(depth_sort ? rects_sorted : rects, n, offsets, scan_status,
 															ctrl->tickets + kMaxPasses, &ctrl->error,
 															g_spin_limit.load(std::memory_order_relaxed), &ctrl->total);
 	timer3.stop();
@@ -813,7 +947,7 @@ const CountWords* count_words(const void* workspace, int64_t n) {
 
 // Enqueues the emitting half. With exact, num_pairs is the pair count; otherwise it is the
 // capacity the buffers were sized for and the kernels take min(count in the workspace, capacity).
-int bin_emit_launch(int64_t n, int64_t num_pairs, bool exact, int width, int height, void* workspace,
+int bin_emit_launch(int64_t n, int64_t num_pairs, bool exact, bool tile_order, int width, int height, void* workspace,
 					void* pairs_workspace, size_t pairs_workspace_bytes, int32_t* values_sorted, int32_t* tile_ranges,
 					hipStream_t s) {
 	HDS_REQUIRE(width > 0 && height > 0, "bin_emit: image size %dx%d must be positive", width, height);
@@ -839,7 +973,7 @@ int bin_emit_launch(int64_t n, int64_t num_pairs, bool exact, int width, int hei
 	const uint64_t* total = exact ? nullptr : &count_words(workspace, n)->total;
 	const uint32_t* offsets = at<uint32_t>(ws, g.offsets);
 	const uint32_t* order = at<uint32_t>(ws, g.vals_a);
-	const uint2* rects_sorted = at<uint2>(ws, g.rects_sorted);
+	const uint2* rects_sorted = at<uint2>(ws, tile_order ? g.rects : g.rects_sorted);
 
 	uint32_t* keys_a = at<uint32_t>(pairs_workspace, p.keys_a);
 	uint32_t* keys_b = at<uint32_t>(pairs_workspace, p.keys_b);
@@ -878,6 +1012,14 @@ int bin_emit_launch(int64_t n, int64_t num_pairs, bool exact, int width, int hei
 		reinterpret_cast<int2*>(tile_ranges));
 	timer3.stop();
 	HDS_LAUNCH_CHECK("identify_tile_ranges", s);
+	if (tile_order) {
+		HdsKernelTimer timer4("tile_sort_kernel", s);
+		tile_sort_kernel<<<(unsigned)num_tiles, kThreads, 0, s>>>(
+			reinterpret_cast<const int2*>(tile_ranges), values_sorted, at<uint32_t>(ws, g.keys_a), n, num_tiles,
+			&at<Control>(ws, g.ctrl)->pair_error);
+		timer4.stop();
+		HDS_LAUNCH_CHECK("tile_depth_order", s);
+	}
 	return HDS_OK;
 }
 
@@ -892,7 +1034,7 @@ extern "C" int hds_bin_count(int64_t n, const float* means2D, const float* depth
 	hipStream_t s = (hipStream_t)stream;
 	bool launched = false;
 	int st = bin_count_launch(n, means2D, depths, radii, conics, colors, opacities, width, height, conic4,
-							  color_opacity4, workspace, workspace_bytes, s, &launched);
+							  color_opacity4, workspace, workspace_bytes, true, s, &launched);
 	if (st != HDS_OK || !launched) return st;
 	CountWords host = {0, 0, 0};
 	HDS_HIP(hipMemcpyAsync(&host, count_words(workspace, n), sizeof(host), hipMemcpyDeviceToHost, s));
@@ -905,15 +1047,17 @@ extern "C" int hds_bin_count(int64_t n, const float* means2D, const float* depth
 	return HDS_OK;
 }
 
-extern "C" int hds_bin_count_async(int64_t n, const float* means2D, const float* depths, const float* radii,
-								   const float* conics, const float* colors, const float* opacities, int width,
-								   int height, float* conic4, float* color_opacity4, void* workspace,
-								   size_t workspace_bytes, void* count_host, hds_stream_t stream) {
+namespace {
+
+int bin_count_async(int64_t n, const float* means2D, const float* depths, const float* radii, const float* conics,
+					const float* colors, const float* opacities, int width, int height, float* conic4,
+					float* color_opacity4, void* workspace, size_t workspace_bytes, void* count_host, bool depth_sort,
+					hds_stream_t stream) {
 	HDS_REQUIRE(count_host, "bin_count_async: count_host must not be NULL");
 	hipStream_t s = (hipStream_t)stream;
 	bool launched = false;
 	int st = bin_count_launch(n, means2D, depths, radii, conics, colors, opacities, width, height, conic4,
-							  color_opacity4, workspace, workspace_bytes, s, &launched);
+							  color_opacity4, workspace, workspace_bytes, depth_sort, s, &launched);
 	if (st != HDS_OK) return st;
 	if (!launched) {
 		// Nothing enqueued: the count is known now.
@@ -922,6 +1066,25 @@ extern "C" int hds_bin_count_async(int64_t n, const float* means2D, const float*
 	}
 	HDS_HIP(hipMemcpyAsync(count_host, count_words(workspace, n), sizeof(CountWords), hipMemcpyDeviceToHost, s));
 	return HDS_OK;
+}
+
+}  // namespace
+
+extern "C" int hds_bin_count_async(int64_t n, const float* means2D, const float* depths, const float* radii,
+								   const float* conics, const float* colors, const float* opacities, int width,
+								   int height, float* conic4, float* color_opacity4, void* workspace,
+								   size_t workspace_bytes, void* count_host, hds_stream_t stream) {
+	return bin_count_async(n, means2D, depths, radii, conics, colors, opacities, width, height, conic4,
+						   color_opacity4, workspace, workspace_bytes, count_host, true, stream);
+}
+
+extern "C" int hds_bin_count_tile_order_async(int64_t n, const float* means2D, const float* depths,
+											  const float* radii, const float* conics, const float* colors,
+											  const float* opacities, int width, int height, float* conic4,
+											  float* color_opacity4, void* workspace, size_t workspace_bytes,
+											  void* count_host, hds_stream_t stream) {
+	return bin_count_async(n, means2D, depths, radii, conics, colors, opacities, width, height, conic4,
+						   color_opacity4, workspace, workspace_bytes, count_host, false, stream);
 }
 
 extern "C" int hds_bin_status(int64_t n, const void* workspace, void* status_host, hds_stream_t stream) {
@@ -944,14 +1107,28 @@ extern "C" int hds_set_lookback_limit(uint32_t polls) {
 extern "C" int hds_bin_emit(int64_t n, int64_t num_pairs, int width, int height, void* workspace,
 							void* pairs_workspace, size_t pairs_workspace_bytes, int32_t* values_sorted,
 							int32_t* tile_ranges, hds_stream_t stream) {
-	return bin_emit_launch(n, num_pairs, true, width, height, workspace, pairs_workspace, pairs_workspace_bytes,
+	return bin_emit_launch(n, num_pairs, true, false, width, height, workspace, pairs_workspace, pairs_workspace_bytes,
 						   values_sorted, tile_ranges, (hipStream_t)stream);
 }
 
 extern "C" int hds_bin_emit_capped(int64_t n, int64_t capacity, int width, int height, void* workspace,
 								   void* pairs_workspace, size_t pairs_workspace_bytes, int32_t* values_sorted,
 								   int32_t* tile_ranges, hds_stream_t stream) {
-	return bin_emit_launch(n, capacity, false, width, height, workspace, pairs_workspace, pairs_workspace_bytes,
+	return bin_emit_launch(n, capacity, false, false, width, height, workspace, pairs_workspace, pairs_workspace_bytes,
+						   values_sorted, tile_ranges, (hipStream_t)stream);
+}
+
+extern "C" int hds_bin_emit_tile_order(int64_t n, int64_t num_pairs, int width, int height, void* workspace,
+									   void* pairs_workspace, size_t pairs_workspace_bytes, int32_t* values_sorted,
+									   int32_t* tile_ranges, hds_stream_t stream) {
+	return bin_emit_launch(n, num_pairs, true, true, width, height, workspace, pairs_workspace, pairs_workspace_bytes,
+						   values_sorted, tile_ranges, (hipStream_t)stream);
+}
+
+extern "C" int hds_bin_emit_tile_order_capped(int64_t n, int64_t capacity, int width, int height, void* workspace,
+											  void* pairs_workspace, size_t pairs_workspace_bytes,
+											  int32_t* values_sorted, int32_t* tile_ranges, hds_stream_t stream) {
+	return bin_emit_launch(n, capacity, false, true, width, height, workspace, pairs_workspace, pairs_workspace_bytes,
 						   values_sorted, tile_ranges, (hipStream_t)stream);
 }
 
@@ -1007,20 +1184,20 @@ extern "C" int hds_bin_static(int64_t n, const float* means2D, const float* dept
 	void* pws = static_cast<char*>(ptr) + align256(gaussian_bytes);
 	bool launched = false;
 	st = bin_count_launch(n, means2D, depths, radii, conics, colors, opacities, width, height, conic4, color_opacity4,
-						  ws, gaussian_bytes, s, &launched);
+						  ws, gaussian_bytes, true, s, &launched);
 	if (st != HDS_OK) return st;
 	if (!launched) {
 		// No gaussians: empty tile ranges and zero status words, from a zeroed control block.
 		const GaussianSpace g = gaussian_space(0);
 		zero_kernel<<<1, kThreads, 0, s>>>(at<uint32_t>(ws, g.ctrl), sizeof(CountWords) / 4, nullptr, 0);
 		HDS_LAUNCH_CHECK("zero_static_status", s);
-		st = bin_emit_launch(0, 0, false, width, height, ws, pws, pair_bytes, values_sorted, tile_ranges, s);
+		st = bin_emit_launch(0, 0, false, false, width, height, ws, pws, pair_bytes, values_sorted, tile_ranges, s);
 		if (st != HDS_OK) return st;
 		HDS_HIP(hipMemcpyAsync(status, count_words(ws, 0), sizeof(CountWords), hipMemcpyDefault, s));
 		return HDS_OK;
 	}
 	HDS_REQUIRE(capacity == 0 || values_sorted, "bin_static: null values_sorted");
-	st = bin_emit_launch(n, capacity, false, width, height, ws, pws, pair_bytes, values_sorted, tile_ranges, s);
+	st = bin_emit_launch(n, capacity, false, false, width, height, ws, pws, pair_bytes, values_sorted, tile_ranges, s);
 	if (st != HDS_OK) return st;
 	HDS_HIP(hipMemcpyAsync(status, count_words(ws, n), sizeof(CountWords), hipMemcpyDefault, s));
 	return HDS_OK;

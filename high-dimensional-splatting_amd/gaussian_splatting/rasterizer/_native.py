@@ -46,6 +46,10 @@ PROTOTYPES = {
     "hds_pairs_workspace_bytes": (_sz, [_i64, _i32, _i32]),
     "hds_bin_emit": (_i32, [_i64, _i64, _i32, _i32, _vp, _vp, _sz, _vp, _vp, _vp]),
     "hds_bin_emit_capped": (_i32, [_i64, _i64, _i32, _i32, _vp, _vp, _sz, _vp, _vp, _vp]),
+    "hds_bin_count_tile_order_async": (_i32, [_i64, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _vp, _vp, _vp, _sz,
+                                              _vp, _vp]),
+    "hds_bin_emit_tile_order": (_i32, [_i64, _i64, _i32, _i32, _vp, _vp, _sz, _vp, _vp, _vp]),
+    "hds_bin_emit_tile_order_capped": (_i32, [_i64, _i64, _i32, _i32, _vp, _vp, _sz, _vp, _vp, _vp]),
     "hds_bin_status": (_i32, [_i64, _vp, _vp, _vp]),
     "hds_set_lookback_limit": (_i32, [ctypes.c_uint32]),
     "hds_bin_static": (_i32, [_i64, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _vp, _vp, _i64, _vp, _vp, _vp, _vp]),
@@ -200,14 +204,17 @@ class StageTimer:
         return out
 
 
-def _raise_on_sort_error(status: torch.Tensor) -> None:
-    """Raises if the (pair count, depth/scan flag | pair-sort flag << 32) words of hds_bin_status
-    report a look-back that gave up."""
+def _raise_on_sort_error(status: torch.Tensor) -> bool:
+    """Raises if the (pair count, depth/scan flag | tile-sort word << 32) words of hds_bin_status
+    report a look-back that gave up; returns whether a tile-order binning met a tile list longer
+    than its per-tile sort takes (bit 1 of the tile-sort word)."""
     word = int(status[1])
     if word & 0xFFFFFFFF:
         raise RuntimeError("bin_count: a sort or scan look-back did not complete")
-    if (word >> 32) & 0xFFFFFFFF:
+    pair_word = (word >> 32) & 0xFFFFFFFF
+    if pair_word & 1:
         raise RuntimeError("bin_emit: a look-back of the tile sort did not complete (every tile range left empty)")
+    return bool(pair_word & 2)
 
 
 def _debug_pairs(n: int, width: int, height: int, pairs: int) -> None:
@@ -237,6 +244,8 @@ class PendingBins:
         self.count = count              # pinned int64 [2]: pair count, look-back error flag
         self.workspace = workspace      # per-gaussian workspace the exact re-emit reads
         self.emit_args = emit_args      # (n, width, height, device)
+        self.tile_order = False         # binned by hds_bin_count_tile_order_async
+        self.inputs = None              # the binning inputs, for a rebin with the global depth sort
         self.status = status            # pinned int64 [2] of hds_bin_status after the capped emit
         self.status_event = status_event  # recorded after that copy
 
@@ -246,11 +255,19 @@ class HipRasterizer:
 
     # Pair buffers of bin_async are sized this much above the last pair count seen on the device.
     PAIR_HEADROOM = 1.25
+    # Longest tile list the tile-order binning sorts (hds_bin_count_tile_order_async), and the share
+    # of it the last frame's longest list may reach for bin_async to choose that binning.
+    TILE_ORDER_MAX = 4096
+    TILE_ORDER_MARGIN = 0.9
 
     def __init__(self) -> None:
         self.lib = load_library()
         self.timer: StageTimer | None = None
         self._pair_capacity: dict[int, int] = {}
+        # Per device: whether bin_async bins in tile order (set from the first frame's longest tile
+        # list, cleared for good when a frame's list overflows). `tile_order` forces the choice.
+        self._tile_order_ok: dict[int, bool] = {}
+        self.tile_order: bool | None = None
 
     def gradient_buffers(self, n: int, channels: int, device: torch.device):
         """Output buffers for a later render_backward (grad_means2D [N,2], grad_conics [N,3],
@@ -378,13 +395,20 @@ class HipRasterizer:
         sized from the last pair count seen on this device and the count reaches the host by an
         asynchronous copy, so the render can be enqueued before the host knows P. `resolve` then
         reads P, and rebins exactly when the capacity was too small. The first call on a device
-        has no history and bins synchronously."""
+        has no history and bins synchronously. Later calls bin in tile order (no global depth sort,
+        each tile's list ordered by depth in LDS; the same values_sorted and tile_ranges) while the
+        device's longest tile list stays within TILE_ORDER_MARGIN of what that takes, else with
+        the global depth sort."""
         dev = means2D.device
         if dev.index not in self._pair_capacity:
             values, ranges, conic4, color_opacity4 = self.bin(means2D, depths, radii, conics, colors, opacities,
                                                               width, height)
             self._remember_pairs(dev, values.numel())
+            longest = int((ranges[:, 1] - ranges[:, 0]).max()) if ranges.numel() else 0
+            self._tile_order_ok[dev.index] = longest <= self.TILE_ORDER_MARGIN * self.TILE_ORDER_MAX
             return PendingBins(values, ranges, conic4, color_opacity4)
+        tile_order = self.tile_order if self.tile_order is not None else self._tile_order_ok.get(dev.index, False)
+        inputs = (means2D, depths, radii, conics, colors, opacities)
         means2D, depths, radii = _dev(means2D, "means2D"), _dev(depths, "depths"), _dev(radii, "radii")
         conics, opacities = _dev(conics, "conics"), _dev(opacities, "opacities")
         colors = None if colors is None else _dev(colors, "colors")
@@ -399,28 +423,34 @@ class HipRasterizer:
         with torch.cuda.device(dev):
             stream = _stream(dev)
             ws = torch.empty(self.lib.hds_bin_workspace_bytes(n, width, height), device=dev, dtype=torch.uint8)
-            self._run("bin_count", lambda: self.lib.hds_bin_count_async(
+            count_entry = self.lib.hds_bin_count_tile_order_async if tile_order else self.lib.hds_bin_count_async
+            self._run("bin_count", lambda: count_entry(
                 n, _ptr(means2D), _ptr(depths), _ptr(radii), _ptr(conics), _ptr(colors), _ptr(opacities), width,
                 height, _ptr(conic4), _ptr(color_opacity4), _ptr(ws), ws.numel(), _ptr(count), stream))
             event = torch.cuda.Event()
             event.record()
             values = torch.empty((cap,), device=dev, dtype=torch.int32)
             pws = torch.empty(self.lib.hds_pairs_workspace_bytes(cap, width, height), device=dev, dtype=torch.uint8)
-            self._run("bin_emit", lambda: self.lib.hds_bin_emit_capped(
+            emit_entry = self.lib.hds_bin_emit_tile_order_capped if tile_order else self.lib.hds_bin_emit_capped
+            self._run("bin_emit", lambda: emit_entry(
                 n, cap, width, height, _ptr(ws), _ptr(pws), pws.numel(), _ptr(values), _ptr(tile_ranges), stream))
             status = torch.zeros(2, dtype=torch.int64, pin_memory=True)
             _check(self.lib.hds_bin_status(n, _ptr(ws), _ptr(status), stream))
             status_event = torch.cuda.Event()
             status_event.record()
-        return PendingBins(values, tile_ranges, conic4, color_opacity4, capacity=cap, event=event, count=count,
-                           workspace=ws, emit_args=(n, width, height, dev), status=status,
-                           status_event=status_event)
+        pending = PendingBins(values, tile_ranges, conic4, color_opacity4, capacity=cap, event=event, count=count,
+                              workspace=ws, emit_args=(n, width, height, dev), status=status,
+                              status_event=status_event)
+        pending.tile_order, pending.inputs = tile_order, inputs
+        return pending
 
     def resolve(self, pending: PendingBins) -> bool:
         """Reads the pair count of a bin_async binning (waiting for its copy only, not for later
         work on the stream) and trims `pending.values` to it. If the count exceeded the capacity,
         bins again with exact buffers and returns True: whatever was rendered from the capped
-        binning must be rendered again."""
+        binning must be rendered again. So does a tile-order binning that met a tile list too long
+        for its per-tile sort: the frame is binned again with the global depth sort (into the same
+        tile_ranges, conic4 and color_opacity4), and the device stays on that binning."""
         if pending.capacity is None:
             return False
         pending.event.synchronize()
@@ -432,27 +462,53 @@ class HipRasterizer:
             raise RuntimeError("bin_count: a sort or scan look-back did not complete")
         # The capped emit's pair sort (its copy of the flags follows the sort, ahead of the render).
         pending.status_event.synchronize()
-        _raise_on_sort_error(pending.status)
+        overflow = _raise_on_sort_error(pending.status)
         if total >= 2**31 - 1:
             raise RuntimeError(f"bin_count: {total} tile-gaussian pairs overflow int32 indices")
         _debug_pairs(n, width, height, total)
         self._remember_pairs(dev, total)
-        if total <= cap:
+        if total <= cap and not overflow:
             pending.values = pending.values[:total]
             return False
         values = torch.empty((total,), device=dev, dtype=torch.int32)
         with torch.cuda.device(dev):
             pws = torch.empty(self.lib.hds_pairs_workspace_bytes(total, width, height), device=dev,
                               dtype=torch.uint8)
-            self._run("bin_emit", lambda: self.lib.hds_bin_emit(
-                n, total, width, height, _ptr(pending.workspace), _ptr(pws), pws.numel(), _ptr(values),
-                _ptr(pending.tile_ranges), _stream(dev)))
-            status = torch.zeros(2, dtype=torch.int64, pin_memory=True)
-            _check(self.lib.hds_bin_status(n, _ptr(pending.workspace), _ptr(status), _stream(dev)))
-            torch.cuda.current_stream(dev).synchronize()
-            _raise_on_sort_error(status)
+            if not overflow:
+                emit = self.lib.hds_bin_emit_tile_order if pending.tile_order else self.lib.hds_bin_emit
+                self._run("bin_emit", lambda: emit(
+                    n, total, width, height, _ptr(pending.workspace), _ptr(pws), pws.numel(), _ptr(values),
+                    _ptr(pending.tile_ranges), _stream(dev)))
+                status = torch.zeros(2, dtype=torch.int64, pin_memory=True)
+                _check(self.lib.hds_bin_status(n, _ptr(pending.workspace), _ptr(status), _stream(dev)))
+                torch.cuda.current_stream(dev).synchronize()
+                overflow = _raise_on_sort_error(status)
+            if overflow:
+                self._tile_order_ok[dev.index] = False
+                self._rebin_depth_order(pending, values, pws)
         pending.values = values
         return True
+
+    def _rebin_depth_order(self, pending: PendingBins, values: torch.Tensor, pws: torch.Tensor) -> None:
+        """Bins pending's frame again with the global depth sort, into `values` (exact P) and the
+        pending tile_ranges, conic4 and color_opacity4."""
+        n, width, height, dev = pending.emit_args
+        means2D, depths, radii, conics, colors, opacities = pending.inputs
+        ws = torch.empty(self.lib.hds_bin_workspace_bytes(n, width, height), device=dev, dtype=torch.uint8)
+        total = ctypes.c_int64(0)
+        self._run("bin_count", lambda: self.lib.hds_bin_count(
+            n, _ptr(means2D), _ptr(depths), _ptr(radii), _ptr(conics), _ptr(colors), _ptr(opacities), width, height,
+            _ptr(pending.conic4), _ptr(pending.color_opacity4), _ptr(ws), ws.numel(), ctypes.byref(total),
+            _stream(dev)))
+        if total.value != values.numel():
+            raise RuntimeError(f"bin_count: {total.value} pairs on the rebin against {values.numel()} counted")
+        self._run("bin_emit", lambda: self.lib.hds_bin_emit(
+            n, total.value, width, height, _ptr(ws), _ptr(pws), pws.numel(), _ptr(values), _ptr(pending.tile_ranges),
+            _stream(dev)))
+        status = torch.zeros(2, dtype=torch.int64, pin_memory=True)
+        _check(self.lib.hds_bin_status(n, _ptr(ws), _ptr(status), _stream(dev)))
+        torch.cuda.current_stream(dev).synchronize()
+        _raise_on_sort_error(status)
 
     def _remember_pairs(self, dev: torch.device, pairs: int) -> None:
         chunk = 4096

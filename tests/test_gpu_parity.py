@@ -217,12 +217,14 @@ def test_empty_scene_renders_background():
     assert int(n_contrib.abs().sum()) == 0 and values.numel() == 0 and int(ranges.abs().sum()) == 0
 
 
+@pytest.mark.parametrize("order", ["depth", "tile"])
 @pytest.mark.parametrize("capacity", ["exact", "short", "tiny", "roomy"])
-def test_async_binning_equals_the_oracle_whatever_the_capacity(capacity):
+def test_async_binning_equals_the_oracle_whatever_the_capacity(capacity, order):
     """bin_async + resolve (the autograd path: render enqueued before the host reads P) gives the
     oracle's binning bit for bit when the pair buffers are exactly P, a partition short of P (the
-    capped sort runs, then resolve rebins exactly), far too small, or larger than P; the render
-    of a capped binning stays inside its buffers."""
+    capped sort runs, then resolve rebins exactly), far too small, or larger than P, with the
+    global depth sort and in tile order (depth order per tile); the render of a capped binning
+    stays inside its buffers."""
     from gaussian_splatting.rasterizer._native import HipRasterizer
 
     wl = synthetic_config(1, n=60_000, channels=1)
@@ -234,9 +236,11 @@ def test_async_binning_equals_the_oracle_whatever_the_capacity(capacity):
     cap = {"exact": p, "short": p - 4096, "tiny": 1, "roomy": p + 10_000}[capacity]
     ext = HipRasterizer()
     ext._pair_capacity[m2.device.index] = cap
+    ext.tile_order = order == "tile"
     colors = torch.rand(wl.n, 3, generator=torch.Generator().manual_seed(3)).to(DEV)
+    print(f"[test] async binning, capacity {capacity}, {order} order", file=sys.stderr, flush=True)
     bins = ext.bin_async(m2, d, r, c, colors, opac, wl.width, wl.height)
-    assert bins.values.numel() == cap
+    assert bins.values.numel() == cap and bins.tile_order == (order == "tile")
     _, _, T, _ = ext.render(m2, bins.conic4, bins.color_opacity4, bins.values, bins.tile_ranges, wl.width,
                             wl.height, torch.zeros(3, device=DEV))
     torch.cuda.synchronize()
@@ -248,11 +252,60 @@ def test_async_binning_equals_the_oracle_whatever_the_capacity(capacity):
     assert bool(torch.isfinite(T).all())
 
 
-def test_async_binning_of_a_scene_with_no_pairs():
+def _one_tile_scene(n, seed):
+    """n small gaussians whose footprints all lie inside tile 0 of a 64x64 image (one list of n
+    pairs), with depths drawn from 50 values so that ties occur."""
+    g = torch.Generator().manual_seed(seed)
+    means2D = 5.0 + torch.rand(n, 2, generator=g) * 6.0
+    depths = torch.randint(0, 50, (n,), generator=g).float() * 0.25 + 1.0
+    conics = torch.tensor([[0.5, 0.0, 0.5]]).repeat(n, 1)
+    return means2D, depths, torch.ones(n), conics, torch.full((n, 1), 0.5)
+
+
+@pytest.mark.parametrize("n", [3000, 5000])
+def test_tile_order_binning_sorts_long_lists_in_lds_and_hands_longer_ones_back(n):
+    """A tile of 3000 pairs (beyond the register network, sorted in LDS) bins bit for bit like the
+    oracle in tile order; one of 5000 pairs (beyond the per-tile sort) is flagged, resolve bins the
+    frame again with the global depth sort (same result) and the device leaves tile order."""
+    from gaussian_splatting.rasterizer._native import HipRasterizer
+
+    means2D, depths, radii, conics, opac = _one_tile_scene(n, 9)
+    _, want_values, want_ranges = oracle.bin_gaussians(np_(means2D), np_(depths), np_(radii), np_(conics),
+                                                       np_(opac), 64, 64)
+    assert int(want_ranges[0, 1] - want_ranges[0, 0]) == n
+    ext = HipRasterizer()
+    dev = torch.device(DEV, torch.cuda.current_device())
+    ext._pair_capacity[dev.index] = n + 8192
+    ext._tile_order_ok[dev.index] = True
+    print(f"[test] tile-order binning, one tile of {n} pairs", file=sys.stderr, flush=True)
+    bins = ext.bin_async(means2D.to(DEV), depths.to(DEV), radii.to(DEV), conics.to(DEV), None, opac.to(DEV), 64, 64)
+    assert bins.tile_order
+    rebinned = ext.resolve(bins)
+    assert rebinned == (n > ext.TILE_ORDER_MAX)
+    assert ext._tile_order_ok[dev.index] == (n <= ext.TILE_ORDER_MAX)
+    np.testing.assert_array_equal(np_(bins.values), want_values)
+    np.testing.assert_array_equal(np_(bins.tile_ranges), want_ranges)
+
+
+def test_first_binning_chooses_the_order_from_the_longest_tile_list():
+    """bin_async's first (synchronous) call on a device picks tile order for later calls when the
+    longest tile list leaves room in the per-tile sort, and the global depth sort when it does not."""
+    from gaussian_splatting.rasterizer._native import HipRasterizer
+
+    for n, want in ((1000, True), (4000, False)):
+        means2D, depths, radii, conics, opac = _one_tile_scene(n, 10)
+        ext = HipRasterizer()
+        ext.bin_async(means2D.to(DEV), depths.to(DEV), radii.to(DEV), conics.to(DEV), None, opac.to(DEV), 64, 64)
+        assert ext._tile_order_ok[torch.cuda.current_device()] == want
+
+
+@pytest.mark.parametrize("tile_order", [False, True])
+def test_async_binning_of_a_scene_with_no_pairs(tile_order):
     from gaussian_splatting.rasterizer._native import HipRasterizer
 
     ext = HipRasterizer()
     ext._pair_capacity[0] = 8192
+    ext.tile_order = tile_order
     n = 500
     means2D = torch.rand(n, 2, device=DEV) * 40
     bins = ext.bin_async(means2D, torch.ones(n, device=DEV), torch.zeros(n, device=DEV),
