@@ -8,7 +8,9 @@
 //      (ceil(log2 T) bits: 12 at 979x546, so 2 passes of 6 bits instead of 6 passes of 8).
 // Stability of both sorts gives exactly the reference's (tile, depth bits, index) order, so
 // values_sorted and tile_ranges equal the CPU oracle's bit for bit, and the pair sort moves
-// 8 B per pair and pass instead of 12. Everything is integer work; the only floating point is the
+// 8 B per pair and pass instead of 12. The tile-order variant (the autograd path) skips step 1:
+// the pairs are emitted in index order, sorted by tile, and each tile's list is then sorted by
+// (depth bits, index) in one work-group (tile_sort_kernel), the same order again. Everything is integer work; the only floating point is the
 // shared tile rectangle of hds_common.h.
 //
 // Sorts and scans are single-pass: every radix pass is ONE launch in which each work-group ranks
