@@ -687,11 +687,11 @@ __device__ inline uint64_t shfl_xor_u64(uint64_t v, int mask) {
 	return ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo;
 }
 
-// The element of a bitonic compare-exchange at index i whose partner holds p: the lower index of
-// the pair keeps the smaller key in an ascending block (i & k == 0), the larger in a descending one.
-__device__ inline uint64_t bitonic_keep(uint64_t v, uint64_t p, int i, int j, int k) {
-	const bool keep_min = ((i & j) == 0) == ((i & k) == 0);
-	return keep_min ? (v < p ? v : p) : (v > p ? v : p);
+// One side of a bitonic compare-exchange: the element keeps the smaller of (v, partner p) when
+// keep_min (the pair's lower index in an ascending block, or its upper index in a descending one),
+// else the larger: it takes p exactly when (v > p) == keep_min. One 64-bit compare and two selects.
+__device__ inline uint64_t bitonic_keep(uint64_t v, uint64_t p, bool keep_min) {
+	return (v > p) == keep_min ? p : v;
 }
 
 // n <= 256 * E; thread t holds keys t * E .. t * E + E - 1 (blocked).
@@ -705,6 +705,8 @@ __device__ void tile_sort_registers(uint64_t* s_keys, int* vals, int n, const ui
 	for (int e = 0; e < E; e++) v[e] = tile_sort_key(vals, t * E + e, n, depth_keys, n_gaussians);
 	for (int k = 2; k <= M; k <<= 1) {
 		for (int j = k >> 1; j >= E; j >>= 1) {
+			// j >= E and k > j: bits j and k of t * E + e do not depend on e.
+			const bool keep_min = ((t * E & j) == 0) == ((t * E & k) == 0);
 			if (j >= HDS_WAVE * E) {
 				// The partner sits in another wave.
 				__syncthreads();
@@ -712,11 +714,11 @@ __device__ void tile_sort_registers(uint64_t* s_keys, int* vals, int n, const ui
 				for (int e = 0; e < E; e++) s_keys[t * E + e] = v[e];
 				__syncthreads();
 #pragma unroll
-				for (int e = 0; e < E; e++) v[e] = bitonic_keep(v[e], s_keys[(t * E + e) ^ j], t * E + e, j, k);
+				for (int e = 0; e < E; e++) v[e] = bitonic_keep(v[e], s_keys[(t * E + e) ^ j], keep_min);
 			} else {
 				// Same slot e of lane t ^ (j / E).
 #pragma unroll
-				for (int e = 0; e < E; e++) v[e] = bitonic_keep(v[e], shfl_xor_u64(v[e], j / E), t * E + e, j, k);
+				for (int e = 0; e < E; e++) v[e] = bitonic_keep(v[e], shfl_xor_u64(v[e], j / E), keep_min);
 			}
 		}
 		// Strides below E: both keys in this thread's registers (compile-time indices).
