@@ -112,11 +112,12 @@ def algorithmic_bytes(n: int, n_vis: int, pairs: int, hw: int, c: int) -> dict[s
     each output written once (gradient outputs counted once, not as zero-fill + read-modify-write).
     Binning: bin_count = the tile counts and their scan (12 B per gaussian); bin_emit = writing the
     pairs (12 B), one read + write of keys and values for a one-pass sort (24 B) and the range build's
-    read (8 B), per pair."""
+    read (8 B), per pair; bin = both, for the one-call tile-order binning."""
     return {
         "project_forward": 44 * n + 28 * n,
         "bin_count": 12 * n,
         "bin_emit": 44 * pairs,
+        "bin": 12 * n + 44 * pairs,
         "render": 4 * pairs + 36 * n_vis + 4 * c * n_vis + 20 * hw + 4 * c * hw,
         "render_backward": 20 * hw + 4 * pairs + 36 * n_vis + 4 * c * n_vis + 4 * c * hw + 4 * c * n + 36 * n,
         "project_backward": 60 * n + 40 * n,

@@ -474,13 +474,30 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const uint2* __restrict_
 
 // Cull, tile rectangle (its w * h is the tile count), packed records and depth key per gaussian
 // (forward.cu:13-61), plus the depth keys' four digit histograms for the sort.
+// Word ranges a kernel clears on the side (grid-stride over its whole grid), so that zeroing the
+// control blocks of a binning costs no launch of its own.
+struct ZeroRanges {
+	uint32_t* p[3];
+	int64_t n[3];
+};
+
+__device__ inline void zero_ranges(const ZeroRanges& z) {
+	const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+#pragma unroll
+	for (int k = 0; k < 3; k++)
+		for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < z.n[k]; i += stride) z.p[k][i] = 0u;
+}
+
 __global__ __launch_bounds__(kThreads) void prepare_kernel(
 	int64_t n, const float* __restrict__ means2D, const float* __restrict__ depths, const float* __restrict__ radii,
 	const float* __restrict__ conics, const float* __restrict__ colors, const float* __restrict__ opacities,
 	int tiles_x, int tiles_y, float4* __restrict__ conic4, float4* __restrict__ color_opacity4,
 	uint2* __restrict__ rects, uint32_t* __restrict__ depth_keys,
-	uint32_t* __restrict__ order, int passes, uint32_t* __restrict__ hist) {
+	uint32_t* __restrict__ order, int passes, uint32_t* __restrict__ hist, ZeroRanges zero) {
 	__shared__ uint32_t s_hist[kMaxPasses][kRadix];
+	// Control words the later kernels of this binning need cleared (none of them is touched here:
+	// with passes > 0 the histograms were cleared by a launch before this one).
+	zero_ranges(zero);
 #pragma unroll
 	for (int p = 0; p < kMaxPasses; p++) s_hist[p][threadIdx.x] = 0;
 	__syncthreads();
@@ -880,8 +897,8 @@ namespace {
 // false when there was nothing to enqueue (n == 0).
 int bin_count_launch(int64_t n, const float* means2D, const float* depths, const float* radii, const float* conics,
 					 const float* colors, const float* opacities, int width, int height, float* conic4,
-					 float* color_opacity4, void* workspace, size_t workspace_bytes, bool depth_sort, hipStream_t s,
-					 bool* launched) {
+					 float* color_opacity4, void* workspace, size_t workspace_bytes, bool depth_sort,
+					 const ZeroRanges* fused_zero, hipStream_t s, bool* launched) {
 	*launched = false;
 	HDS_REQUIRE(n >= 0 && n < INT32_MAX, "bin_count: gaussian count %lld outside [0, 2^31)", (long long)n);
 	HDS_REQUIRE(width > 0 && height > 0, "bin_count: image size %dx%d must be positive", width, height);
@@ -908,15 +925,24 @@ int bin_count_launch(int64_t n, const float* means2D, const float* depths, const
 	uint64_t* scan_status = at<uint64_t>(workspace, g.scan_status);
 
 	const int64_t zero_words = (int64_t)(g.bytes - g.ctrl) / 4;
-	HdsKernelTimer timer1("zero_kernel", s);
-	zero_kernel<<<hds_blocks(zero_words, kThreads), kThreads, 0, s>>>(at<uint32_t>(workspace, g.ctrl), zero_words,
-																	   nullptr, 0);
-	timer1.stop();
-	HDS_LAUNCH_CHECK("zero_sort_control", s);
+	ZeroRanges zero{};
+	if (fused_zero) {
+		// Without the depth sort prepare keeps no histograms, so it clears the control blocks itself.
+		HDS_REQUIRE(!depth_sort, "bin_count: fused zeroing needs the tile order");
+		zero = *fused_zero;
+		zero.p[0] = at<uint32_t>(workspace, g.ctrl);
+		zero.n[0] = zero_words;
+	} else {
+		HdsKernelTimer timer1("zero_kernel", s);
+		zero_kernel<<<hds_blocks(zero_words, kThreads), kThreads, 0, s>>>(at<uint32_t>(workspace, g.ctrl), zero_words,
+																		   nullptr, 0);
+		timer1.stop();
+		HDS_LAUNCH_CHECK("zero_sort_control", s);
+	}
 	HdsKernelTimer timer2("prepare_kernel", s);
 	prepare_kernel<<<hds_blocks(n, 4 * kThreads), kThreads, 0, s>>>(
 		n, means2D, depths, radii, conics, colors, opacities, tiles_x, tiles_y, reinterpret_cast<float4*>(conic4),
-		reinterpret_cast<float4*>(color_opacity4), rects, keys_a, vals_a, depth_sort ? kMaxPasses : 0, ctrl->hist);
+		reinterpret_cast<float4*>(color_opacity4), rects, keys_a, vals_a, depth_sort ? kMaxPasses : 0, ctrl->hist, zero);
 	timer2.stop();
 	HDS_LAUNCH_CHECK("prepare_gaussians", s);
 	if (depth_sort) {
@@ -953,7 +979,7 @@ const CountWords* count_words(const void* workspace, int64_t n) {
 // capacity the buffers were sized for and the kernels take min(count in the workspace, capacity).
 int bin_emit_launch(int64_t n, int64_t num_pairs, bool exact, bool tile_order, int width, int height, void* workspace,
 					void* pairs_workspace, size_t pairs_workspace_bytes, int32_t* values_sorted, int32_t* tile_ranges,
-					hipStream_t s) {
+					hipStream_t s, bool control_zeroed = false) {
 	HDS_REQUIRE(width > 0 && height > 0, "bin_emit: image size %dx%d must be positive", width, height);
 	HDS_REQUIRE(num_pairs >= 0 && num_pairs < INT32_MAX, "bin_emit: pair count %lld outside [0, 2^31)",
 				(long long)num_pairs);
@@ -996,11 +1022,13 @@ int bin_emit_launch(int64_t n, int64_t num_pairs, bool exact, bool tile_order, i
 	uint32_t* vals_b = (passes % 2 == 0) ? vals_tmp : out;
 
 	const int64_t ctrl_words = (int64_t)(p.bytes - p.ctrl) / 4;
-	HdsKernelTimer timer1("zero_kernel", s);
-	zero_kernel<<<hds_blocks(ctrl_words + 2 * num_tiles, kThreads), kThreads, 0, s>>>(
-		at<uint32_t>(pairs_workspace, p.ctrl), ctrl_words, ranges_words, 2 * num_tiles);
-	timer1.stop();
-	HDS_LAUNCH_CHECK("zero_sort_control", s);
+	if (!control_zeroed) {
+		HdsKernelTimer timer1("zero_kernel", s);
+		zero_kernel<<<hds_blocks(ctrl_words + 2 * num_tiles, kThreads), kThreads, 0, s>>>(
+			at<uint32_t>(pairs_workspace, p.ctrl), ctrl_words, ranges_words, 2 * num_tiles);
+		timer1.stop();
+		HDS_LAUNCH_CHECK("zero_sort_control", s);
+	}
 	HdsKernelTimer timer2("emit_kernel", s);
 	emit_kernel<<<hds_blocks(n, kThreads), kThreads, 0, s>>>(n, num_pairs, total, offsets, order, rects_sorted,
 																	tiles_x, passes, bits, keys_a, vals_a, ctrl->hist);
@@ -1038,7 +1066,7 @@ extern "C" int hds_bin_count(int64_t n, const float* means2D, const float* depth
 	hipStream_t s = (hipStream_t)stream;
 	bool launched = false;
 	int st = bin_count_launch(n, means2D, depths, radii, conics, colors, opacities, width, height, conic4,
-							  color_opacity4, workspace, workspace_bytes, true, s, &launched);
+							  color_opacity4, workspace, workspace_bytes, true, nullptr, s, &launched);
 	if (st != HDS_OK || !launched) return st;
 	CountWords host = {0, 0, 0};
 	HDS_HIP(hipMemcpyAsync(&host, count_words(workspace, n), sizeof(host), hipMemcpyDeviceToHost, s));
@@ -1061,7 +1089,7 @@ int bin_count_async(int64_t n, const float* means2D, const float* depths, const 
 	hipStream_t s = (hipStream_t)stream;
 	bool launched = false;
 	int st = bin_count_launch(n, means2D, depths, radii, conics, colors, opacities, width, height, conic4,
-							  color_opacity4, workspace, workspace_bytes, depth_sort, s, &launched);
+							  color_opacity4, workspace, workspace_bytes, depth_sort, nullptr, s, &launched);
 	if (st != HDS_OK) return st;
 	if (!launched) {
 		// Nothing enqueued: the count is known now.
@@ -1082,14 +1110,6 @@ extern "C" int hds_bin_count_async(int64_t n, const float* means2D, const float*
 						   color_opacity4, workspace, workspace_bytes, count_host, true, stream);
 }
 
-extern "C" int hds_bin_count_tile_order_async(int64_t n, const float* means2D, const float* depths,
-											  const float* radii, const float* conics, const float* colors,
-											  const float* opacities, int width, int height, float* conic4,
-											  float* color_opacity4, void* workspace, size_t workspace_bytes,
-											  void* count_host, hds_stream_t stream) {
-	return bin_count_async(n, means2D, depths, radii, conics, colors, opacities, width, height, conic4,
-						   color_opacity4, workspace, workspace_bytes, count_host, false, stream);
-}
 
 extern "C" int hds_bin_status(int64_t n, const void* workspace, void* status_host, hds_stream_t stream) {
 	HDS_REQUIRE(status_host, "bin_status: status_host must not be NULL");
@@ -1129,11 +1149,44 @@ extern "C" int hds_bin_emit_tile_order(int64_t n, int64_t num_pairs, int width, 
 						   values_sorted, tile_ranges, (hipStream_t)stream);
 }
 
-extern "C" int hds_bin_emit_tile_order_capped(int64_t n, int64_t capacity, int width, int height, void* workspace,
-											  void* pairs_workspace, size_t pairs_workspace_bytes,
-											  int32_t* values_sorted, int32_t* tile_ranges, hds_stream_t stream) {
-	return bin_emit_launch(n, capacity, false, true, width, height, workspace, pairs_workspace, pairs_workspace_bytes,
-						   values_sorted, tile_ranges, (hipStream_t)stream);
+extern "C" int hds_bin_tile_order_async(int64_t n, const float* means2D, const float* depths, const float* radii,
+										const float* conics, const float* colors, const float* opacities, int width,
+										int height, float* conic4, float* color_opacity4, void* workspace,
+										size_t workspace_bytes, int64_t capacity, void* pairs_workspace,
+										size_t pairs_workspace_bytes, int32_t* values_sorted, int32_t* tile_ranges,
+										void* status_host, hds_stream_t stream) {
+	HDS_REQUIRE(status_host && tile_ranges, "bin_tile_order: null status_host / tile_ranges");
+	HDS_REQUIRE(capacity >= 0 && capacity < INT32_MAX, "bin_tile_order: capacity %lld outside [0, 2^31)",
+				(long long)capacity);
+	HDS_REQUIRE(width > 0 && height > 0, "bin_tile_order: image size %dx%d must be positive", width, height);
+	hipStream_t s = (hipStream_t)stream;
+	const int tiles_x = (width + HDS_TILE - 1) / HDS_TILE, tiles_y = (height + HDS_TILE - 1) / HDS_TILE;
+	const int64_t num_tiles = (int64_t)tiles_x * tiles_y;
+	if (n == 0) {
+		*static_cast<CountWords*>(status_host) = CountWords{0, 0, 0};
+		return bin_emit_launch(0, 0, false, true, width, height, workspace, pairs_workspace, pairs_workspace_bytes,
+							   values_sorted, tile_ranges, s);
+	}
+	const PairSpace p = pair_space(capacity);
+	HDS_REQUIRE(pairs_workspace && pairs_workspace_bytes >= p.bytes,
+				"bin_tile_order: pairs workspace of %zu bytes, need %zu", pairs_workspace_bytes, p.bytes);
+	HDS_REQUIRE(capacity == 0 || values_sorted, "bin_tile_order: null values_sorted");
+	// prepare clears the gaussian control block (slot 0, filled in by bin_count_launch), the pair
+	// control block and the tile ranges, so neither half launches a zeroing kernel of its own.
+	ZeroRanges zero{};
+	zero.p[1] = at<uint32_t>(pairs_workspace, p.ctrl);
+	zero.n[1] = (int64_t)(p.bytes - p.ctrl) / 4;
+	zero.p[2] = reinterpret_cast<uint32_t*>(tile_ranges);
+	zero.n[2] = 2 * num_tiles;
+	bool launched = false;
+	int st = bin_count_launch(n, means2D, depths, radii, conics, colors, opacities, width, height, conic4,
+							  color_opacity4, workspace, workspace_bytes, false, &zero, s, &launched);
+	if (st != HDS_OK) return st;
+	st = bin_emit_launch(n, capacity, false, true, width, height, workspace, pairs_workspace, pairs_workspace_bytes,
+						 values_sorted, tile_ranges, s, true);
+	if (st != HDS_OK) return st;
+	HDS_HIP(hipMemcpyAsync(status_host, count_words(workspace, n), sizeof(CountWords), hipMemcpyDeviceToHost, s));
+	return HDS_OK;
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -1188,7 +1241,7 @@ extern "C" int hds_bin_static(int64_t n, const float* means2D, const float* dept
 	void* pws = static_cast<char*>(ptr) + align256(gaussian_bytes);
 	bool launched = false;
 	st = bin_count_launch(n, means2D, depths, radii, conics, colors, opacities, width, height, conic4, color_opacity4,
-						  ws, gaussian_bytes, true, s, &launched);
+						  ws, gaussian_bytes, true, nullptr, s, &launched);
 	if (st != HDS_OK) return st;
 	if (!launched) {
 		// No gaussians: empty tile ranges and zero status words, from a zeroed control block.

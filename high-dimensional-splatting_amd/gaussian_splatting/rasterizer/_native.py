@@ -46,10 +46,9 @@ PROTOTYPES = {
     "hds_pairs_workspace_bytes": (_sz, [_i64, _i32, _i32]),
     "hds_bin_emit": (_i32, [_i64, _i64, _i32, _i32, _vp, _vp, _sz, _vp, _vp, _vp]),
     "hds_bin_emit_capped": (_i32, [_i64, _i64, _i32, _i32, _vp, _vp, _sz, _vp, _vp, _vp]),
-    "hds_bin_count_tile_order_async": (_i32, [_i64, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _vp, _vp, _vp, _sz,
-                                              _vp, _vp]),
+    "hds_bin_tile_order_async": (_i32, [_i64, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _vp, _vp, _vp, _sz, _i64,
+                                        _vp, _sz, _vp, _vp, _vp, _vp]),
     "hds_bin_emit_tile_order": (_i32, [_i64, _i64, _i32, _i32, _vp, _vp, _sz, _vp, _vp, _vp]),
-    "hds_bin_emit_tile_order_capped": (_i32, [_i64, _i64, _i32, _i32, _vp, _vp, _sz, _vp, _vp, _vp]),
     "hds_bin_status": (_i32, [_i64, _vp, _vp, _vp]),
     "hds_set_lookback_limit": (_i32, [ctypes.c_uint32]),
     "hds_bin_static": (_i32, [_i64, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _vp, _vp, _i64, _vp, _vp, _vp, _vp]),
@@ -244,7 +243,7 @@ class PendingBins:
         self.count = count              # pinned int64 [2]: pair count, look-back error flag
         self.workspace = workspace      # per-gaussian workspace the exact re-emit reads
         self.emit_args = emit_args      # (n, width, height, device)
-        self.tile_order = False         # binned by hds_bin_count_tile_order_async
+        self.tile_order = False         # binned by hds_bin_tile_order_async
         self.inputs = None              # the binning inputs, for a rebin with the global depth sort
         self.status = status            # pinned int64 [2] of hds_bin_status after the capped emit
         self.status_event = status_event  # recorded after that copy
@@ -255,7 +254,7 @@ class HipRasterizer:
 
     # Pair buffers of bin_async are sized this much above the last pair count seen on the device.
     PAIR_HEADROOM = 1.25
-    # Longest tile list the tile-order binning sorts (hds_bin_count_tile_order_async), and the share
+    # Longest tile list the tile-order binning sorts (hds_bin_tile_order_async), and the share
     # of it the last frame's longest list may reach for bin_async to choose that binning.
     TILE_ORDER_MAX = 4096
     TILE_ORDER_MARGIN = 0.9
@@ -419,25 +418,33 @@ class HipRasterizer:
         conic4 = torch.empty((n, 4), device=dev, dtype=torch.float32)
         color_opacity4 = torch.empty((n, 4), device=dev, dtype=torch.float32)
         tile_ranges = torch.empty((tiles, 2), device=dev, dtype=torch.int32)
-        count = torch.zeros(2, dtype=torch.int64, pin_memory=True)
         with torch.cuda.device(dev):
             stream = _stream(dev)
             ws = torch.empty(self.lib.hds_bin_workspace_bytes(n, width, height), device=dev, dtype=torch.uint8)
-            count_entry = self.lib.hds_bin_count_tile_order_async if tile_order else self.lib.hds_bin_count_async
-            self._run("bin_count", lambda: count_entry(
-                n, _ptr(means2D), _ptr(depths), _ptr(radii), _ptr(conics), _ptr(colors), _ptr(opacities), width,
-                height, _ptr(conic4), _ptr(color_opacity4), _ptr(ws), ws.numel(), _ptr(count), stream))
-            event = torch.cuda.Event()
-            event.record()
             values = torch.empty((cap,), device=dev, dtype=torch.int32)
             pws = torch.empty(self.lib.hds_pairs_workspace_bytes(cap, width, height), device=dev, dtype=torch.uint8)
-            emit_entry = self.lib.hds_bin_emit_tile_order_capped if tile_order else self.lib.hds_bin_emit_capped
-            self._run("bin_emit", lambda: emit_entry(
-                n, cap, width, height, _ptr(ws), _ptr(pws), pws.numel(), _ptr(values), _ptr(tile_ranges), stream))
             status = torch.zeros(2, dtype=torch.int64, pin_memory=True)
-            _check(self.lib.hds_bin_status(n, _ptr(ws), _ptr(status), stream))
-            status_event = torch.cuda.Event()
-            status_event.record()
+            if tile_order:
+                # One call: the whole binning, then its status words (P and the flags) to `status`.
+                self._run("bin", lambda: self.lib.hds_bin_tile_order_async(
+                    n, _ptr(means2D), _ptr(depths), _ptr(radii), _ptr(conics), _ptr(colors), _ptr(opacities), width,
+                    height, _ptr(conic4), _ptr(color_opacity4), _ptr(ws), ws.numel(), cap, _ptr(pws), pws.numel(),
+                    _ptr(values), _ptr(tile_ranges), _ptr(status), stream))
+                count, event = status, torch.cuda.Event()
+                event.record()
+                status_event = event
+            else:
+                count = torch.zeros(2, dtype=torch.int64, pin_memory=True)
+                self._run("bin_count", lambda: self.lib.hds_bin_count_async(
+                    n, _ptr(means2D), _ptr(depths), _ptr(radii), _ptr(conics), _ptr(colors), _ptr(opacities), width,
+                    height, _ptr(conic4), _ptr(color_opacity4), _ptr(ws), ws.numel(), _ptr(count), stream))
+                event = torch.cuda.Event()
+                event.record()
+                self._run("bin_emit", lambda: self.lib.hds_bin_emit_capped(
+                    n, cap, width, height, _ptr(ws), _ptr(pws), pws.numel(), _ptr(values), _ptr(tile_ranges), stream))
+                _check(self.lib.hds_bin_status(n, _ptr(ws), _ptr(status), stream))
+                status_event = torch.cuda.Event()
+                status_event.record()
         pending = PendingBins(values, tile_ranges, conic4, color_opacity4, capacity=cap, event=event, count=count,
                               workspace=ws, emit_args=(n, width, height, dev), status=status,
                               status_event=status_event)

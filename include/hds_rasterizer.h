@@ -136,30 +136,33 @@ HDS_API int hds_bin_emit_capped(int64_t n, int64_t capacity, int width, int heig
 						void* pairs_workspace, size_t pairs_workspace_bytes, int32_t* values_sorted,
 						int32_t* tile_ranges, hds_stream_t stream);
 
-/* The same binning with the depth order built per tile (forward.cu:284-404 reordered): no global
- * depth sort; the scan and the pairs follow gaussian index order, the pairs are sorted by tile
- * alone, and each tile's list is then sorted by (depth bits, index) in one work-group, which gives
- * the reference's (tile, depth bits, index) order. values_sorted and tile_ranges equal
- * hds_bin_count + hds_bin_emit's bit for bit. Takes tiles of up to 4096 pairs: a longer list is
- * left in index order and flagged (bit 1 of the tile-sort word of hds_bin_status), and the caller
- * bins again with hds_bin_count + hds_bin_emit. hds_bin_emit_tile_order(_capped) continue only a
- * hds_bin_count_tile_order_async workspace, with the capacity contract of hds_bin_emit_capped. */
-HDS_API int hds_bin_count_tile_order_async(int64_t n, const float* means2D, const float* depths,
-								   const float* radii, const float* conics, const float* colors,
-								   const float* opacities, int width, int height, float* conic4,
-								   float* color_opacity4, void* workspace, size_t workspace_bytes,
-								   void* count_host, hds_stream_t stream);
+/* The whole binning (forward.cu:284-404) in one call for a pair count the host has not read yet,
+ * with the depth order built per tile: no global depth sort; the tile counts are scanned and the
+ * pairs emitted in gaussian-index order, the pairs are sorted by tile alone, and each tile's list is
+ * then sorted by (depth bits, index) in one work-group, which gives the reference's (tile, depth
+ * bits, index) order. values_sorted, tile_ranges, conic4 and color_opacity4 equal hds_bin_count +
+ * hds_bin_emit's bit for bit, under hds_bin_emit_capped's capacity contract (values_sorted and
+ * pairs_workspace sized for `capacity` pairs; hds_pairs_workspace_bytes(capacity)). The call ends
+ * with an asynchronous copy of the 16 status bytes of hds_bin_status to status_host (pinned host
+ * memory), valid once the stream has passed the call. It takes tile lists of up to 4096 pairs: a
+ * longer one is left in index order and flagged (bit 1 of the tile-sort word), and the caller bins
+ * the frame again with hds_bin_count + hds_bin_emit. When P > capacity, hds_bin_emit_tile_order
+ * emits again with buffers for P from the same workspace (then read the flags with
+ * hds_bin_status). No counterpart in the reference. */
+HDS_API int hds_bin_tile_order_async(int64_t n, const float* means2D, const float* depths, const float* radii,
+							 const float* conics, const float* colors, const float* opacities, int width,
+							 int height, float* conic4, float* color_opacity4, void* workspace,
+							 size_t workspace_bytes, int64_t capacity, void* pairs_workspace,
+							 size_t pairs_workspace_bytes, int32_t* values_sorted, int32_t* tile_ranges,
+							 void* status_host, hds_stream_t stream);
 HDS_API int hds_bin_emit_tile_order(int64_t n, int64_t num_pairs, int width, int height, void* workspace,
 							void* pairs_workspace, size_t pairs_workspace_bytes, int32_t* values_sorted,
 							int32_t* tile_ranges, hds_stream_t stream);
-HDS_API int hds_bin_emit_tile_order_capped(int64_t n, int64_t capacity, int width, int height,
-								   void* workspace, void* pairs_workspace, size_t pairs_workspace_bytes,
-								   int32_t* values_sorted, int32_t* tile_ranges, hds_stream_t stream);
 
 /* No counterpart in the reference (CUB's sort reports nothing): enqueues an asynchronous copy of
  * the binning's 16 status bytes from `workspace` (the one hds_bin_count(_async) filled for n
  * gaussians) to pinned host memory status_host: uint64 pair count P, uint32 flag of the depth sort
- * and count scan, uint32 word of the tile sort of the last hds_bin_emit(_capped / _tile_order):
+ * and count scan, uint32 word of the tile sort of the last emit (hds_bin_emit(_capped / _tile_order)):
  * a nonzero flag, or bit 0 of the word, means a look-back gave up and the binning must not be used;
  * bit 1 means a tile-order binning met a tile of more than 4096 pairs. Valid once the stream has
  * passed this call. */
