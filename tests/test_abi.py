@@ -105,6 +105,20 @@ def test_zero_fill_rejects_bad_ranges_before_launch(lib):
     assert lib.hds_zero_async(None, 0, 0, None) == 0  # nothing to clear, nothing enqueued
 
 
+def test_tile_order_binning_rejects_bad_arguments_before_launch(lib):
+    fake = ctypes.c_void_p(16)
+
+    def call(width=32, capacity=8, status=fake, workspace_bytes=1 << 20, pairs_bytes=1 << 20):
+        return lib.hds_bin_tile_order_async(10, fake, fake, fake, fake, None, fake, width, 32, fake, None, fake,
+                                            workspace_bytes, capacity, fake, pairs_bytes, fake, fake, status, None)
+
+    assert call(status=None) == 1 and b"null status_host" in lib.hds_last_error()
+    assert call(capacity=-1) == 1 and b"capacity" in lib.hds_last_error()
+    assert call(width=0) == 1 and b"must be positive" in lib.hds_last_error()
+    assert call(pairs_bytes=16) == 1 and b"pairs workspace" in lib.hds_last_error()
+    assert call(workspace_bytes=16) == 1 and b"workspace of 16 bytes" in lib.hds_last_error()
+
+
 def test_render_clear_rejects_bad_ranges_before_launch(lib):
     fake = ctypes.c_void_p(16)
 
