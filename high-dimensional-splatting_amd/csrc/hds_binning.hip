@@ -1079,17 +1079,15 @@ extern "C" int hds_bin_count(int64_t n, const float* means2D, const float* depth
 	return HDS_OK;
 }
 
-namespace {
-
-int bin_count_async(int64_t n, const float* means2D, const float* depths, const float* radii, const float* conics,
-					const float* colors, const float* opacities, int width, int height, float* conic4,
-					float* color_opacity4, void* workspace, size_t workspace_bytes, void* count_host, bool depth_sort,
-					hds_stream_t stream) {
+extern "C" int hds_bin_count_async(int64_t n, const float* means2D, const float* depths, const float* radii,
+								   const float* conics, const float* colors, const float* opacities, int width,
+								   int height, float* conic4, float* color_opacity4, void* workspace,
+								   size_t workspace_bytes, void* count_host, hds_stream_t stream) {
 	HDS_REQUIRE(count_host, "bin_count_async: count_host must not be NULL");
 	hipStream_t s = (hipStream_t)stream;
 	bool launched = false;
 	int st = bin_count_launch(n, means2D, depths, radii, conics, colors, opacities, width, height, conic4,
-							  color_opacity4, workspace, workspace_bytes, depth_sort, nullptr, s, &launched);
+							  color_opacity4, workspace, workspace_bytes, true, nullptr, s, &launched);
 	if (st != HDS_OK) return st;
 	if (!launched) {
 		// Nothing enqueued: the count is known now.
@@ -1099,17 +1097,6 @@ int bin_count_async(int64_t n, const float* means2D, const float* depths, const 
 	HDS_HIP(hipMemcpyAsync(count_host, count_words(workspace, n), sizeof(CountWords), hipMemcpyDeviceToHost, s));
 	return HDS_OK;
 }
-
-}  // namespace
-
-extern "C" int hds_bin_count_async(int64_t n, const float* means2D, const float* depths, const float* radii,
-								   const float* conics, const float* colors, const float* opacities, int width,
-								   int height, float* conic4, float* color_opacity4, void* workspace,
-								   size_t workspace_bytes, void* count_host, hds_stream_t stream) {
-	return bin_count_async(n, means2D, depths, radii, conics, colors, opacities, width, height, conic4,
-						   color_opacity4, workspace, workspace_bytes, count_host, true, stream);
-}
-
 
 extern "C" int hds_bin_status(int64_t n, const void* workspace, void* status_host, hds_stream_t stream) {
 	HDS_REQUIRE(status_host, "bin_status: status_host must not be NULL");
