@@ -87,14 +87,28 @@ def test_projection_backward_matches_oracle():
 
 # ---- binning ----------------------------------------------------------------------------------
 
+@pytest.mark.parametrize("order", ["depth", "tile"])
 @pytest.mark.parametrize("index,n", [(0, 10_000), (1, 200_000), (2, None)])
-def test_binning_is_bitwise_equal_to_oracle(index, n):
-    # (2, None) is the headline scene at full size: 1.18M gaussians, 1.92M pairs, 470 sort partitions.
+def test_binning_is_bitwise_equal_to_oracle(index, n, order):
+    """Both binnings at full size: the global depth sort (bin, the reference's two-phase sequence) and
+    tile order (bin_async with the depth order built per tile, the autograd path). (2, None) is the
+    headline scene: 1.18M gaussians, 1.92M pairs, 470 sort partitions, tile lists of up to 1,736 pairs."""
+    from gaussian_splatting.rasterizer._native import HipRasterizer
+
     wl = synthetic_config(index, n=n, channels=1)
     (m2, d, r, c), _ = project_both(wl.means, wl.scales, wl.quats, wl.opacities, wl.cam)
     colors = torch.rand(wl.n, 3, generator=torch.Generator().manual_seed(3)).to(DEV)
-    values, ranges, conic4, color4 = _get_rasterizer().bin(m2, d, r, c, colors, wl.opacities.to(DEV), wl.width,
-                                                           wl.height)
+    opac = wl.opacities.to(DEV)
+    print(f"[test] binning config {index}, {order} order", file=sys.stderr, flush=True)
+    if order == "depth":
+        values, ranges, conic4, color4 = _get_rasterizer().bin(m2, d, r, c, colors, opac, wl.width, wl.height)
+    else:
+        ext = HipRasterizer()
+        ext._pair_capacity[m2.device.index] = 1 << 22
+        ext.tile_order = True
+        bins = ext.bin_async(m2, d, r, c, colors, opac, wl.width, wl.height)
+        assert not ext.resolve(bins) and bins.tile_order
+        values, ranges, conic4, color4 = bins.values, bins.tile_ranges, bins.conic4, bins.color_opacity4
     counts, want_values, want_ranges = oracle.bin_gaussians(np_(m2), np_(d), np_(r), np_(c), np_(wl.opacities),
                                                             wl.width, wl.height)
     assert values.numel() == counts.sum() == want_values.size
