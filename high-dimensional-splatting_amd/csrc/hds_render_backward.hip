@@ -440,7 +440,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void b
 											hds_u2f(d1.x), hds_u2f(d1.y), hds_u2f(d1.z), hds_u2f(d1.w)};
 						hds_bf16x8 b_hi, b_lo;
 						hds_split8(v, b_hi, b_lo);
-						ms = hds_mfma_split(pt_hi[kk], pt_lo[kk], b_hi, b_lo, ms);
+						// Only rows 0-5 of ms are read, and P is exact in bf16 there (pt_lo = 0): the
+						// lo x hi product adds exact zeros, so two MFMAs give the same bits as three.
+						ms = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pt_hi[kk], b_lo, ms, 0, 0, 0);
+						ms = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pt_hi[kk], b_hi, ms, 0, 0, 0);
 					}
 					if (do_rgb) {
 						const hds_u32x4 d0 = hds_lds_read128(reinterpret_cast<const uint32_t*>(tr_w + off));
