@@ -15,7 +15,9 @@ against MI355X HBM (8 TB/s), a CPU baseline: the oracle (oracle/hds_oracle.c, Op
 frame on this host, and the environment (GPU, clocks and power from amd-smi, source digest). After the
 headline it times, on the same GPU, the channel sweep (C = 32, 64, 256, 512 on the
 headline scene) and configs 0, 1 and 4 (their step, fwd / bwd split, blend backward span and per-stage
-means), reported under 'channel_sweep' and 'other_configs'.
+means), reported under 'channel_sweep' and 'other_configs', and one iteration of the reference's
+training loop on the headline scene (main.py:159-200, SH and the optimizer step included), reported
+under 'training_iteration'.
 
 Like the reference harness, which times only what agrees with its comparison (harness.py:196-208), it
 first checks one fwd+bwd step of this frame against the oracle (images and every leaf gradient within
@@ -74,6 +76,10 @@ def parse_args():
                          "includes the loss, none otherwise")
     ap.add_argument("--bwd-slice", type=int, default=None,
                     help="channels per backward work-group (gaussian_splatting.rasterizer.FEATURE_SLICE_WIDTH)")
+    ap.add_argument("--train", choices=("auto", "on", "off"), default="auto",
+                    help="also time a training iteration of the reference's loop (main.py:159-200) on the headline "
+                         "scene and report it under 'training_iteration'; auto: on for the default run, off under a "
+                         "profiler")
     ap.add_argument("--configs", default="auto",
                     help="comma-separated other BASELINE configs timed after the headline on the same GPU (step, "
                          "fwd / bwd split, blend backward span, per-stage ms) and reported under 'other_configs'; "
@@ -374,6 +380,13 @@ def main() -> int:
         torch.cuda.empty_cache()
         other_configs = [measure_config(index, args) for index in other]
 
+    train = (args.train == "on" or (args.train == "auto" and args.config == 2 and args.checkpoint is None
+                                     and not args.rgb_only and not args.frozen_features and not _profiled()))
+    training_iteration = None
+    if train:
+        torch.cuda.empty_cache()
+        training_iteration = measure_training_iteration(args.config)
+
     line = {
         "metric": METRIC, "value": round(ms_per_step, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": False, "scaling": "weak",
@@ -388,6 +401,7 @@ def main() -> int:
         "roofline": roofline, "breakdown_steps": args.breakdown_steps, "stages": stage_report,
         "kernels": kernel_report, "cpu_baseline": cpu,
         "agreement": agreement, "channel_sweep": channel_sweep, "other_configs": other_configs,
+        "training_iteration": training_iteration,
         "environment": environment(),
     }
     print(json.dumps(line), flush=True)
@@ -507,6 +521,74 @@ def measure_sweep(wl, leaves: dict, w2c, channels_list, n_vis: int, pairs: int, 
         del feats, grad_image, grad_features, holder
         torch.cuda.empty_cache()
     return out
+
+
+def measure_training_iteration(index: int, iterations: int = 20, warmup: int = 5) -> dict:
+    """One iteration of the reference's training loop (main.py:159-200) on config `index`'s scene: the
+    model's activations (exp scales, normalised quats, sigmoid opacities), projection, eval_sh with the
+    fused SH Adam (utils/sh.py:59-109), rasterize with the features, 0.8 L1 + 0.2 (1 - SSIM) plus an L1
+    term on the feature image against U[0, 1] targets, backward, the densification statistics from
+    means2D.grad (utils/gaussian.py:143-160) and fused torch Adam over the other parameters. Returns the
+    mean ms per iteration over `iterations` after `warmup`, timed with CUDA events."""
+    import torch
+    import torch.nn.functional as F
+
+    from gaussian_splatting.rasterizer import project_gaussians, rasterize
+    from gaussian_splatting.utils.densification import DensificationStats
+    from gaussian_splatting.utils.loss import l1_loss, ssim
+    from gaussian_splatting.utils.sh import eval_sh
+    from tests.scenes import synthetic_config
+
+    dev = torch.device("cuda:0")
+    wl = synthetic_config(index).to(dev)
+    cam, W, H = wl.cam, wl.width, wl.height
+    print(f"[bench] training iteration on {wl.name}", file=sys.stderr, flush=True)
+    model = {"means": wl.means, "scales": torch.log(wl.scales), "quats": wl.quats,
+             "opacities": torch.logit(wl.opacities.clamp(1e-4, 1 - 1e-4)), "sh_dc": wl.sh_dc, "sh_rest": wl.sh_rest,
+             "features": wl.features}
+    model = {k: v.detach().clone().contiguous().requires_grad_(True) for k, v in model.items()}
+    # Learning rates of the reference's config (config.py); they set no cost.
+    lrs = {"means": 1.6e-4, "scales": 5e-3, "quats": 1e-3, "opacities": 5e-2, "sh_dc": 2.5e-3, "sh_rest": 1.25e-4,
+           "features": 2.5e-3}
+    optimizer = torch.optim.Adam([{"params": [model[k]], "lr": lrs[k], "name": k} for k in model], eps=1e-15,
+                                 fused=True)
+    g = torch.Generator(device=dev).manual_seed(2)
+    gt = torch.rand(H, W, 3, device=dev, generator=g)
+    gt_features = torch.rand(H, W, wl.channels, device=dev, generator=g)
+    centre = wl.center
+    stats = DensificationStats(wl.n, dev)
+
+    def iteration():
+        opac = torch.sigmoid(model["opacities"])
+        means2D, depths, radii, conics = project_gaussians(
+            model["means"], torch.exp(model["scales"]), F.normalize(model["quats"], dim=-1), opac,
+            wl.world_to_camera, cam["fx"], cam["fy"], cam["cx"], cam["cy"], W, H)
+        means2D.retain_grad()
+        dirs = F.normalize(model["means"] - centre, dim=-1)
+        colors = eval_sh(model["sh_dc"], model["sh_rest"], dirs, wl.sh_degree, radii, optimizer)
+        image, feature_image = rasterize(means2D, depths, radii, conics, colors, opac, W, H,
+                                         features=model["features"])
+        loss = 0.8 * l1_loss(image, gt) + 0.2 * (1 - ssim(image, gt)) + l1_loss(feature_image, gt_features)
+        loss.backward()
+        with torch.no_grad():
+            stats.add(means2D.grad, radii, W, H)
+            optimizer.step()
+            optimizer.zero_grad(set_to_none=True)
+
+    for _ in range(warmup):
+        iteration()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(iterations):
+        iteration()
+    end.record()
+    torch.cuda.synchronize()
+    parameters = sum(v.numel() for v in model.values())
+    return {"workload": wl.name, "ms": round(start.elapsed_time(end) / iterations, 4), "iterations": iterations,
+            "warmup": warmup, "parameters": parameters,
+            "scope": "activations, projection, eval_sh + fused SH Adam, rasterize (RGB + features), "
+                     "0.8 L1 + 0.2 (1 - SSIM) + L1(features), backward, densification statistics, fused Adam"}
 
 
 def measure_config(index: int, args) -> dict:

@@ -71,3 +71,16 @@ def test_bench_times_another_config_with_its_loss():
     # The binning is one stage in tile order ("bin"), two with the global depth sort.
     assert {"bin"} <= stages or {"bin_count", "bin_emit"} <= stages
     assert {"render", "render_backward", "ssim_forward", "ssim_backward"} <= stages
+
+
+def test_bench_times_a_training_iteration():
+    """bench.py's training-iteration pass (the reference's loop: projection, eval_sh with the fused SH
+    Adam, rasterize, the loss, backward, densification statistics, Adam) runs on config 0's scene and
+    reports its time and parameter count."""
+    import bench
+
+    print("[test] bench.measure_training_iteration(0)", file=sys.stderr, flush=True)
+    out = bench.measure_training_iteration(0, iterations=2, warmup=1)
+    assert out["workload"].startswith("cpu-plumbing-10k") and out["iterations"] == 2
+    assert out["ms"] > 0
+    assert out["parameters"] == 10_000 * (3 + 3 + 4 + 1 + 3 + 45 + 32)
