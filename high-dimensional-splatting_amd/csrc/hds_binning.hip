@@ -892,6 +892,39 @@ extern "C" size_t hds_pairs_workspace_bytes(int64_t num_pairs, int width, int he
 
 namespace {
 
+// Which count last filled each gaussian workspace: depth-sorted (hds_bin_count(_async)) or index
+// order (hds_bin_tile_order_async). The two leave different things in it (offsets scanned over the
+// depth order or over the index order, sorted or unsorted rectangles), so an emit checks the record
+// and rejects a workspace the other count filled, or one no count of this process filled, before it
+// enqueues anything. Keyed by address; the most recent kModeRecords workspaces are remembered.
+constexpr size_t kModeRecords = 256;
+std::mutex g_mode_mutex;
+std::vector<std::pair<const void*, bool>> g_mode_records;  // (workspace, depth sorted), newest last
+
+void record_count_mode(const void* workspace, bool depth_sort) {
+	std::lock_guard<std::mutex> lock(g_mode_mutex);
+	for (size_t i = 0; i < g_mode_records.size(); i++)
+		if (g_mode_records[i].first == workspace) {
+			g_mode_records.erase(g_mode_records.begin() + (ptrdiff_t)i);
+			break;
+		}
+	if (g_mode_records.size() == kModeRecords) g_mode_records.erase(g_mode_records.begin());
+	g_mode_records.emplace_back(workspace, depth_sort);
+}
+
+int check_count_mode(const void* workspace, bool depth_sort, const char* entry) {
+	std::lock_guard<std::mutex> lock(g_mode_mutex);
+	for (const auto& r : g_mode_records)
+		if (r.first == workspace) {
+			if (r.second == depth_sort) return HDS_OK;
+			return hds_set_error(HDS_ERR_INVALID, "%s: the workspace was filled by %s, this emit needs %s", entry,
+								 r.second ? "hds_bin_count (depth order)" : "hds_bin_tile_order_async (tile order)",
+								 depth_sort ? "hds_bin_count's depth order" : "hds_bin_tile_order_async's tile order");
+		}
+	return hds_set_error(HDS_ERR_INVALID, "%s: the workspace was not filled by a count of this process (%s)", entry,
+						 depth_sort ? "hds_bin_count" : "hds_bin_tile_order_async");
+}
+
 // Enqueues the counting half of the binning (cull, records, depth order, scan of the tile counts);
 // the pair count and the look-back error flag end in the workspace's control block. *launched is
 // false when there was nothing to enqueue (n == 0).
@@ -960,6 +993,7 @@ int bin_count_launch(int64_t n, const float* means2D, const float* depths, const
 															g_spin_limit.load(std::memory_order_relaxed), &ctrl->total);
 	timer3.stop();
 	HDS_LAUNCH_CHECK("scan_tile_counts", s);
+	record_count_mode(workspace, depth_sort);
 	*launched = true;
 	return HDS_OK;
 }
@@ -1118,6 +1152,10 @@ extern "C" int hds_set_lookback_limit(uint32_t polls) {
 extern "C" int hds_bin_emit(int64_t n, int64_t num_pairs, int width, int height, void* workspace,
 							void* pairs_workspace, size_t pairs_workspace_bytes, int32_t* values_sorted,
 							int32_t* tile_ranges, hds_stream_t stream) {
+	if (n > 0 && num_pairs > 0) {
+		const int st = check_count_mode(workspace, true, "bin_emit");
+		if (st != HDS_OK) return st;
+	}
 	return bin_emit_launch(n, num_pairs, true, false, width, height, workspace, pairs_workspace, pairs_workspace_bytes,
 						   values_sorted, tile_ranges, (hipStream_t)stream);
 }
@@ -1125,6 +1163,10 @@ extern "C" int hds_bin_emit(int64_t n, int64_t num_pairs, int width, int height,
 extern "C" int hds_bin_emit_capped(int64_t n, int64_t capacity, int width, int height, void* workspace,
 								   void* pairs_workspace, size_t pairs_workspace_bytes, int32_t* values_sorted,
 								   int32_t* tile_ranges, hds_stream_t stream) {
+	if (n > 0 && capacity > 0) {
+		const int st = check_count_mode(workspace, true, "bin_emit_capped");
+		if (st != HDS_OK) return st;
+	}
 	return bin_emit_launch(n, capacity, false, false, width, height, workspace, pairs_workspace, pairs_workspace_bytes,
 						   values_sorted, tile_ranges, (hipStream_t)stream);
 }
@@ -1132,6 +1174,10 @@ extern "C" int hds_bin_emit_capped(int64_t n, int64_t capacity, int width, int h
 extern "C" int hds_bin_emit_tile_order(int64_t n, int64_t num_pairs, int width, int height, void* workspace,
 									   void* pairs_workspace, size_t pairs_workspace_bytes, int32_t* values_sorted,
 									   int32_t* tile_ranges, hds_stream_t stream) {
+	if (n > 0 && num_pairs > 0) {
+		const int st = check_count_mode(workspace, false, "bin_emit_tile_order");
+		if (st != HDS_OK) return st;
+	}
 	return bin_emit_launch(n, num_pairs, true, true, width, height, workspace, pairs_workspace, pairs_workspace_bytes,
 						   values_sorted, tile_ranges, (hipStream_t)stream);
 }
@@ -1215,6 +1261,7 @@ extern "C" int hds_bin_static(int64_t n, const float* means2D, const float* dept
 							  int32_t* tile_ranges, void* status, hds_stream_t stream) {
 	HDS_REQUIRE(n >= 0 && capacity >= 0, "bin_static: negative gaussian count or capacity");
 	HDS_REQUIRE(status && tile_ranges, "bin_static: null pointer argument");
+	HDS_REQUIRE(n == 0 || capacity == 0 || values_sorted, "bin_static: null values_sorted");
 	const size_t gaussian_bytes = gaussian_space(n).bytes;
 	const size_t pair_bytes = pair_space(capacity).bytes;
 	HDS_REQUIRE(gaussian_bytes + pair_bytes <= kStaticScratchBytes,
@@ -1240,7 +1287,6 @@ extern "C" int hds_bin_static(int64_t n, const float* means2D, const float* dept
 		HDS_HIP(hipMemcpyAsync(status, count_words(ws, 0), sizeof(CountWords), hipMemcpyDefault, s));
 		return HDS_OK;
 	}
-	HDS_REQUIRE(capacity == 0 || values_sorted, "bin_static: null values_sorted");
 	st = bin_emit_launch(n, capacity, false, false, width, height, ws, pws, pair_bytes, values_sorted, tile_ranges, s);
 	if (st != HDS_OK) return st;
 	HDS_HIP(hipMemcpyAsync(status, count_words(ws, n), sizeof(CountWords), hipMemcpyDefault, s));

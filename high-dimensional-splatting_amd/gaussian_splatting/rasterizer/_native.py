@@ -407,10 +407,12 @@ class HipRasterizer:
             self._tile_order_ok[dev.index] = longest <= self.TILE_ORDER_MARGIN * self.TILE_ORDER_MAX
             return PendingBins(values, ranges, conic4, color_opacity4)
         tile_order = self.tile_order if self.tile_order is not None else self._tile_order_ok.get(dev.index, False)
-        inputs = (means2D, depths, radii, conics, colors, opacities)
         means2D, depths, radii = _dev(means2D, "means2D"), _dev(depths, "depths"), _dev(radii, "radii")
         conics, opacities = _dev(conics, "conics"), _dev(opacities, "opacities")
         colors = None if colors is None else _dev(colors, "colors")
+        # Kept for a rebin with the global depth sort, which passes their pointers to the library as
+        # dense aligned float32: the converted tensors, not the caller's.
+        inputs = (means2D, depths, radii, conics, colors, opacities)
         n = means2D.shape[0]
         width, height = int(width), int(height)
         tiles = ((width + TILE - 1) // TILE) * ((height + TILE - 1) // TILE)

@@ -120,7 +120,11 @@ HDS_API size_t hds_pairs_workspace_bytes(int64_t num_pairs, int width, int heigh
  * index order on ties, and builds the per-tile [start, end) ranges, (0, 0) when untouched.
  * values_sorted [P] int32, tile_ranges [T,2] int32. If a look-back of the tile sort gives up
  * (bounded wait, see hds_set_lookback_limit), every tile range is left (0, 0), so nothing reads
- * the unsorted list, and the flag is raised in `workspace` for hds_bin_status. */
+ * the unsorted list, and the flag is raised in `workspace` for hds_bin_status. `workspace` must be
+ * the one hds_bin_count(_async) last filled (the emits read what that count left in it); a workspace
+ * hds_bin_tile_order_async filled, or one no count of this process filled, is rejected (status 1)
+ * before anything is enqueued. The same holds for hds_bin_emit_capped, and the other way round for
+ * hds_bin_emit_tile_order. */
 HDS_API int hds_bin_emit(int64_t n, int64_t num_pairs, int width, int height, void* workspace,
 				 void* pairs_workspace, size_t pairs_workspace_bytes, int32_t* values_sorted,
 				 int32_t* tile_ranges, hds_stream_t stream);

@@ -119,6 +119,25 @@ def test_tile_order_binning_rejects_bad_arguments_before_launch(lib):
     assert call(workspace_bytes=16) == 1 and b"workspace of 16 bytes" in lib.hds_last_error()
 
 
+def test_emits_reject_a_workspace_no_matching_count_filled(lib):
+    """Each emit reads what its own count left in the gaussian workspace (depth-ordered offsets and
+    rectangles, or index-ordered ones); an emit handed a workspace the other count filled, or that
+    no count filled, is rejected before any launch."""
+    fake = ctypes.c_void_p(1 << 20)
+    args = (10, 8, 32, 32, fake, fake, 1 << 20, fake, fake, None)
+    assert lib.hds_bin_emit(*args) == 1 and b"not filled by a count" in lib.hds_last_error()
+    assert lib.hds_bin_emit_capped(*args) == 1 and b"not filled by a count" in lib.hds_last_error()
+    assert lib.hds_bin_emit_tile_order(*args) == 1 and b"hds_bin_tile_order_async" in lib.hds_last_error()
+    # With nothing to emit the workspace is not read: the tile ranges are only cleared (a launch, so
+    # not called here).
+
+
+def test_static_binning_rejects_a_null_values_sorted_before_launch(lib):
+    fake = ctypes.c_void_p(16)
+    st = lib.hds_bin_static(10, fake, fake, fake, fake, None, fake, 32, 32, fake, None, 8, None, fake, fake, None)
+    assert st == 1 and b"null values_sorted" in lib.hds_last_error()
+
+
 def test_render_clear_rejects_bad_ranges_before_launch(lib):
     fake = ctypes.c_void_p(16)
 

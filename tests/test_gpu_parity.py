@@ -276,11 +276,13 @@ def _one_tile_scene(n, seed):
     return means2D, depths, torch.ones(n), conics, torch.full((n, 1), 0.5)
 
 
-@pytest.mark.parametrize("n", [3000, 5000])
-def test_tile_order_binning_sorts_long_lists_in_lds_and_hands_longer_ones_back(n):
+@pytest.mark.parametrize("n,strided", [(3000, False), (5000, False), (5000, True)])
+def test_tile_order_binning_sorts_long_lists_in_lds_and_hands_longer_ones_back(n, strided):
     """A tile of 3000 pairs (beyond the register network, sorted in LDS) bins bit for bit like the
     oracle in tile order; one of 5000 pairs (beyond the per-tile sort) is flagged, resolve bins the
-    frame again with the global depth sort (same result) and the device leaves tile order."""
+    frame again with the global depth sort (same result) and the device leaves tile order. With
+    `strided`, means2D is a non-contiguous [:, :2] view of an [N, 3] tensor: the rebin must read the
+    dense copy the binning made, not the caller's view."""
     from gaussian_splatting.rasterizer._native import HipRasterizer
 
     means2D, depths, radii, conics, opac = _one_tile_scene(n, 9)
@@ -291,8 +293,14 @@ def test_tile_order_binning_sorts_long_lists_in_lds_and_hands_longer_ones_back(n
     dev = torch.device(DEV, torch.cuda.current_device())
     ext._pair_capacity[dev.index] = n + 8192
     ext._tile_order_ok[dev.index] = True
-    print(f"[test] tile-order binning, one tile of {n} pairs", file=sys.stderr, flush=True)
-    bins = ext.bin_async(means2D.to(DEV), depths.to(DEV), radii.to(DEV), conics.to(DEV), None, opac.to(DEV), 64, 64)
+    means2D_dev = means2D.to(DEV)
+    if strided:
+        wide = torch.full((n, 3), 1e6, device=DEV)
+        wide[:, :2] = means2D_dev
+        means2D_dev = wide[:, :2]
+        assert not means2D_dev.is_contiguous()
+    print(f"[test] tile-order binning, one tile of {n} pairs, strided means2D {strided}", file=sys.stderr, flush=True)
+    bins = ext.bin_async(means2D_dev, depths.to(DEV), radii.to(DEV), conics.to(DEV), None, opac.to(DEV), 64, 64)
     assert bins.tile_order
     rebinned = ext.resolve(bins)
     assert rebinned == (n > ext.TILE_ORDER_MAX)
