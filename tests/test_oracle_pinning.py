@@ -466,3 +466,96 @@ def test_config0_golden_vectors_are_reproduced():
                                                cam["height"], np.zeros(3, np.float32), data["features"])
     np.testing.assert_allclose(image, data["image"], rtol=1e-6, atol=1e-7)
     np.testing.assert_allclose(fimg, data["feature_image"], rtol=1e-5, atol=1e-6)
+
+
+def _config1_frame(channels):
+    """Config 1 (200k gaussians, 979x546) projected, binned and blended by the oracle, with U[0, 1]
+    colours and upstream gradients (seeds as bench.py)."""
+    from tests.scenes import upstream
+
+    wl = synthetic_config(1, channels=channels)
+    cam = wl.cam
+    quats = np_(wl.quats / wl.quats.norm(dim=-1, keepdim=True))
+    m2, d, r, c = oracle.project_forward(np_(wl.means), np_(wl.scales), quats, np_(wl.opacities),
+                                         np.eye(4, dtype=np.float32), cam["fx"], cam["fy"], cam["cx"], cam["cy"],
+                                         cam["width"], cam["height"])
+    colors = torch.rand(wl.n, 3, generator=torch.Generator().manual_seed(3)).numpy()
+    gi, gf = upstream(2, cam["height"], cam["width"], channels)
+    return wl, cam, quats, (m2, d, r, c), colors, np_(gi), np_(gf)
+
+
+def test_tile_mask_binning_blend_and_backward_equal_the_full_frame_on_the_selected_tiles():
+    """oracle.bin_gaussians(tile_mask=) (used for the stress scene's GPU parity on selected tiles)
+    against the unmasked oracle at config 1: the selected tiles' lists are the full binning's, the
+    others are empty; the blend of the selected tiles' pixels is bit for bit the full frame's; and
+    with the upstream gradients zeroed outside the selected tiles every gradient equals the full
+    binning's bit for bit (the other tiles then add exact zeros)."""
+    wl, cam, quats, (m2, d, r, c), colors, gi, gf = _config1_frame(8)
+    W, H = cam["width"], cam["height"]
+    op, feats = np_(wl.opacities).reshape(-1), np_(wl.features)
+    tx, ty = (W + 15) // 16, (H + 15) // 16
+    counts, values, ranges = oracle.bin_gaussians(m2, d, r, c, op, W, H)
+    rng = np.random.default_rng(7)
+    mask = rng.random(tx * ty) < 0.2
+    mask[np.argsort(ranges[:, 1] - ranges[:, 0])[-4:]] = True  # the longest lists too
+    mcounts, mvalues, mranges = oracle.bin_gaussians(m2, d, r, c, op, W, H, tile_mask=mask)
+    np.testing.assert_array_equal(mcounts, counts)
+    assert mvalues.size == int((ranges[mask, 1] - ranges[mask, 0]).sum())
+    for t in range(tx * ty):
+        got = mvalues[mranges[t, 0]:mranges[t, 1]]
+        want = values[ranges[t, 0]:ranges[t, 1]] if mask[t] else values[:0]
+        np.testing.assert_array_equal(got, want)
+    bg = np.zeros(3, np.float32)
+    full = oracle.render_forward(W, H, ranges, values, m2, c, op, colors, bg, feats)
+    part = oracle.render_forward(W, H, mranges, mvalues, m2, c, op, colors, bg, feats)
+    pix = np.repeat(np.repeat(mask.reshape(ty, tx), 16, 0), 16, 1)[:H, :W]
+    for got, want in zip(part, full):
+        np.testing.assert_array_equal(got[pix], want[pix])
+    assert (part[1][~pix] == 1.0).all() and (part[2][~pix] == 0).all()
+    gi_m, gf_m = gi * pix[..., None], gf * pix[..., None]
+    want = oracle.render_backward(W, H, ranges, values, m2, c, op, colors, bg, full[1], full[2], gi_m, feats, gf_m)
+    got = oracle.render_backward(W, H, mranges, mvalues, m2, c, op, colors, bg, part[1], part[2], gi_m, feats, gf_m)
+    for g, w in zip(got, want):
+        np.testing.assert_array_equal(g, w)
+    assert np.abs(want[0]).max() > 0
+
+
+def test_end_to_end_quats_gradient_amplifies_rasterizer_differences_far_below_the_bar():
+    """Why bench.py gates the projection backward on identical inputs instead of end to end: the
+    quaternion gradient (projection backward, then the normalize of the quats leaf) of the
+    elongated gaussians of a scene amplifies differences in the rasterizer's means2D / conic
+    gradients by orders of magnitude. At config 1, changing those gradients by 1e-6 of their max
+    (500x below the 2e-3 bar that both stages pass) moves the quats gradient by more than that bar,
+    and changing each value by about one float32 ulp (1e-7 relative) moves it by more than 1e-5 of
+    its max, while the means gradient stays within 1e-4."""
+    from tests.tolerances import grad_error
+
+    wl, cam, quats, (m2, d, r, c), colors, gi, _ = _config1_frame(1)
+    W, H = cam["width"], cam["height"]
+    op = np_(wl.opacities).reshape(-1)
+    _, values, ranges = oracle.bin_gaussians(m2, d, r, c, op, W, H)
+    bg = np.zeros(3, np.float32)
+    _, T, nc, _ = oracle.render_forward(W, H, ranges, values, m2, c, op, colors, bg)
+    dm, dc, _, _, _ = oracle.render_backward(W, H, ranges, values, m2, c, op, colors, bg, T, nc, gi)
+
+    def leaves(gm, gc):
+        pm, _, pq = oracle.project_backward(gm, gc, np_(wl.means), np_(wl.scales), quats, np.eye(4, dtype=np.float32),
+                                            cam["fx"], cam["fy"], cam["cx"], cam["cy"], W, H)
+        q = wl.quats.detach().clone().requires_grad_(True)
+        F.normalize(q, dim=-1).backward(torch.from_numpy(pq))
+        return pm, q.grad.numpy()
+
+    ref_m, ref_q = leaves(dm, dc)
+    rng = np.random.default_rng(0)
+    eps = 1e-6
+    gm = (dm + eps * np.abs(dm).max() * rng.uniform(-1, 1, dm.shape)).astype(np.float32)
+    gc = (dc + eps * np.abs(dc).max() * rng.uniform(-1, 1, dc.shape)).astype(np.float32)
+    assert grad_error(gm, dm)[1] <= 1.01 * eps and grad_error(gc, dc)[1] <= 1.01 * eps
+    got_m, got_q = leaves(gm, gc)
+    assert grad_error(got_m, ref_m)[1] < 1e-3
+    assert grad_error(got_q, ref_q)[1] > 2e-3
+    gm = (dm * (1 + 1e-7 * rng.uniform(-1, 1, dm.shape))).astype(np.float32)
+    gc = (dc * (1 + 1e-7 * rng.uniform(-1, 1, dc.shape))).astype(np.float32)
+    got_m, got_q = leaves(gm, gc)
+    assert grad_error(got_m, ref_m)[1] < 1e-4
+    assert grad_error(got_q, ref_q)[1] > 1e-5
