@@ -12,10 +12,13 @@ Prints ONE JSON line: the metric (ms per fwd+bwd, lower is better), the fwd / bw
 harness way (events around each sample, a pause after each, median; bench/harness.py:130-153), per-stage
 HIP-event timings taken inside the timed region, the roofline of the dominant kernel (render_backward)
 against MI355X HBM (8 TB/s), a CPU baseline: the oracle (oracle/hds_oracle.c, OpenMP) running the same
-frame on this host, and the environment (GPU, clocks and power from amd-smi, source digest). After the
-headline it times, on the same GPU, the channel sweep (C = 32, 64, 256, 512 on the
-headline scene) and configs 0, 1 and 4 (their step, fwd / bwd split, blend backward span and per-stage
-means), reported under 'channel_sweep' and 'other_configs', and one iteration of the reference's
+frame on this host, the median of --cpu-samples runs with its fwd / bwd split and the host (logical
+CPUs, usable CPUs, OpenMP threads, CPU model), and the environment (GPU, clocks and power from amd-smi,
+source digest). After the headline it times, on the same GPU, the channel sweep (
+C = 32, 64, 256, 512 on the headline scene) and configs 0, 1 and 4 (their step, fwd / bwd split, blend
+backward span and per-stage means), each with the oracle's CPU figure on the same frame beside it
+(config 4's on the 64 tiles its parity test compares, labelled; config 0's also with the dense float64
+blend, timed once), reported under 'channel_sweep' and 'other_configs', and one iteration of the reference's
 training loop on the headline scene (main.py:159-200, SH and the optimizer step included), reported
 under 'training_iteration'.
 
@@ -53,6 +56,8 @@ def parse_args():
     ap.add_argument("--channels", type=int, default=None, help="override the config's feature width")
     ap.add_argument("--no-cpu-baseline", action="store_true",
                     help="skip the CPU oracle (its timing and the agreement check it provides)")
+    ap.add_argument("--cpu-samples", type=int, default=5,
+                    help="oracle fwd+bwd runs per CPU figure (median; config 4's masked frame takes at most 3)")
     ap.add_argument("--no-split", action="store_true", help="skip the separate fwd / bwd median timing")
     ap.add_argument("--breakdown-steps", type=int, default=10,
                     help="steps after the timed region with events around every call and kernel, for the "
@@ -275,7 +280,7 @@ def main() -> int:
         gpu_out["rasterizer_inputs"] = [t.detach().cpu().numpy() for t in state.pop("projected")] + [
             leaves["colors"].detach().cpu().numpy(), leaves["opacities"].detach().cpu().numpy()]
         state.pop("means2D"), state.pop("conics")
-        cpu, want = cpu_baseline(wl, colors, grad_image, grad_features, loss_target=target)
+        cpu, want = cpu_baseline(wl, colors, grad_image, grad_features, args.cpu_samples, loss_target=target)
         agreement = agree(gpu_out, want)
         print(f"[bench] agreement with the oracle: {agreement}", file=sys.stderr, flush=True)
         if not agreement["passed"]:
@@ -464,8 +469,9 @@ def harness_split(fn_fwd, fn_bwd, reset, samples: int) -> dict:
 def measure_sweep(wl, leaves: dict, w2c, channels_list, n_vis: int, pairs: int, args) -> list[dict]:
     """the headline scene's gaussians with C feature channels ~ N(0, 1) (seed 1, as
     tests/scenes.py draws them) and dL/dimage, dL/dF ~ U[0, 1] (seed 2), for each C: the fwd+bwd step
-    (a few warm-up steps, then HIP events around each timed step), the harness fwd / bwd split and the
-    blend backward's roofline over the span of its kernels."""
+    (a few warm-up steps, then HIP events around each timed step), the harness fwd / bwd split, the
+    blend backward's roofline over the span of its kernels and, unless --no-cpu-baseline, the CPU
+    oracle's median fwd+bwd on the same frame."""
     import torch
     import torch.nn.functional as F
 
@@ -518,6 +524,12 @@ def measure_sweep(wl, leaves: dict, w2c, channels_list, n_vis: int, pairs: int, 
                     "fwd_ms_median": split["fwd_ms_median"], "bwd_ms_median": split["bwd_ms_median"],
                     "render_backward_ms": round(bwd_ms, 4), "render_backward_algorithmic_MB": round(alg / 1e6, 1),
                     "render_backward_GBs": round(gbs, 1), "render_backward_hbm_frac": round(gbs / HBM_PEAK_GBS, 4)})
+        if not args.no_cpu_baseline:
+            x = oracle_inputs(wl, leaves["colors"], grad_image, grad_features, features=feats)
+            out[-1]["cpu_baseline"] = cpu_timing(
+                x, args.cpu_samples, f"median of {args.cpu_samples} full fwd+bwd frames of the headline scene at "
+                                     f"C={c} (same inputs) on the C oracle, OpenMP")[0]
+            del x
         del feats, grad_image, grad_features, holder
         torch.cuda.empty_cache()
     return out
@@ -596,7 +608,10 @@ def measure_config(index: int, args) -> dict:
     step as the headline's runs (with the 0.8 L1 + 0.2 (1 - SSIM) loss for configs 0 and 4, whose
     BASELINE definition includes it), timed the same way, the harness fwd / bwd split, the blend
     backward's span and HBM fraction, and the per-stage means of a short breakdown pass. It has no
-    oracle gate of its own: the -m gpu tests compare these configs with the oracle."""
+    oracle gate of its own: the -m gpu tests compare these configs with the oracle. Unless
+    --no-cpu-baseline, the CPU oracle's median fwd+bwd of the same frame goes beside it: for config 4
+    on the 64 tiles its parity test compares (the oracle's sort cannot take its ~94M pairs in
+    seconds), labelled; for config 0 also the dense float64 blend, timed once."""
     import torch
 
     from gaussian_splatting.rasterizer import _get_rasterizer
@@ -639,7 +654,9 @@ def measure_config(index: int, args) -> dict:
                                         lv["opacities"][:, None], frame.w2c, cam["fx"], cam["fy"], cam["cx"],
                                         cam["cy"], wl.width, wl.height)
         n_vis = int((r > 0).sum())
-        pairs = int(ext.bin(m2, d, r, c, None, lv["opacities"][:, None], wl.width, wl.height)[0].numel())
+        values, ranges = ext.bin(m2, d, r, c, None, lv["opacities"][:, None], wl.width, wl.height)[:2]
+        pairs, ranges = int(values.numel()), ranges.cpu().numpy()
+        del values
     alg = algorithmic_bytes(wl.n, n_vis, pairs, wl.width * wl.height, wl.channels)["render_backward"]
     gbs = alg / (bwd_ms * 1e-3) / 1e9
     out = {"config": index, "workload": wl.name, "gaussians": wl.n, "width": wl.width, "height": wl.height,
@@ -649,9 +666,38 @@ def measure_config(index: int, args) -> dict:
            "bwd_ms_median": split["bwd_ms_median"], "render_backward_ms": round(bwd_ms, 4),
            "render_backward_GBs": round(gbs, 1), "render_backward_hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
            "stages_ms": stages}
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = config_cpu_baseline(wl, frame, index, ranges, args.cpu_samples)
     del frame
     torch.cuda.empty_cache()
     return out
+
+
+def config_cpu_baseline(wl, frame, index: int, ranges, samples: int) -> dict:
+    """The CPU oracle on a config's frame (same inputs as the GPU's): the median of `samples` full
+    fwd+bwd frames, with the loss when the GPU step has it; config 4 on the 64 tiles of its parity test
+    (tests/scenes.py tile_selection on the GPU binning's list lengths), at most 3 samples, without the
+    loss (its SSIM would run on a frame rendered only there); config 0 adds the dense float64 blend."""
+    from tests.scenes import tile_selection
+
+    x = oracle_inputs(wl, frame.colors, frame.grad_image, frame.grad_features)
+    if index == 4:
+        mask = tile_selection(ranges, (wl.width + 15) // 16)
+        samples = max(1, min(samples, 3))
+        record, _ = cpu_timing(x, samples, f"median of {samples} fwd+bwd of {wl.name} restricted to {int(mask.sum())} "
+                                           f"of {mask.size} tiles (the 16 longest lists + 48 at random, seed 0): "
+                                           "projection of every gaussian, binning and blend fwd+bwd on those "
+                                           "tiles; dL/dimage U[0, 1], no SSIM; C oracle, OpenMP",
+                               tile_mask=mask)
+        record["tile_masked"] = True
+        return record
+    target = None if frame.target is None else frame.target.detach().cpu().numpy()
+    record, _ = cpu_timing(x, samples, f"median of {samples} full fwd+bwd frames of {wl.name} (same inputs"
+                                       + (", 0.8 L1 + 0.2 (1 - SSIM)" if target is not None else "")
+                                       + ") on the C oracle, OpenMP", loss_target=target)
+    if index == 0:
+        record["dense_fp64"] = dense_fp64_timing(x)
+    return record
 
 
 def concurrent_span_ms(timeline, first: str, second: str) -> float:
@@ -703,43 +749,98 @@ def traffic_per_step(kernel_names, workload: str) -> int | None:
     return sum(per_kernel[k] for k in kernel_names)
 
 
-def cpu_baseline(wl, colors, grad_image, grad_features, loss_target=None):
-    """The CPU oracle (OpenMP, all host threads) on the same frame: projection, binning, blend forward,
-    blend backward and projection backward, once (with loss_target, dL/dimage of 0.8 L1 + 0.2 (1 - SSIM)
-    against it from the oracle's SSIM instead of grad_image). Sample = the full frame. Returns the
-    baseline record and the oracle's outputs in the leaves' shapes (for the agreement gate)."""
+def oracle_inputs(wl, colors, grad_image, grad_features, features=None) -> dict:
+    """The frame's inputs as the CPU oracle takes them (numpy float32 copies of the GPU's leaves and
+    upstream gradients; features default to the workload's)."""
+    import numpy as np
+
+    np_ = lambda t: t.detach().cpu().numpy()  # noqa: E731
+    return {"wl": wl, "means": np_(wl.means), "scales": np_(wl.scales),
+            "quats": np_(wl.quats / wl.quats.norm(dim=-1, keepdim=True)), "opacities": np_(wl.opacities),
+            "features": np_(wl.features if features is None else features), "colors": np_(colors),
+            "grad_image": np_(grad_image), "grad_features": np_(grad_features),
+            "w2c": np_(wl.world_to_camera).astype(np.float32)}
+
+
+def oracle_frame(x: dict, loss_target=None, tile_mask=None):
+    """One fwd+bwd of the frame on the C oracle (OpenMP): projection, binning, blend forward, then
+    (with loss_target, dL/dimage of 0.8 L1 + 0.2 (1 - SSIM) against it from the oracle's SSIM instead
+    of the given dL/dimage) blend backward and projection backward. With tile_mask the binning, and
+    so the blend, covers only the selected tiles. Returns the forward's and backward's seconds and the
+    outputs."""
+    import numpy as np
+
+    import oracle
+
+    cam, wl = x["wl"].cam, x["wl"]
+    W, H = wl.width, wl.height
+    bg = np.zeros(3, np.float32)
+    t0 = time.perf_counter()
+    m2, d, r, c = oracle.project_forward(x["means"], x["scales"], x["quats"], x["opacities"], x["w2c"], cam["fx"],
+                                         cam["fy"], cam["cx"], cam["cy"], W, H)
+    _, values, ranges = oracle.bin_gaussians(m2, d, r, c, x["opacities"], W, H, tile_mask=tile_mask)
+    image, T, nc, fimg = oracle.render_forward(W, H, ranges, values, m2, c, x["opacities"], x["colors"], bg,
+                                               x["features"])
+    t1 = time.perf_counter()
+    gi = x["grad_image"]
+    if loss_target is not None:
+        # d/dimage of 0.8 mean|image - target| + 0.2 (1 - mean SSIM): sign / numel, and the SSIM
+        # backward with dL/dmean = -0.2 (utils/loss.py:57-96 there).
+        gi = (0.8 * np.sign(image - loss_target) / image.size).astype(np.float32)
+        _, d_mu, d_aa, d_ab = oracle.ssim_forward(image, loss_target)
+        gi += oracle.ssim_backward(-0.2, image, loss_target, d_mu, d_aa, d_ab)
+    dm, dc, dcol, dop, df = oracle.render_backward(W, H, ranges, values, m2, c, x["opacities"], x["colors"], bg, T, nc,
+                                                   gi, x["features"], x["grad_features"])
+    dmeans, dscales, dq = oracle.project_backward(dm, dc, x["means"], x["scales"], x["quats"], x["w2c"], cam["fx"],
+                                                  cam["fy"], cam["cx"], cam["cy"], W, H)
+    t2 = time.perf_counter()
+    return t1 - t0, t2 - t1, {"image": image, "feature_image": fimg, "means2D": dm, "conics": dc, "colors": dcol,
+                              "opacities": dop, "features": df, "means": dmeans, "scales": dscales, "quats": dq}
+
+
+def host() -> dict:
+    """The host the CPU figures ran on: logical CPUs, the ones this process may use, the OpenMP
+    thread count the oracle ran with, and the CPU model."""
+    import oracle
+
+    return {"nproc": os.cpu_count(), "usable_cpus": len(os.sched_getaffinity(0)), "omp_threads": oracle.num_threads(),
+            "cpu": _cpu_model()}
+
+
+def cpu_timing(x: dict, samples: int, sample: str, loss_target=None, tile_mask=None):
+    """`samples` oracle fwd+bwd runs of the frame: the median total, forward and backward (ms), every
+    sample's total, and the host. Returns the record and the last run's outputs."""
+    import oracle
+
+    totals, fwds, bwds, out = [], [], [], None
+    for i in range(samples):
+        fwd, bwd, out = oracle_frame(x, loss_target=loss_target, tile_mask=tile_mask)
+        fwds.append(fwd * 1e3), bwds.append(bwd * 1e3), totals.append((fwd + bwd) * 1e3)
+        print(f"[bench] cpu baseline {x['wl'].name}: sample {i + 1}/{samples} {totals[-1]:.0f} ms",
+              file=sys.stderr, flush=True)
+    return ({"value": round(statistics.median(totals), 1), "unit": "ms", "cores": oracle.num_threads(),
+             "kind": "port", "fwd_ms": round(statistics.median(fwds), 1), "bwd_ms": round(statistics.median(bwds), 1),
+             "samples": samples, "samples_ms": [round(t, 1) for t in totals], "statistic": "median",
+             "sample": sample, **host()}, out)
+
+
+def cpu_baseline(wl, colors, grad_image, grad_features, samples: int, loss_target=None):
+    """The CPU oracle (OpenMP, all usable host threads) on the same frame, `samples` times (median;
+    fwd = projection + binning + blend forward, bwd = loss gradient + blend backward + projection
+    backward). Returns the baseline record and the oracle's outputs in the leaves' shapes (for the
+    agreement gate)."""
     import numpy as np
     import torch
 
     import oracle
 
-    np_ = lambda t: t.detach().cpu().numpy()  # noqa: E731
+    x = oracle_inputs(wl, colors, grad_image, grad_features)
+    target = None if loss_target is None else loss_target.detach().cpu().numpy()
+    print(f"[bench] cpu baseline: oracle fwd+bwd of the full frame, {samples} samples", file=sys.stderr, flush=True)
+    record, out = cpu_timing(x, samples, f"median of {samples} full fwd+bwd frames of {wl.name} (same inputs) on "
+                                         "the C oracle, OpenMP", loss_target=target)
     cam = wl.cam
-    means, scales = np_(wl.means), np_(wl.scales)
-    quats = np_(wl.quats / wl.quats.norm(dim=-1, keepdim=True))
-    opac, feats = np_(wl.opacities), np_(wl.features)
-    cols, gi, gf = np_(colors), np_(grad_image), np_(grad_features)
-    w2c = np_(wl.world_to_camera).astype(np.float32)
-    print("[bench] cpu baseline: oracle fwd+bwd of the full frame", file=sys.stderr, flush=True)
-    t0 = time.perf_counter()
-    m2, d, r, c = oracle.project_forward(means, scales, quats, opac, w2c, cam["fx"], cam["fy"], cam["cx"],
-                                         cam["cy"], cam["width"], cam["height"])
-    _, values, ranges = oracle.bin_gaussians(m2, d, r, c, opac, cam["width"], cam["height"])
-    image, T, nc, fimg = oracle.render_forward(cam["width"], cam["height"], ranges, values, m2, c, opac, cols,
-                                               np.zeros(3, np.float32), feats)
-    t1 = time.perf_counter()
-    if loss_target is not None:
-        # d/dimage of 0.8 mean|image - target| + 0.2 (1 - mean SSIM): sign / numel, and the SSIM
-        # backward with dL/dmean = -0.2 (utils/loss.py:57-96 there).
-        tgt = np_(loss_target)
-        gi = (0.8 * np.sign(image - tgt) / image.size).astype(np.float32)
-        _, d_mu, d_aa, d_ab = oracle.ssim_forward(image, tgt)
-        gi += oracle.ssim_backward(-0.2, image, tgt, d_mu, d_aa, d_ab)
-    dm, dc, dcol, dop, df = oracle.render_backward(cam["width"], cam["height"], ranges, values, m2, c, opac, cols,
-                                                   np.zeros(3, np.float32), T, nc, gi, feats, gf)
-    dmeans, dscales, dq = oracle.project_backward(dm, dc, means, scales, quats, w2c, cam["fx"], cam["fy"],
-                                                  cam["cx"], cam["cy"], cam["width"], cam["height"])
-    t2 = time.perf_counter()
+    means, scales, quats, w2c, feats = x["means"], x["scales"], x["quats"], x["w2c"], x["features"]
 
     def normalize_backward(d_unit):
         # The quats leaf goes through F.normalize before the projection: its gradient, on the CPU.
@@ -750,9 +851,9 @@ def cpu_baseline(wl, colors, grad_image, grad_features, loss_target=None):
     def forward_stage(m2_, d_, r_, c_, col_, op_):
         # The oracle's binning and blend forward on the GPU projection's outputs (identical inputs).
         _, values_, ranges_ = oracle.bin_gaussians(m2_, d_, r_, c_, op_, cam["width"], cam["height"])
-        out = oracle.render_forward(cam["width"], cam["height"], ranges_, values_, m2_, c_, op_, col_,
-                                    np.zeros(3, np.float32), feats)
-        return out[0], out[3]
+        out_ = oracle.render_forward(cam["width"], cam["height"], ranges_, values_, m2_, c_, op_, col_,
+                                     np.zeros(3, np.float32), feats)
+        return out_[0], out_[3]
 
     def projection_stage(grad_means2D, grad_conics):
         # The oracle's projection backward (and the normalize chain) on given upstream gradients.
@@ -760,14 +861,40 @@ def cpu_baseline(wl, colors, grad_image, grad_features, loss_target=None):
                                              cam["fy"], cam["cx"], cam["cy"], cam["width"], cam["height"])
         return {"means": pm, "scales": ps, "quats": normalize_backward(pq)}
 
-    want = {"image": image, "feature_image": fimg, "means2D": dm, "conics": dc,
-            "opacities": np.asarray(dop).reshape(-1), "colors": dcol, "features": df,
-            "chain": {"means": dmeans, "scales": dscales, "quats": normalize_backward(dq)},
+    want = {"image": out["image"], "feature_image": out["feature_image"], "means2D": out["means2D"],
+            "conics": out["conics"], "opacities": np.asarray(out["opacities"]).reshape(-1), "colors": out["colors"],
+            "features": out["features"],
+            "chain": {"means": out["means"], "scales": out["scales"], "quats": normalize_backward(out["quats"])},
             "projection_stage": projection_stage, "forward_stage": forward_stage}
-    return ({"value": round((t2 - t0) * 1e3, 1), "unit": "ms", "cores": oracle.num_threads(), "kind": "port",
-             "fwd_ms": round((t1 - t0) * 1e3, 1), "bwd_ms": round((t2 - t1) * 1e3, 1),
-             "sample": f"one full fwd+bwd frame of {wl.name} (same inputs) on the C oracle, OpenMP",
-             "cpu": _cpu_model()}, want)
+    return record, want
+
+
+def dense_fp64_timing(x: dict) -> dict:
+    """The dense float64 formulation (tests/dense_reference.py, the formulation of the reference's
+    tests/oracle.py:9-77: every pixel against every visible gaussian, torch autograd for the backward)
+    timed once on the frame's blend: the oracle's projection (not timed), then the blend of colours and
+    features as one [N, 3 + C] value per gaussian, forward and backward of dL/dimage and
+    dL/dfeature_image."""
+    import numpy as np
+    import torch
+
+    import oracle
+    from tests.dense_reference import dense_blend_grad
+
+    wl, cam = x["wl"], x["wl"].cam
+    m2, d, r, c = oracle.project_forward(x["means"], x["scales"], x["quats"], x["opacities"], x["w2c"], cam["fx"],
+                                         cam["fy"], cam["cx"], cam["cy"], wl.width, wl.height)
+    values = torch.from_numpy(np.concatenate([x["colors"], x["features"]], axis=1))
+    upstream = torch.from_numpy(np.concatenate([x["grad_image"], x["grad_features"]], axis=-1))
+    print(f"[bench] dense fp64 blend of {wl.name}, once", file=sys.stderr, flush=True)
+    _, _, fwd, bwd = dense_blend_grad(*(torch.from_numpy(a) for a in (m2, d, r, c)), values,
+                                      torch.from_numpy(x["opacities"]), wl.width, wl.height, upstream)
+    return {"value": round((fwd + bwd) * 1e3, 1), "unit": "ms", "fwd_ms": round(fwd * 1e3, 1),
+            "bwd_ms": round(bwd * 1e3, 1), "samples": 1, "kind": "dense fp64 (tests/dense_reference.py)",
+            "torch_threads": torch.get_num_threads(),
+            "sample": f"one dense float64 blend fwd+bwd of {wl.name} (RGB + {wl.channels} features as one "
+                      f"{3 + wl.channels}-wide value, {int((r > 0).sum())} visible gaussians x {wl.width * wl.height} "
+                      "pixels), the formulation of the reference's tests/oracle.py; projection not timed"}
 
 
 # Largest gradient error allowed by the gate, relative to max|want|: the parity tests' bar, from the

@@ -24,36 +24,76 @@ MAX_ALPHA = 0.99
 MIN_TRANSMITTANCE = 1e-4
 
 
-def dense_blend(means2D, depths, radii, conics, colors, opacities, width, height, background=None):
-    """[H, W, D] blend of every pixel against every visible gaussian, float64 torch (autograd-able)."""
+def _sorted_visible(means2D, depths, radii, conics, colors, opacities):
+    """The visible gaussians in blend order, as float64: means, conics, colours, opacities."""
     f64 = torch.float64
-    if background is None:
-        background = torch.zeros(colors.shape[1], dtype=f64)
     # Equal depths keep index order; the kernels sort the float bits of the depth, which for the
     # positive depths used here orders like the values.
     order = torch.sort(depths, stable=True).indices
     order = order[radii[order] > 0]
-    mean, conic, color = means2D[order].to(f64), conics[order].to(f64), colors[order].to(f64)
-    opacity = opacities[order, 0].to(f64)
+    return order, means2D[order].to(f64), conics[order].to(f64), colors[order].to(f64), opacities[order, 0].to(f64)
+
+
+def _pixel_centres(width, height):
     ys, xs = torch.meshgrid(torch.arange(height), torch.arange(width), indexing="ij")
-    pixels = torch.stack([xs, ys], dim=-1).reshape(-1, 2).to(f64) + 0.5
-    chunk = max(1, 2 ** 22 // max(1, len(order)))
-    out = []
-    for px in pixels.split(chunk):
-        d = px[:, None] - mean
-        dx, dy = d[..., 0], d[..., 1]
-        m = dx * (conic[:, 0] * dx + conic[:, 1] * dy) + dy * (conic[:, 1] * dx + conic[:, 2] * dy)
-        alpha = (opacity * torch.exp(-0.5 * m)).clamp(max=MAX_ALPHA)
-        alpha = torch.where(alpha >= MIN_ALPHA, alpha, torch.zeros_like(alpha))
-        post = torch.cumprod(1 - alpha, dim=1)
-        pre = torch.cat([torch.ones_like(post[:, :1]), post[:, :-1]], dim=1)
-        w = alpha * pre
-        # A gaussian that would push T below the floor ends the pixel: it and everything behind it
-        # are dropped (post is monotone, so the mask is a prefix).
-        w = torch.where(post >= MIN_TRANSMITTANCE, w, torch.zeros_like(w))
-        remaining = 1 - w.sum(dim=1, keepdim=True)
-        out.append(w @ color + background.to(f64) * remaining)
+    return torch.stack([xs, ys], dim=-1).reshape(-1, 2).to(torch.float64) + 0.5
+
+
+def _blend_pixels(px, mean, conic, color, opacity, background):
+    """[P, D] blend of the pixel centres px against every gaussian of the sorted visible list."""
+    d = px[:, None] - mean
+    dx, dy = d[..., 0], d[..., 1]
+    m = dx * (conic[:, 0] * dx + conic[:, 1] * dy) + dy * (conic[:, 1] * dx + conic[:, 2] * dy)
+    alpha = (opacity * torch.exp(-0.5 * m)).clamp(max=MAX_ALPHA)
+    alpha = torch.where(alpha >= MIN_ALPHA, alpha, torch.zeros_like(alpha))
+    post = torch.cumprod(1 - alpha, dim=1)
+    pre = torch.cat([torch.ones_like(post[:, :1]), post[:, :-1]], dim=1)
+    w = alpha * pre
+    # A gaussian that would push T below the floor ends the pixel: it and everything behind it
+    # are dropped (post is monotone, so the mask is a prefix).
+    w = torch.where(post >= MIN_TRANSMITTANCE, w, torch.zeros_like(w))
+    remaining = 1 - w.sum(dim=1, keepdim=True)
+    return w @ color + background * remaining
+
+
+def dense_blend(means2D, depths, radii, conics, colors, opacities, width, height, background=None):
+    """[H, W, D] blend of every pixel against every visible gaussian, float64 torch (autograd-able)."""
+    background = torch.zeros(colors.shape[1], dtype=torch.float64) if background is None else background.double()
+    _, mean, conic, color, opacity = _sorted_visible(means2D, depths, radii, conics, colors, opacities)
+    pixels = _pixel_centres(width, height)
+    chunk = max(1, 2 ** 22 // max(1, mean.shape[0]))
+    out = [_blend_pixels(px, mean, conic, color, opacity, background) for px in pixels.split(chunk)]
     return torch.cat(out).reshape(height, width, colors.shape[1])
+
+
+def dense_blend_grad(means2D, depths, radii, conics, colors, opacities, width, height, grad_image,
+                     chunk: int | None = None):
+    """Forward and backward of dense_blend with upstream gradient grad_image [H, W, D], one pixel
+    chunk at a time (`chunk` pixels, by default as many as keep one [pixels, gaussians] float64 array
+    at 32 MiB; each chunk's autograd graph is freed before the next, so memory stays at one chunk's). Pixels are independent, so the chunks' gradients add up to the full frame's. Returns the
+    [H, W, D] image and the float64 gradients of means2D [N, 2], conics [N, 3], colors [N, D] and
+    opacities [N, 1] (zero for culled gaussians), plus the forward's and backward's seconds."""
+    import time
+
+    f64 = torch.float64
+    leaves = [t.detach().to(f64).requires_grad_(True) for t in (means2D, conics, colors, opacities)]
+    order, *_ = _sorted_visible(means2D, depths, radii, conics, colors, opacities)
+    background = torch.zeros(colors.shape[1], dtype=f64)
+    pixels = _pixel_centres(width, height)
+    upstream = grad_image.reshape(-1, colors.shape[1]).to(f64)
+    chunk = chunk or max(1, 2 ** 22 // max(1, order.numel()))
+    out, t_fwd, t_bwd = [], 0.0, 0.0
+    for start in range(0, pixels.shape[0], chunk):
+        t0 = time.perf_counter()
+        mean, conic, color, opacity = (leaves[0][order], leaves[1][order], leaves[2][order], leaves[3][order, 0])
+        img = _blend_pixels(pixels[start:start + chunk], mean, conic, color, opacity, background)
+        t1 = time.perf_counter()
+        img.backward(upstream[start:start + chunk])
+        t_bwd += time.perf_counter() - t1
+        t_fwd += t1 - t0
+        out.append(img.detach())
+    grads = {name: leaf.grad for name, leaf in zip(("means2D", "conics", "colors", "opacities"), leaves)}
+    return torch.cat(out).reshape(height, width, colors.shape[1]), grads, t_fwd, t_bwd
 
 
 def quat_to_rotmat(q):

@@ -10,6 +10,7 @@ from __future__ import annotations
 import math
 from dataclasses import dataclass
 
+import numpy as np
 import torch
 import torch.nn.functional as F
 
@@ -137,3 +138,22 @@ def flat_scene(means2D: list, depths: list, sigmas: list, opacities: list, devic
 
 def tiles(width: int, height: int) -> int:
     return math.ceil(width / 16) * math.ceil(height / 16)
+
+
+def tile_selection(ranges: np.ndarray, tiles_x: int, seed: int = 0, longest: int = 16, random: int = 48) -> np.ndarray:
+    """Mask of the `longest` tiles with the longest lists plus `random` other tiles drawn with `seed`."""
+    lens = ranges[:, 1] - ranges[:, 0]
+    order = np.argsort(-lens, kind="stable")
+    mask = np.zeros(lens.size, bool)
+    mask[order[:longest]] = True
+    rest = np.flatnonzero(~mask)
+    mask[np.random.default_rng(seed).choice(rest, random, replace=False)] = True
+    return mask
+
+
+def pixel_mask(tile_mask: np.ndarray, width: int, height: int) -> np.ndarray:
+    """[H, W] bool: the pixels of the selected 16x16 tiles."""
+    tiles_x = (width + 15) // 16
+    grid = tile_mask.reshape(-1, tiles_x)
+    full = np.repeat(np.repeat(grid, 16, axis=0), 16, axis=1)
+    return full[:height, :width]

@@ -33,7 +33,7 @@ import oracle
 from gaussian_splatting.rasterizer import _get_rasterizer, rasterize
 from gaussian_splatting.rasterizer.projection import JACOBIAN_FOV_SCALE, LOW_PASS, NEAR_PLANE
 from gaussian_splatting.utils.loss import l1_loss, ssim
-from tests.scenes import synthetic_config, upstream, view_dirs
+from tests.scenes import pixel_mask, synthetic_config, tile_selection, upstream, view_dirs
 from tests.tolerances import assert_grads_close, assert_image_close, grad_error
 
 pytestmark = pytest.mark.gpu
@@ -60,26 +60,6 @@ def project_and_shade(wl):
                                         JACOBIAN_FOV_SCALE)
     colors = ext.eval_sh(wl.sh_dc.to(DEV), wl.sh_rest.to(DEV), view_dirs(means), 3, r)
     return m2, d, r, c, colors, opac
-
-
-def tile_selection(ranges: np.ndarray, tiles_x: int, seed: int = 0, longest: int = 16, random: int = 48) -> np.ndarray:
-    """Mask of the `longest` tiles with the longest lists plus `random` other tiles drawn with `seed`."""
-    lens = ranges[:, 1] - ranges[:, 0]
-    order = np.argsort(-lens, kind="stable")
-    mask = np.zeros(lens.size, bool)
-    mask[order[:longest]] = True
-    rest = np.flatnonzero(~mask)
-    mask[np.random.default_rng(seed).choice(rest, random, replace=False)] = True
-    return mask
-
-
-def pixel_mask(tile_mask: np.ndarray, width: int, height: int) -> np.ndarray:
-    """[H, W] bool: the pixels of the selected 16x16 tiles."""
-    tiles_x = (width + 15) // 16
-    ty, tx = np.divmod(np.arange(tile_mask.size), tiles_x)
-    grid = tile_mask.reshape(-1, tiles_x)
-    full = np.repeat(np.repeat(grid, 16, axis=0), 16, axis=1)
-    return full[:height, :width]
 
 
 def report_worst(name, got, want, extra: dict[str, np.ndarray], k: int = 5) -> str:

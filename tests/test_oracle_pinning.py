@@ -249,6 +249,28 @@ def test_backward_matches_autograd_of_dense_blend(seed, n, width, height, channe
                        [t.grad.numpy() for t in leaves])
 
 
+def test_chunked_dense_backward_equals_the_oracle_backward():
+    # dense_blend_grad (the dense float64 formulation bench.py times at config 0) splits the frame
+    # into pixel chunks, here 97 pixels, which cut image rows: its gradients must still be the
+    # oracle's, and its image the dense forward's.
+    width, height, n = 40, 32, 600
+    m2, d, r, c, col, op = project_scene(4, n, width, height)
+    rng = np.random.default_rng(4)
+    gimg = rng.uniform(0, 1, (height, width, 3)).astype(np.float32)
+    _, values, ranges = oracle.bin_gaussians(m2, d, r, c, op, width, height)
+    bg = np.zeros(3, np.float32)
+    _, T, nc, _ = oracle.render_forward(width, height, ranges, values, m2, c, op, col, bg)
+    got = oracle.render_backward(width, height, ranges, values, m2, c, op, col, bg, T, nc, gimg)
+    t = lambda a: torch.tensor(a)  # noqa: E731
+    image, grads, t_fwd, t_bwd = ref.dense_blend_grad(t(m2), t(d), t(r), t(c), t(col), t(op), width, height, t(gimg),
+                                                      chunk=97)
+    assert t_fwd > 0 and t_bwd > 0
+    np.testing.assert_allclose(image.numpy(), ref.dense_blend(t(m2), t(d), t(r), t(c), t(col), t(op), width,
+                                                              height).numpy(), rtol=0, atol=1e-12)
+    names = ("means2D", "conics", "colors", "opacities")
+    assert_grads_close(names, got[:4], [grads[k].numpy() for k in names])
+
+
 # ---- projection ---------------------------------------------------------------------------------
 
 def test_projection_closed_form_for_isotropic_gaussian_on_axis():
