@@ -8,10 +8,14 @@
 //      (ceil(log2 T) bits: 12 at 979x546, so 2 passes of 6 bits instead of 6 passes of 8).
 // Stability of both sorts gives exactly the reference's (tile, depth bits, index) order, so
 // values_sorted and tile_ranges equal the CPU oracle's bit for bit, and the pair sort moves
-// 8 B per pair and pass instead of 12. The tile-order variant (the autograd path) skips step 1:
-// the pairs are emitted in index order, sorted by tile, and each tile's list is then sorted by
-// (depth bits, index) in one work-group (tile_sort_kernel), the same order again. Everything is integer work; the only floating point is the
-// shared tile rectangle of hds_common.h.
+// 8 B per pair and pass instead of 12. The tile-order variant (the autograd path) skips step 1
+// and needs no pair sort at all: each chunk of 4096 gaussians counts its pairs per tile in LDS
+// (one column of a tile-major count matrix), one exclusive scan of that matrix gives every
+// (tile, chunk) run its place in the tile-major pair list and tile_ranges, and each chunk then
+// scatters its pairs into its runs (counting scatter); each tile's list is finally sorted by
+// (depth bits, index) in one work-group (tile_sort_kernel), the same order again. Frames whose
+// count matrix would exceed 2^24 words take the emit + pair sort by tile instead. Everything is
+// integer work; the only floating point is the shared tile rectangle of hds_common.h.
 //
 // Sorts and scans are single-pass: every radix pass is ONE launch in which each work-group ranks
 // its 4096-item partition in registers and LDS, publishes its per-digit counts, and reads the
@@ -47,6 +51,17 @@ constexpr int kHistWords = kHistCopies * kRadix;        // one pass's histogram 
 // before its first poll, so the failure is certain while every kernel still runs to its end.
 constexpr uint32_t kSpinLimit = HDS_LOOKBACK_LIMIT_DEFAULT;
 std::atomic<uint32_t> g_spin_limit{kSpinLimit};
+// Counting scatter of the tile-order binning: one work-group of kScatterThreads threads per chunk of
+// kChunk gaussians, with an LDS histogram of up to kHistBins tiles at a time. Workspaces reserve the
+// count matrix (chunks x tiles words) when it stays within kScatterWords; a test hook can only
+// lower the limit the path choice uses (hds_set_tile_scatter_limit), so a workspace always holds
+// what the chosen path needs.
+constexpr int kScatterThreads = 1024;
+constexpr int kScatterWaves = kScatterThreads / HDS_WAVE;
+constexpr int kChunk = 4 * kScatterThreads;
+constexpr int kHistBins = 8192;
+constexpr uint64_t kScatterWords = uint64_t(1) << 24;
+std::atomic<uint64_t> g_scatter_words{kScatterWords};
 
 static_assert(kRadix == kThreads, "one thread per radix bin");
 
@@ -409,8 +424,10 @@ int onesweep_sort(uint32_t* keys_a, uint32_t* vals_a, uint32_t* keys_b, uint32_t
 // out[i] = sum_{j<i} count[j]; the grand total goes to *total.
 // ---------------------------------------------------------------------------------------------
 
-__global__ __launch_bounds__(kThreads) void scan_kernel(const uint2* __restrict__ rects, int64_t n,
-														 uint32_t* __restrict__ out, uint64_t* status,
+// kRects: the counts are the w * h of rectangles (in = uint2 rects); else plain words (in =
+// uint32 counts, which may be `out` itself: a partition reads all its items before writing any).
+template <bool kRects>
+__global__ __launch_bounds__(kThreads) void scan_kernel(const void* in, int64_t n, uint32_t* out, uint64_t* status,
 														 uint32_t* ticket, uint32_t* error, uint32_t spin_limit,
 														 uint64_t* __restrict__ total) {
 	// Items go through LDS so that global loads and stores stay coalesced while each thread
@@ -425,8 +442,12 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(const uint2* __restrict_
 	for (int r = 0; r < kItemsPerThread; r++) {
 		const int j = r * kThreads + threadIdx.x;
 		const int64_t i = base + j;
-		const uint32_t wh = i < n ? rects[i].y : 0u;
-		s_items[j + j / 16] = (wh & 0xffffu) * (wh >> 16);
+		if constexpr (kRects) {
+			const uint32_t wh = i < n ? static_cast<const uint2*>(in)[i].y : 0u;
+			s_items[j + j / 16] = (wh & 0xffffu) * (wh >> 16);
+		} else {
+			s_items[j + j / 16] = i < n ? static_cast<const uint32_t*>(in)[i] : 0u;
+		}
 	}
 	__syncthreads();
 	uint32_t local[kItemsPerThread];
@@ -488,12 +509,45 @@ __device__ inline void zero_ranges(const ZeroRanges& z) {
 		for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < z.n[k]; i += stride) z.p[k][i] = 0u;
 }
 
-__global__ __launch_bounds__(kThreads) void prepare_kernel(
-	int64_t n, const float* __restrict__ means2D, const float* __restrict__ depths, const float* __restrict__ radii,
-	const float* __restrict__ conics, const float* __restrict__ colors, const float* __restrict__ opacities,
-	int tiles_x, int tiles_y, float4* __restrict__ conic4, float4* __restrict__ color_opacity4,
-	uint2* __restrict__ rects, uint32_t* __restrict__ depth_keys,
-	uint32_t* __restrict__ order, int passes, uint32_t* __restrict__ hist, ZeroRanges zero) {
+// The per-gaussian records of both binnings: the conic (and colour) packed with the opacity, the
+// tile rectangle ((x0 | y0 << 16), (w | h << 16)), zero for a culled gaussian, and the depth key.
+struct GaussianInputs {
+	const float* means2D;
+	const float* depths;
+	const float* radii;
+	const float* conics;
+	const float* colors;
+	const float* opacities;
+	int tiles_x, tiles_y;
+	float4* conic4;
+	float4* color_opacity4;
+	uint2* rects;
+	uint32_t* depth_keys;
+};
+
+// Writes gaussian i's records and returns its rectangle and depth key.
+__device__ inline uint2 prepare_gaussian(const GaussianInputs& in, int64_t i, uint32_t* key) {
+	const float radius = in.radii[i];
+	const float op = in.opacities[i];
+	const float a = in.conics[i * 3], b = in.conics[i * 3 + 1], c = in.conics[i * 3 + 2];
+	const float ux = in.means2D[i * 2], uy = in.means2D[i * 2 + 1];
+	in.conic4[i] = make_float4(a, b, c, op);
+	if (in.colors)
+		in.color_opacity4[i] = make_float4(in.colors[i * 3], in.colors[i * 3 + 1], in.colors[i * 3 + 2], op);
+	int x0 = 0, y0 = 0, w = 0, h = 0;
+	// !(radius > 0) culls NaN radii too (forward.cu:31-37).
+	const bool ok = radius > 0.0f && hds_tile_rect(ux, uy, a, b, c, op, in.tiles_x, in.tiles_y, &x0, &y0, &w, &h);
+	const uint2 rect = ok ? make_uint2((uint32_t)x0 | ((uint32_t)y0 << 16), (uint32_t)w | ((uint32_t)h << 16))
+						  : make_uint2(0u, 0u);
+	in.rects[i] = rect;
+	*key = hds_f2u(in.depths[i]);
+	in.depth_keys[i] = *key;
+	return rect;
+}
+
+__global__ __launch_bounds__(kThreads) void prepare_kernel(int64_t n, const GaussianInputs in,
+														   uint32_t* __restrict__ order, int passes,
+														   uint32_t* __restrict__ hist, ZeroRanges zero) {
 	__shared__ uint32_t s_hist[kMaxPasses][kRadix];
 	// Control words the later kernels of this binning need cleared (none of them is touched here:
 	// with passes > 0 the histograms were cleared by a launch before this one).
@@ -510,19 +564,7 @@ __global__ __launch_bounds__(kThreads) void prepare_kernel(
 		const bool valid = i < n;
 		uint32_t key = 0;
 		if (valid) {
-			const float radius = radii[i];
-			const float op = opacities[i];
-			const float a = conics[i * 3], b = conics[i * 3 + 1], c = conics[i * 3 + 2];
-			const float ux = means2D[i * 2], uy = means2D[i * 2 + 1];
-			conic4[i] = make_float4(a, b, c, op);
-			if (colors) color_opacity4[i] = make_float4(colors[i * 3], colors[i * 3 + 1], colors[i * 3 + 2], op);
-			int x0 = 0, y0 = 0, w = 0, h = 0;
-			// !(radius > 0) culls NaN radii too (forward.cu:31-37).
-			const bool ok = radius > 0.0f && hds_tile_rect(ux, uy, a, b, c, op, tiles_x, tiles_y, &x0, &y0, &w, &h);
-			rects[i] = ok ? make_uint2((uint32_t)x0 | ((uint32_t)y0 << 16), (uint32_t)w | ((uint32_t)h << 16))
-						  : make_uint2(0u, 0u);
-			key = hds_f2u(depths[i]);
-			depth_keys[i] = key;
+			prepare_gaussian(in, i, &key);
 			order[i] = (uint32_t)i;
 		}
 		count_digits(key, valid, passes, kRadixBits, s_hist);
@@ -784,12 +826,17 @@ __device__ void tile_sort_lds(uint64_t* s_keys, int* vals, int n, const uint32_t
 	for (int i = threadIdx.x; i < n; i += kThreads) vals[i] = (int)(uint32_t)s_keys[i];
 }
 
+// With pairs_total (the counting scatter), nothing is sorted when the binning outgrew its pair
+// buffers (P > cap) or its scan failed: the caller bins that frame again.
 __global__ __launch_bounds__(kThreads) void tile_sort_kernel(const int2* __restrict__ ranges, int* __restrict__ values,
 															 const uint32_t* __restrict__ depth_keys, int64_t n_gaussians,
-															 int64_t num_tiles, uint32_t* __restrict__ overflow) {
+															 int64_t num_tiles, uint32_t* __restrict__ overflow,
+															 const uint64_t* __restrict__ pairs_total, int64_t cap) {
 	__shared__ uint64_t s_keys[kTileSortMax];
 	const int64_t tile = blockIdx.x;
 	if (tile >= num_tiles) return;
+	if (pairs_total && (reinterpret_cast<const uint32_t*>(pairs_total + 1)[0] != 0u || *pairs_total > (uint64_t)cap))
+		return;
 	const int2 r = ranges[tile];
 	const int n = r.y - r.x;
 	if (n <= 1) return;
@@ -803,6 +850,147 @@ __global__ __launch_bounds__(kThreads) void tile_sort_kernel(const int2* __restr
 	else if (n <= 1024) tile_sort_registers<4>(s_keys, vals, n, depth_keys, n_gaussians);
 	else if (n <= kTileSortRegMax) tile_sort_registers<8>(s_keys, vals, n, depth_keys, n_gaussians);
 	else tile_sort_lds(s_keys, vals, n, depth_keys, n_gaussians);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Counting scatter (tile-order binning): prepare_tiles_kernel, scan_kernel<false> over the
+// tile-major count matrix, scatter_kernel, then tile_sort_kernel.
+// ---------------------------------------------------------------------------------------------
+
+// Calls f(tile, gaussian) for every pair of a wave's 64 consecutive gaussians (lane l holds
+// gaussian first + l and its rectangle rc, zero when culled or past n). The wave's pairs form one
+// run, which its lanes take 64 at a time; each lane finds its pair's gaussian as the last lane
+// whose exclusive offset (in the wave's 64 LDS words s_off) is <= the pair index, so gaussians
+// without tiles, which share their successor's offset, never own a pair (the emit kernel's search).
+template <typename F>
+__device__ inline void for_each_pair(uint2 rc, uint32_t first, int tiles_x, uint32_t* s_off, F&& f) {
+	const int lane = threadIdx.x & (HDS_WAVE - 1);
+	const uint32_t cnt = (rc.y & 0xffffu) * (rc.y >> 16);
+	uint32_t x = cnt;
+#pragma unroll
+	for (int off = 1; off < HDS_WAVE; off <<= 1) {
+		const uint32_t y = (uint32_t)__shfl_up((int)x, off, HDS_WAVE);
+		if (lane >= off) x += y;
+	}
+	const uint32_t run = (uint32_t)__shfl((int)x, HDS_WAVE - 1, HDS_WAVE);
+	s_off[lane] = x - cnt;
+	hds_wave_fence();
+	for (uint32_t base = 0; base < run; base += HDS_WAVE) {
+		const uint32_t p = base + (uint32_t)lane;
+		int j = 0;
+#pragma unroll
+		for (int step = HDS_WAVE / 2; step > 0; step >>= 1)
+			if (s_off[j + step] <= p) j += step;
+		const uint32_t jx = (uint32_t)__shfl((int)rc.x, j, HDS_WAVE);
+		const uint32_t jy = (uint32_t)__shfl((int)rc.y, j, HDS_WAVE);
+		if (p < run) {
+			uint32_t row, col;
+			divmod_small(p - s_off[j], jy & 0xffffu, row, col);
+			f(((jx >> 16) + row) * (uint32_t)tiles_x + (jx & 0xffffu) + col, first + (uint32_t)j);
+		}
+	}
+	// The next call rewrites s_off: every lane's reads above come first in the wave's LDS order.
+	hds_wave_fence();
+}
+
+// Gaussian i of thread t in round r of chunk c: c * kChunk + r * kScatterThreads + t, so that wave w
+// holds 64 consecutive gaussians in every round.
+__device__ inline int64_t chunk_gaussian(int64_t chunk, int r) {
+	return chunk * kChunk + (int64_t)r * kScatterThreads + threadIdx.x;
+}
+
+// Step 1: the records of one chunk (prepare_kernel's, without the index order) and the chunk's
+// pair count per tile, one LDS histogram of up to kHistBins tiles at a time, stored to column
+// `chunk` of the tile-major count matrix: counts[tile * chunks + chunk]. Also clears `zero` (the
+// control block the scan uses, tile_ranges) for the later launches.
+__global__ __launch_bounds__(kScatterThreads) void prepare_tiles_kernel(int64_t n, const GaussianInputs in,
+																		int64_t num_tiles, int64_t chunks,
+																		uint32_t* __restrict__ counts, ZeroRanges zero) {
+	__shared__ uint32_t s_bins[kHistBins];
+	__shared__ uint32_t s_off[kScatterWaves][HDS_WAVE];
+	zero_ranges(zero);
+	const int64_t chunk = blockIdx.x;
+	const int wave = threadIdx.x / HDS_WAVE;
+	uint2 rc[4];
+#pragma unroll
+	for (int r = 0; r < 4; r++) {
+		const int64_t i = chunk_gaussian(chunk, r);
+		uint32_t key;
+		rc[r] = i < n ? prepare_gaussian(in, i, &key) : make_uint2(0u, 0u);
+	}
+	for (int64_t w0 = 0; w0 < num_tiles; w0 += kHistBins) {
+		const int nb = (int)min((int64_t)kHistBins, num_tiles - w0);
+		for (int i = threadIdx.x; i < nb; i += kScatterThreads) s_bins[i] = 0u;
+		__syncthreads();
+#pragma unroll
+		for (int r = 0; r < 4; r++) {
+			const uint32_t first = (uint32_t)(chunk_gaussian(chunk, r) - (threadIdx.x & (HDS_WAVE - 1)));
+			for_each_pair(rc[r], first, in.tiles_x, s_off[wave], [&](uint32_t tile, uint32_t) {
+				const uint32_t b = tile - (uint32_t)w0;
+				if (b < (uint32_t)nb) atomicAdd(&s_bins[b], 1u);
+			});
+		}
+		__syncthreads();
+		for (int i = threadIdx.x; i < nb; i += kScatterThreads) counts[(w0 + i) * chunks + chunk] = s_bins[i];
+		__syncthreads();
+	}
+}
+
+// Step 3, after the exclusive scan of the count matrix (entry (tile, chunk) = where the chunk's run
+// of that tile starts in the tile-major pair list): the chunk's pairs go to their runs, the LDS copy
+// of the chunk's run starts serving as write cursors (one LDS atomic per pair; the order inside a
+// run is whatever the atomics make it, and tile_sort_kernel replaces it by (depth bits, index)).
+// Every work-group also writes a share of tile_ranges: [run start of (tile, chunk 0), run start of
+// (tile + 1, chunk 0)), (0, 0) when empty. Nothing at or past limit = min(P, cap) is written and the ranges are cut
+// there, so a binning whose pair buffers were too small still leaves only written entries inside its
+// ranges (the caller bins it again with exact buffers); a failed scan, or P beyond int32 indices,
+// writes nothing (tile_ranges were cleared by prepare_tiles_kernel). With pairs_total null, cap is
+// the exact pair count.
+__global__ __launch_bounds__(kScatterThreads) void scatter_kernel(int64_t n, const uint2* __restrict__ rects,
+																  int tiles_x, int64_t num_tiles, int64_t chunks,
+																  const uint32_t* __restrict__ starts,
+																  const uint64_t* __restrict__ pairs_total, int64_t cap,
+																  int32_t* __restrict__ values, int2* __restrict__ ranges) {
+	__shared__ uint32_t s_cursor[kHistBins];
+	__shared__ uint32_t s_off[kScatterWaves][HDS_WAVE];
+	int64_t total = cap;
+	if (pairs_total) {
+		if (reinterpret_cast<const uint32_t*>(pairs_total + 1)[0] != 0u) return;
+		total = (int64_t)min(*pairs_total, (uint64_t)INT32_MAX);
+	}
+	if (total >= INT32_MAX) return;
+	const int64_t limit = min(total, cap);
+	const int64_t chunk = blockIdx.x;
+	const int wave = threadIdx.x / HDS_WAVE;
+	for (int64_t t = chunk * kScatterThreads + threadIdx.x; t < num_tiles; t += chunks * kScatterThreads) {
+		const int64_t start = min((int64_t)starts[t * chunks], limit);
+		const int64_t end = min(t + 1 < num_tiles ? (int64_t)starts[(t + 1) * chunks] : total, limit);
+		// An empty range is (0, 0), as for a tile no pair touches (forward.cu:115-139).
+		ranges[t] = end > start ? make_int2((int)start, (int)end) : make_int2(0, 0);
+	}
+	uint2 rc[4];
+#pragma unroll
+	for (int r = 0; r < 4; r++) {
+		const int64_t i = chunk_gaussian(chunk, r);
+		rc[r] = i < n ? rects[i] : make_uint2(0u, 0u);
+	}
+	for (int64_t w0 = 0; w0 < num_tiles; w0 += kHistBins) {
+		const int nb = (int)min((int64_t)kHistBins, num_tiles - w0);
+		for (int i = threadIdx.x; i < nb; i += kScatterThreads) s_cursor[i] = starts[(w0 + i) * chunks + chunk];
+		__syncthreads();
+#pragma unroll
+		for (int r = 0; r < 4; r++) {
+			const uint32_t first = (uint32_t)(chunk_gaussian(chunk, r) - (threadIdx.x & (HDS_WAVE - 1)));
+			for_each_pair(rc[r], first, tiles_x, s_off[wave], [&](uint32_t tile, uint32_t g) {
+				const uint32_t b = tile - (uint32_t)w0;
+				if (b < (uint32_t)nb) {
+					const uint32_t pos = atomicAdd(&s_cursor[b], 1u);
+					if ((int64_t)pos < limit) values[pos] = (int32_t)g;
+				}
+			});
+		}
+		__syncthreads();
+	}
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -822,14 +1010,31 @@ struct Control {
 	uint32_t hist[kMaxPasses * kHistWords];
 };
 
-struct GaussianSpace {
-	size_t rects, rects_sorted, keys_a, vals_a, keys_b, vals_b, offsets, ctrl, status, scan_status, bytes;
+// Chunks of the counting scatter and the words of its count matrix (chunks x tiles); words = 0 when
+// the matrix would exceed `limit` words (the frame then takes the emit + pair sort).
+struct ScatterShape {
+	int64_t chunks;
+	uint64_t words;
 };
 
-GaussianSpace gaussian_space(int64_t n) {
+ScatterShape scatter_shape(int64_t n, int64_t num_tiles, uint64_t limit) {
+	const int64_t chunks = n > 0 ? (n + kChunk - 1) / kChunk : 0;
+	const uint64_t words = (uint64_t)chunks * (uint64_t)(num_tiles > 0 ? num_tiles : 0);
+	return {chunks, words <= limit ? words : 0};
+}
+
+// [ctrl, zero_end) is cleared before use; the count matrix after it is written whole by
+// prepare_tiles_kernel. num_tiles = 0 leaves out the matrix (the depth-order binning never uses it).
+struct GaussianSpace {
+	size_t rects, rects_sorted, keys_a, vals_a, keys_b, vals_b, offsets, ctrl, status, scan_status, counts_status,
+		zero_end, counts, bytes;
+};
+
+GaussianSpace gaussian_space(int64_t n, int64_t num_tiles = 0) {
 	GaussianSpace g;
 	const size_t items = (size_t)(n > 0 ? n : 1);
 	const size_t parts = (size_t)parts_of((int64_t)items);
+	const uint64_t words = scatter_shape(n, num_tiles, kScatterWords).words;
 	size_t o = 0;
 	g.rects = o; o = align256(o + 8 * items);
 	g.rects_sorted = o; o = align256(o + 8 * items);
@@ -841,6 +1046,9 @@ GaussianSpace gaussian_space(int64_t n) {
 	g.ctrl = o; o = align256(o + sizeof(Control));
 	g.status = o; o = align256(o + 8 * parts * kRadix);
 	g.scan_status = o; o = align256(o + 8 * parts);
+	g.counts_status = o; o = align256(o + 8 * (size_t)parts_of((int64_t)(words > 0 ? words : 1)));
+	g.zero_end = o;
+	g.counts = o; o = align256(o + 4 * words);
 	g.bytes = o;
 	return g;
 }
@@ -879,9 +1087,9 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 }  // namespace
 
 extern "C" size_t hds_bin_workspace_bytes(int64_t n, int width, int height) {
-	(void)width;
-	(void)height;
-	return gaussian_space(n).bytes;
+	const int64_t tiles_x = width > 0 ? (width + HDS_TILE - 1) / HDS_TILE : 0;
+	const int64_t tiles_y = height > 0 ? (height + HDS_TILE - 1) / HDS_TILE : 0;
+	return gaussian_space(n, tiles_x * tiles_y).bytes;
 }
 
 extern "C" size_t hds_pairs_workspace_bytes(int64_t num_pairs, int width, int height) {
@@ -893,15 +1101,18 @@ extern "C" size_t hds_pairs_workspace_bytes(int64_t num_pairs, int width, int he
 namespace {
 
 // Which count last filled each gaussian workspace: depth-sorted (hds_bin_count(_async)) or index
-// order (hds_bin_tile_order_async). The two leave different things in it (offsets scanned over the
-// depth order or over the index order, sorted or unsorted rectangles), so an emit checks the record
-// and rejects a workspace the other count filled, or one no count of this process filled, before it
-// enqueues anything. Keyed by address; the most recent kModeRecords workspaces are remembered.
+// order (hds_bin_tile_order_async, by the emit + pair sort or by the counting scatter). They leave
+// different things in it (offsets scanned over the depth order or over the index order, or the
+// scanned count matrix), so an emit checks the record and rejects a workspace another count
+// filled, or one no count of this process filled, before it enqueues anything; the tile-order emit
+// follows the recorded path. Keyed by address; the most recent kModeRecords workspaces are
+// remembered.
+enum CountMode { kModeDepth = 0, kModeTileEmit = 1, kModeTileScatter = 2 };
 constexpr size_t kModeRecords = 256;
 std::mutex g_mode_mutex;
-std::vector<std::pair<const void*, bool>> g_mode_records;  // (workspace, depth sorted), newest last
+std::vector<std::pair<const void*, int>> g_mode_records;  // (workspace, CountMode), newest last
 
-void record_count_mode(const void* workspace, bool depth_sort) {
+void record_count_mode(const void* workspace, int mode) {
 	std::lock_guard<std::mutex> lock(g_mode_mutex);
 	for (size_t i = 0; i < g_mode_records.size(); i++)
 		if (g_mode_records[i].first == workspace) {
@@ -909,16 +1120,20 @@ void record_count_mode(const void* workspace, bool depth_sort) {
 			break;
 		}
 	if (g_mode_records.size() == kModeRecords) g_mode_records.erase(g_mode_records.begin());
-	g_mode_records.emplace_back(workspace, depth_sort);
+	g_mode_records.emplace_back(workspace, mode);
 }
 
-int check_count_mode(const void* workspace, bool depth_sort, const char* entry) {
+// HDS_OK when the workspace was last filled in the depth order (depth_sort) or in tile order (not
+// depth_sort); *mode, when given, receives the recorded CountMode.
+int check_count_mode(const void* workspace, bool depth_sort, const char* entry, int* mode = nullptr) {
 	std::lock_guard<std::mutex> lock(g_mode_mutex);
 	for (const auto& r : g_mode_records)
 		if (r.first == workspace) {
-			if (r.second == depth_sort) return HDS_OK;
+			const bool depth = r.second == kModeDepth;
+			if (mode) *mode = r.second;
+			if (depth == depth_sort) return HDS_OK;
 			return hds_set_error(HDS_ERR_INVALID, "%s: the workspace was filled by %s, this emit needs %s", entry,
-								 r.second ? "hds_bin_count (depth order)" : "hds_bin_tile_order_async (tile order)",
+								 depth ? "hds_bin_count (depth order)" : "hds_bin_tile_order_async (tile order)",
 								 depth_sort ? "hds_bin_count's depth order" : "hds_bin_tile_order_async's tile order");
 		}
 	return hds_set_error(HDS_ERR_INVALID, "%s: the workspace was not filled by a count of this process (%s)", entry,
@@ -957,7 +1172,7 @@ int bin_count_launch(int64_t n, const float* means2D, const float* depths, const
 	uint64_t* status = at<uint64_t>(workspace, g.status);
 	uint64_t* scan_status = at<uint64_t>(workspace, g.scan_status);
 
-	const int64_t zero_words = (int64_t)(g.bytes - g.ctrl) / 4;
+	const int64_t zero_words = (int64_t)(g.zero_end - g.ctrl) / 4;
 	ZeroRanges zero{};
 	if (fused_zero) {
 		// Without the depth sort prepare keeps no histograms, so it clears the control blocks itself.
@@ -973,9 +1188,10 @@ int bin_count_launch(int64_t n, const float* means2D, const float* depths, const
 		HDS_LAUNCH_CHECK("zero_sort_control", s);
 	}
 	HdsKernelTimer timer2("prepare_kernel", s);
-	prepare_kernel<<<hds_blocks(n, 4 * kThreads), kThreads, 0, s>>>(
-		n, means2D, depths, radii, conics, colors, opacities, tiles_x, tiles_y, reinterpret_cast<float4*>(conic4),
-		reinterpret_cast<float4*>(color_opacity4), rects, keys_a, vals_a, depth_sort ? kMaxPasses : 0, ctrl->hist, zero);
+	const GaussianInputs in{means2D, depths, radii, conics, colors, opacities, tiles_x, tiles_y,
+							reinterpret_cast<float4*>(conic4), reinterpret_cast<float4*>(color_opacity4), rects, keys_a};
+	prepare_kernel<<<hds_blocks(n, 4 * kThreads), kThreads, 0, s>>>(n, in, vals_a, depth_sort ? kMaxPasses : 0,
+																	 ctrl->hist, zero);
 	timer2.stop();
 	HDS_LAUNCH_CHECK("prepare_gaussians", s);
 	if (depth_sort) {
@@ -988,12 +1204,12 @@ int bin_count_launch(int64_t n, const float* means2D, const float* depths, const
 	// Without the depth sort (tile order) the entries stay in index order: vals_a = identity,
 	// keys_a = each gaussian's depth key, and the scan and the emit read the rectangles as prepared.
 	HdsKernelTimer timer3("scan_kernel", s);
-	scan_kernel<<<(unsigned)parts_of(n), kThreads, 0, s>>>(depth_sort ? rects_sorted : rects, n, offsets, scan_status,
+	scan_kernel<true><<<(unsigned)parts_of(n), kThreads, 0, s>>>(depth_sort ? rects_sorted : rects, n, offsets, scan_status,
 															ctrl->tickets + kMaxPasses, &ctrl->error,
 															g_spin_limit.load(std::memory_order_relaxed), &ctrl->total);
 	timer3.stop();
 	HDS_LAUNCH_CHECK("scan_tile_counts", s);
-	record_count_mode(workspace, depth_sort);
+	record_count_mode(workspace, depth_sort ? kModeDepth : kModeTileEmit);
 	*launched = true;
 	return HDS_OK;
 }
@@ -1082,11 +1298,86 @@ int bin_emit_launch(int64_t n, int64_t num_pairs, bool exact, bool tile_order, i
 		HdsKernelTimer timer4("tile_sort_kernel", s);
 		tile_sort_kernel<<<(unsigned)num_tiles, kThreads, 0, s>>>(
 			reinterpret_cast<const int2*>(tile_ranges), values_sorted, at<uint32_t>(ws, g.keys_a), n, num_tiles,
-			&at<Control>(ws, g.ctrl)->pair_error);
+			&at<Control>(ws, g.ctrl)->pair_error, nullptr, 0);
 		timer4.stop();
 		HDS_LAUNCH_CHECK("tile_depth_order", s);
 	}
 	return HDS_OK;
+}
+
+// The counting scatter's second half: the pairs into their runs and tile_ranges (scatter_kernel),
+// then each tile's depth order. With exact, cap is the pair count; otherwise it is the capacity of
+// values_sorted and the kernels read P (and the scan's error flag) from the workspace.
+int scatter_emit_launch(int64_t n, int64_t cap, bool exact, int width, int height, void* workspace,
+						int32_t* values_sorted, int32_t* tile_ranges, hipStream_t s) {
+	const int tiles_x = (width + HDS_TILE - 1) / HDS_TILE, tiles_y = (height + HDS_TILE - 1) / HDS_TILE;
+	const int64_t num_tiles = (int64_t)tiles_x * tiles_y;
+	const GaussianSpace g = gaussian_space(n, num_tiles);
+	const ScatterShape sh = scatter_shape(n, num_tiles, kScatterWords);
+	Control* ctrl = at<Control>(workspace, g.ctrl);
+	const uint64_t* total = exact ? nullptr : &ctrl->total;
+	HdsKernelTimer timer1("scatter_kernel", s);
+	scatter_kernel<<<(unsigned)sh.chunks, kScatterThreads, 0, s>>>(
+		n, at<uint2>(workspace, g.rects), tiles_x, num_tiles, sh.chunks, at<uint32_t>(workspace, g.counts), total, cap,
+		values_sorted, reinterpret_cast<int2*>(tile_ranges));
+	timer1.stop();
+	HDS_LAUNCH_CHECK("scatter_pairs", s);
+	HdsKernelTimer timer2("tile_sort_kernel", s);
+	tile_sort_kernel<<<(unsigned)num_tiles, kThreads, 0, s>>>(reinterpret_cast<const int2*>(tile_ranges),
+															 values_sorted, at<uint32_t>(workspace, g.keys_a), n,
+															 num_tiles, &ctrl->pair_error, total, cap);
+	timer2.stop();
+	HDS_LAUNCH_CHECK("tile_depth_order", s);
+	return HDS_OK;
+}
+
+// The whole tile-order binning by counting scatter (n > 0, the matrix within the path's limit):
+// prepare_tiles_kernel (records, per-chunk tile counts, clearing the control block and tile_ranges
+// on the side), the exclusive scan of the count matrix (run starts; P and the look-back flag into
+// the control block), then scatter_emit_launch.
+int bin_tile_scatter_launch(int64_t n, const float* means2D, const float* depths, const float* radii,
+							const float* conics, const float* colors, const float* opacities, int width, int height,
+							float* conic4, float* color_opacity4, void* workspace, size_t workspace_bytes,
+							int64_t capacity, int32_t* values_sorted, int32_t* tile_ranges, hipStream_t s) {
+	HDS_REQUIRE(n > 0 && n < INT32_MAX, "bin_tile_order: gaussian count %lld outside [1, 2^31)", (long long)n);
+	const int tiles_x = (width + HDS_TILE - 1) / HDS_TILE, tiles_y = (height + HDS_TILE - 1) / HDS_TILE;
+	HDS_REQUIRE(tiles_x < 65536 && tiles_y < 65536, "bin_tile_order: image %dx%d has too many tiles", width, height);
+	const int64_t num_tiles = (int64_t)tiles_x * tiles_y;
+	const GaussianSpace g = gaussian_space(n, num_tiles);
+	const ScatterShape sh = scatter_shape(n, num_tiles, kScatterWords);
+	HDS_REQUIRE(workspace && workspace_bytes >= g.bytes, "bin_tile_order: workspace of %zu bytes, need %zu",
+				workspace_bytes, g.bytes);
+	HDS_REQUIRE(means2D && depths && radii && conics && opacities && conic4, "bin_tile_order: null pointer argument");
+	HDS_REQUIRE(colors == nullptr || color_opacity4 != nullptr,
+				"bin_tile_order: colors given without color_opacity4");
+	HDS_REQUIRE(aligned16(conic4) && (!color_opacity4 || aligned16(color_opacity4)),
+				"bin_tile_order: conic4 / color_opacity4 must be 16-byte aligned");
+	Control* ctrl = at<Control>(workspace, g.ctrl);
+	uint32_t* counts = at<uint32_t>(workspace, g.counts);
+	// Cleared on the side: the control block (P, flags, the scan's ticket), the scan's status words
+	// and tile_ranges (left empty if the scan fails).
+	ZeroRanges zero{};
+	zero.p[0] = at<uint32_t>(workspace, g.ctrl);
+	zero.n[0] = (int64_t)sizeof(Control) / 4;
+	zero.p[1] = at<uint32_t>(workspace, g.counts_status);
+	zero.n[1] = (int64_t)(g.zero_end - g.counts_status) / 4;
+	zero.p[2] = reinterpret_cast<uint32_t*>(tile_ranges);
+	zero.n[2] = 2 * num_tiles;
+	const GaussianInputs in{means2D, depths, radii, conics, colors, opacities, tiles_x, tiles_y,
+							reinterpret_cast<float4*>(conic4), reinterpret_cast<float4*>(color_opacity4),
+							at<uint2>(workspace, g.rects), at<uint32_t>(workspace, g.keys_a)};
+	HdsKernelTimer timer1("prepare_tiles_kernel", s);
+	prepare_tiles_kernel<<<(unsigned)sh.chunks, kScatterThreads, 0, s>>>(n, in, num_tiles, sh.chunks, counts, zero);
+	timer1.stop();
+	HDS_LAUNCH_CHECK("prepare_tile_counts", s);
+	HdsKernelTimer timer2("scan_kernel", s);
+	scan_kernel<false><<<(unsigned)parts_of((int64_t)sh.words), kThreads, 0, s>>>(
+		counts, (int64_t)sh.words, counts, at<uint64_t>(workspace, g.counts_status), ctrl->tickets + kMaxPasses,
+		&ctrl->error, g_spin_limit.load(std::memory_order_relaxed), &ctrl->total);
+	timer2.stop();
+	HDS_LAUNCH_CHECK("scan_tile_counts", s);
+	record_count_mode(workspace, kModeTileScatter);
+	return scatter_emit_launch(n, capacity, false, width, height, workspace, values_sorted, tile_ranges, s);
 }
 
 }  // namespace
@@ -1149,6 +1440,11 @@ extern "C" int hds_set_lookback_limit(uint32_t polls) {
 	return HDS_OK;
 }
 
+extern "C" int hds_set_tile_scatter_limit(uint64_t words) {
+	g_scatter_words.store(words == 0 || words > kScatterWords ? kScatterWords : words, std::memory_order_relaxed);
+	return HDS_OK;
+}
+
 extern "C" int hds_bin_emit(int64_t n, int64_t num_pairs, int width, int height, void* workspace,
 							void* pairs_workspace, size_t pairs_workspace_bytes, int32_t* values_sorted,
 							int32_t* tile_ranges, hds_stream_t stream) {
@@ -1174,9 +1470,17 @@ extern "C" int hds_bin_emit_capped(int64_t n, int64_t capacity, int width, int h
 extern "C" int hds_bin_emit_tile_order(int64_t n, int64_t num_pairs, int width, int height, void* workspace,
 									   void* pairs_workspace, size_t pairs_workspace_bytes, int32_t* values_sorted,
 									   int32_t* tile_ranges, hds_stream_t stream) {
+	int mode = kModeTileEmit;
 	if (n > 0 && num_pairs > 0) {
-		const int st = check_count_mode(workspace, false, "bin_emit_tile_order");
+		const int st = check_count_mode(workspace, false, "bin_emit_tile_order", &mode);
 		if (st != HDS_OK) return st;
+	}
+	if (mode == kModeTileScatter) {
+		HDS_REQUIRE(width > 0 && height > 0, "bin_emit: image size %dx%d must be positive", width, height);
+		HDS_REQUIRE(num_pairs < INT32_MAX, "bin_emit: pair count %lld outside [0, 2^31)", (long long)num_pairs);
+		HDS_REQUIRE(tile_ranges && values_sorted, "bin_emit: null values_sorted / tile_ranges");
+		return scatter_emit_launch(n, num_pairs, true, width, height, workspace, values_sorted, tile_ranges,
+								   (hipStream_t)stream);
 	}
 	return bin_emit_launch(n, num_pairs, true, true, width, height, workspace, pairs_workspace, pairs_workspace_bytes,
 						   values_sorted, tile_ranges, (hipStream_t)stream);
@@ -1200,10 +1504,19 @@ extern "C" int hds_bin_tile_order_async(int64_t n, const float* means2D, const f
 		return bin_emit_launch(0, 0, false, true, width, height, workspace, pairs_workspace, pairs_workspace_bytes,
 							   values_sorted, tile_ranges, s);
 	}
+	HDS_REQUIRE(capacity == 0 || values_sorted, "bin_tile_order: null values_sorted");
+	if (scatter_shape(n, num_tiles, g_scatter_words.load(std::memory_order_relaxed)).words > 0) {
+		// Counting scatter: no pair workspace is used.
+		int st = bin_tile_scatter_launch(n, means2D, depths, radii, conics, colors, opacities, width, height, conic4,
+										 color_opacity4, workspace, workspace_bytes, capacity, values_sorted,
+										 tile_ranges, s);
+		if (st != HDS_OK) return st;
+		HDS_HIP(hipMemcpyAsync(status_host, count_words(workspace, n), sizeof(CountWords), hipMemcpyDeviceToHost, s));
+		return HDS_OK;
+	}
 	const PairSpace p = pair_space(capacity);
 	HDS_REQUIRE(pairs_workspace && pairs_workspace_bytes >= p.bytes,
 				"bin_tile_order: pairs workspace of %zu bytes, need %zu", pairs_workspace_bytes, p.bytes);
-	HDS_REQUIRE(capacity == 0 || values_sorted, "bin_tile_order: null values_sorted");
 	// prepare clears the gaussian control block (slot 0, filled in by bin_count_launch), the pair
 	// control block and the tile ranges, so neither half launches a zeroing kernel of its own.
 	ZeroRanges zero{};

@@ -51,6 +51,7 @@ PROTOTYPES = {
     "hds_bin_emit_tile_order": (_i32, [_i64, _i64, _i32, _i32, _vp, _vp, _sz, _vp, _vp, _vp]),
     "hds_bin_status": (_i32, [_i64, _vp, _vp, _vp]),
     "hds_set_lookback_limit": (_i32, [ctypes.c_uint32]),
+    "hds_set_tile_scatter_limit": (_i32, [ctypes.c_uint64]),
     "hds_bin_static": (_i32, [_i64, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _vp, _vp, _i64, _vp, _vp, _vp, _vp]),
     "hds_render": (_i32, [_i64, _i32, _i32, _i32, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                           _vp]),

@@ -91,7 +91,10 @@ HDS_API int hds_eval_sh_backward_adam(int64_t n, int degree, const float* grad_r
 
 /* ---- binning: replaces the binning half of rasterize (forward.cu:239-405) ------------------ */
 
-/* Bytes of the per-gaussian workspace hds_bin_count fills and hds_bin_emit reads. */
+/* Bytes of the per-gaussian workspace hds_bin_count / hds_bin_tile_order_async fill and the emits
+ * read. It includes the tile-order binning's count matrix (4 bytes per tile and chunk of 4096
+ * gaussians) when that stays within 2^24 words; width = height = 0 leaves the matrix out (enough
+ * for the depth-order binning). */
 HDS_API size_t hds_bin_workspace_bytes(int64_t n, int width, int height);
 
 /* forward.cu:284-326: culls, packs conic4 / color_opacity4 (colors may be NULL), counts the
@@ -141,12 +144,17 @@ HDS_API int hds_bin_emit_capped(int64_t n, int64_t capacity, int width, int heig
 						int32_t* tile_ranges, hds_stream_t stream);
 
 /* The whole binning (forward.cu:284-404) in one call for a pair count the host has not read yet,
- * with the depth order built per tile: no global depth sort; the tile counts are scanned and the
- * pairs emitted in gaussian-index order, the pairs are sorted by tile alone, and each tile's list is
- * then sorted by (depth bits, index) in one work-group, which gives the reference's (tile, depth
- * bits, index) order. values_sorted, tile_ranges, conic4 and color_opacity4 equal hds_bin_count +
- * hds_bin_emit's bit for bit, under hds_bin_emit_capped's capacity contract (values_sorted and
- * pairs_workspace sized for `capacity` pairs; hds_pairs_workspace_bytes(capacity)). The call ends
+ * with the depth order built per tile: no global depth sort. Each chunk of 4096 gaussians counts
+ * its pairs per tile, one exclusive scan over (tile, chunk) places every chunk's run of every tile,
+ * the pairs are scattered into their runs (counting scatter), and each tile's list is then sorted
+ * by (depth bits, index) in one work-group, which gives the reference's (tile, depth bits, index)
+ * order. When the count matrix (chunks x tiles) exceeds 2^24 words, the tile counts are scanned, the
+ * pairs emitted in gaussian-index order and sorted by tile alone instead, before the same per-tile
+ * sort. values_sorted, tile_ranges, conic4 and color_opacity4 equal hds_bin_count + hds_bin_emit's
+ * bit for bit, under hds_bin_emit_capped's capacity contract (values_sorted sized for `capacity`
+ * pairs; when P > capacity, tile_ranges are cut at `capacity` and everything inside them is
+ * written, but the binning is incomplete). The pairs workspace (hds_pairs_workspace_bytes(capacity))
+ * is used only when the count matrix is too large; it may be NULL otherwise. The call ends
  * with an asynchronous copy of the 16 status bytes of hds_bin_status to status_host (pinned host
  * memory), valid once the stream has passed the call. It takes tile lists of up to 4096 pairs: a
  * longer one is left in index order and flagged (bit 1 of the tile-sort word), and the caller bins
@@ -180,6 +188,13 @@ HDS_API int hds_bin_status(int64_t n, const void* workspace, void* status_host, 
 #define HDS_LOOKBACK_LIMIT_DEFAULT 4194304u
 HDS_API int hds_set_lookback_limit(uint32_t polls);
 
+/* No counterpart in the reference; for tests of the tile-order binning's two paths. The largest
+ * count matrix (chunks x tiles words) hds_bin_tile_order_async takes the counting scatter for; 0
+ * restores the default, 2^24, which is also the most a workspace reserves room for. Applies to
+ * calls made after it, on every thread; hds_bin_emit_tile_order follows the path its workspace's
+ * count took. */
+HDS_API int hds_set_tile_scatter_limit(uint64_t words);
+
 /* No counterpart in the reference. For callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc): hds_bin_count_async
  * followed by hds_bin_emit_capped in one call, with both workspaces in a static device array of
@@ -190,8 +205,8 @@ HDS_API int hds_set_lookback_limit(uint32_t polls);
  * that receive uint64 P, uint32 depth-sort / scan flag, uint32 tile-sort flag once the stream has
  * passed this call. As with hds_bin_emit_capped, the binning is complete when P <= capacity and
  * both flags are zero; otherwise call again with a larger capacity. Rejects (status 1) a gaussian
- * count and capacity whose workspaces exceed the scratch: hds_bin_workspace_bytes(n) +
- * hds_pairs_workspace_bytes(capacity) must fit, which holds for 1.5M gaussians with 4M pairs.
+ * count and capacity whose workspaces exceed the scratch: hds_bin_workspace_bytes(n, 0, 0) +
+ * hds_pairs_workspace_bytes(capacity, 0, 0) must fit, which holds for 1.5M gaussians with 4M pairs.
  * Every call on a GPU shares that GPU's scratch: calls that overlap on one GPU (other streams,
  * other host threads) race and must be serialised by the caller. */
 #define HDS_BIN_STATIC_SCRATCH_MIB 112

@@ -80,6 +80,11 @@ def test_workspace_queries_grow_with_the_problem(lib):
     small = lib.hds_bin_workspace_bytes(1000, 128, 128)
     big = lib.hds_bin_workspace_bytes(1_000_000, 128, 128)
     assert 0 < small < big and big >= 7 * 4 * 1_000_000
+    # The tile-order count matrix: 4 bytes per (tile, 4096-gaussian chunk), 245 x 64 here, which the
+    # depth-order size (no tiles) leaves out; above 2^24 words it is not reserved at all.
+    assert big - lib.hds_bin_workspace_bytes(1_000_000, 0, 0) >= 4 * 245 * 64
+    assert (lib.hds_bin_workspace_bytes(4096 * 4097, 64 * 16, 64 * 16)
+            - lib.hds_bin_workspace_bytes(4096 * 4097, 0, 0)) < 1 << 20
     assert lib.hds_pairs_workspace_bytes(10_000, 64, 64) >= 3 * 4 * 10_000
 
 
@@ -115,8 +120,15 @@ def test_tile_order_binning_rejects_bad_arguments_before_launch(lib):
     assert call(status=None) == 1 and b"null status_host" in lib.hds_last_error()
     assert call(capacity=-1) == 1 and b"capacity" in lib.hds_last_error()
     assert call(width=0) == 1 and b"must be positive" in lib.hds_last_error()
-    assert call(pairs_bytes=16) == 1 and b"pairs workspace" in lib.hds_last_error()
     assert call(workspace_bytes=16) == 1 and b"workspace of 16 bytes" in lib.hds_last_error()
+    # The counting scatter (a 1 x 4 count matrix here) uses no pairs workspace; the emit + pair sort,
+    # which a matrix above the limit takes, checks it.
+    assert call(pairs_bytes=16, workspace_bytes=16) == 1 and b"workspace of 16 bytes" in lib.hds_last_error()
+    assert lib.hds_set_tile_scatter_limit(1) == 0
+    try:
+        assert call(pairs_bytes=16) == 1 and b"pairs workspace" in lib.hds_last_error()
+    finally:
+        assert lib.hds_set_tile_scatter_limit(0) == 0
 
 
 def test_emits_reject_a_workspace_no_matching_count_filled(lib):

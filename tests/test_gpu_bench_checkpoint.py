@@ -54,13 +54,18 @@ def test_bench_times_a_checkpoint_frame_that_agrees_with_the_oracle(tmp_path, mo
 
 def test_bench_times_another_config_with_its_loss():
     """bench.py's other-config pass (configs 0, 1 and 4 after the headline): config 0 runs its step with
-    the L1 + SSIM loss and reports the step, the harness split, the blend backward and the stages."""
+    the L1 + SSIM loss and reports the step, the harness split, the blend backward and the stages, and
+    beside them the CPU oracle's median fwd+bwd of the same frame and the dense float64 blend."""
     import argparse
 
     import bench
 
     print("[test] bench.measure_config(0)", file=sys.stderr, flush=True)
-    out = bench.measure_config(0, argparse.Namespace(steps=3))
+    out = bench.measure_config(0, argparse.Namespace(steps=3, no_cpu_baseline=False, cpu_samples=2))
+    cpu = out["cpu_baseline"]
+    assert cpu["samples"] == 2 and len(cpu["samples_ms"]) == 2 and cpu["value"] > 0 and cpu["kind"] == "port"
+    assert cpu["fwd_ms"] > 0 and cpu["bwd_ms"] > 0 and cpu["nproc"] >= 1 and "SSIM" in cpu["sample"]
+    assert cpu["dense_fp64"]["samples"] == 1 and cpu["dense_fp64"]["value"] > 0
     assert out["config"] == 0 and out["workload"].startswith("cpu-plumbing-10k")
     assert out["loss"].startswith("0.8 L1")
     assert out["gaussians"] == 10_000 and out["channels"] == 32

@@ -87,3 +87,24 @@ def test_failed_depth_sort_fails_the_count_and_the_async_resolve(lib):
     lib.hds_set_lookback_limit(DEFAULT_LIMIT)
     values, ranges, _, _ = ext.bin(m2, d, r, c, None, op, width, height)
     assert torch.equal(values, want_values) and torch.equal(ranges, want_ranges)
+
+
+def test_failed_tile_count_scan_fails_the_resolve_and_leaves_every_range_empty(lib):
+    """Tile order by counting scatter: when the scan of the (tile, chunk) count matrix gives up, the
+    scatter writes nothing, the per-tile sort does not run, every tile range stays (0, 0) and resolve()
+    raises; with the default limit restored the next tile-order binning equals the depth-order one."""
+    m2, d, r, c, op, width, height = scene()
+    ext = HipRasterizer()
+    want_values, want_ranges, _, _ = ext.bin(m2, d, r, c, None, op, width, height)
+    ext._pair_capacity[m2.device.index] = want_values.numel()
+    ext.tile_order = True
+    lib.hds_set_lookback_limit(0)
+    bins = ext.bin_async(m2, d, r, c, None, op, width, height)
+    torch.cuda.synchronize()
+    with pytest.raises(RuntimeError, match="look-back did not complete"):
+        ext.resolve(bins)
+    assert int(bins.tile_ranges.abs().sum()) == 0, "a failed count scan writes no range"
+    lib.hds_set_lookback_limit(DEFAULT_LIMIT)
+    bins = ext.bin_async(m2, d, r, c, None, op, width, height)
+    assert not ext.resolve(bins)
+    assert torch.equal(bins.values, want_values) and torch.equal(bins.tile_ranges, want_ranges)

@@ -266,6 +266,48 @@ def test_async_binning_equals_the_oracle_whatever_the_capacity(capacity, order):
     assert bool(torch.isfinite(T).all())
 
 
+@pytest.mark.parametrize("path", ["scatter", "emit"])
+@pytest.mark.parametrize("frame", ["mid", "wide"])
+def test_tile_order_binning_paths_equal_the_oracle(path, frame):
+    """Both tile-order paths bin like the oracle bit for bit: the counting scatter (per-chunk LDS tile
+    histograms, one scan over the (tile, chunk) count matrix, pairs scattered into their runs, then
+    the per-tile depth sort) and the emit + pair sort by tile that frames with a count matrix above
+    the limit take (forced here with hds_set_tile_scatter_limit). "wide" is a 2048x1088 frame of 8704
+    tiles, more than one LDS histogram holds (8192), so the counts and the scatter run in two
+    windows of tiles."""
+    from gaussian_splatting.rasterizer._native import HipRasterizer, load_library
+
+    if frame == "mid":
+        wl = synthetic_config(1, n=120_000, channels=1)
+        (m2, d, r, c), _ = project_both(wl.means, wl.scales, wl.quats, wl.opacities, wl.cam)
+        opac, width, height = wl.opacities.to(DEV), wl.width, wl.height
+    else:
+        g = torch.Generator().manual_seed(31)
+        n, width, height = 150_000, 2048, 1088
+        m2 = torch.rand(n, 2, generator=g) * torch.tensor([float(width), float(height)])
+        d = 1.0 + torch.rand(n, generator=g) * 9.0
+        sigma = 0.5 + torch.rand(n, generator=g) * 6.0
+        c = torch.stack([sigma ** -2, torch.zeros(n), sigma ** -2], -1)
+        r = 3.0 * sigma
+        opac = (0.05 + 0.9 * torch.rand(n, generator=g))[:, None]
+        m2, d, r, c, opac = (t.contiguous().to(DEV) for t in (m2, d, r, c, opac))
+    counts, want_values, want_ranges = oracle.bin_gaussians(np_(m2), np_(d), np_(r), np_(c), np_(opac), width,
+                                                            height)
+    lib = load_library()
+    ext = HipRasterizer()
+    ext._pair_capacity[m2.device.index] = int(counts.sum()) + 4096
+    ext.tile_order = True
+    print(f"[test] tile-order binning by {path}, {frame} frame {width}x{height}", file=sys.stderr, flush=True)
+    assert lib.hds_set_tile_scatter_limit(1 if path == "emit" else 0) == 0
+    try:
+        bins = ext.bin_async(m2, d, r, c, None, opac, width, height)
+        assert not ext.resolve(bins)
+    finally:
+        assert lib.hds_set_tile_scatter_limit(0) == 0
+    np.testing.assert_array_equal(np_(bins.values), want_values)
+    np.testing.assert_array_equal(np_(bins.tile_ranges), want_ranges)
+
+
 def _one_tile_scene(n, seed):
     """n small gaussians whose footprints all lie inside tile 0 of a 64x64 image (one list of n
     pairs), with depths drawn from 50 values so that ties occur."""
