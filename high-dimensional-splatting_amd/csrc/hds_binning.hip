@@ -748,21 +748,51 @@ __device__ inline uint64_t shfl_xor_u64(uint64_t v, int mask) {
 
 // One side of a bitonic compare-exchange: the element keeps the smaller of (v, partner p) when
 // keep_min (the pair's lower index in an ascending block, or its upper index in a descending one),
-// else the larger: it takes p exactly when (v > p) == keep_min. One 64-bit compare and two selects.
-__device__ inline uint64_t bitonic_keep(uint64_t v, uint64_t p, bool keep_min) {
+// else the larger: it takes p exactly when (v > p) == keep_min. One compare and one select per
+// 32 bits.
+template <typename K>
+__device__ inline K bitonic_keep(K v, K p, bool keep_min) {
 	return (v > p) == keep_min ? p : v;
 }
 
-// n <= 256 * E; thread t holds keys t * E .. t * E + E - 1 (blocked).
-template <int E>
-__device__ void tile_sort_registers(uint64_t* s_keys, int* vals, int n, const uint32_t* __restrict__ depth_keys,
-									int64_t n_gaussians) {
+// The value of lane (this lane ^ m), m a power of two below 64, by the cheapest exchange for each
+// stride (the network below is unrolled, so m is a constant at every call): DPP quad permutes for 1
+// and 2, ds_swizzle for 4 and 8, and the row swaps for 16 and 32 (v_permlane16/32_swap exchange the
+// odd rows of their first operand with the even rows of their second; with the same value in both,
+// r[1] holds what the lower row of each pair needs and r[0] what the upper one needs). Each value
+// passes through hds_opaque first, which keeps the compiler from merging the swaps of different
+// values into one.
+__device__ __attribute__((always_inline)) inline uint32_t lane_xor(uint32_t v, int m) {
+	const uint32_t u = hds_opaque(v);
+	if (m == 1) return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)u, 0xB1, 0xF, 0xF, false);  // quad_perm 1,0,3,2
+	if (m == 2) return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)u, 0x4E, 0xF, 0xF, false);  // quad_perm 2,3,0,1
+	if (m == 4) return (uint32_t)__builtin_amdgcn_ds_swizzle((int)u, 0x1F | (4 << 10));           // and 31, xor 4
+	if (m == 8) return (uint32_t)__builtin_amdgcn_ds_swizzle((int)u, 0x1F | (8 << 10));           // and 31, xor 8
+	const int lane = (int)(threadIdx.x & (HDS_WAVE - 1));
+	if (m == 16) {
+		const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+		return (lane & 16) ? (uint32_t)r[0] : (uint32_t)r[1];
+	}
+	const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+	return (lane & 32) ? (uint32_t)r[0] : (uint32_t)r[1];
+}
+
+__device__ __attribute__((always_inline)) inline uint32_t shfl_xor_key(uint32_t v, int mask) { return lane_xor(v, mask); }
+__device__ __attribute__((always_inline)) inline uint64_t shfl_xor_key(uint64_t v, int mask) {
+	return ((uint64_t)lane_xor((uint32_t)(v >> 32), mask) << 32) | lane_xor((uint32_t)v, mask);
+}
+
+// Ascending bitonic sort of 256 * E keys held blocked (thread t: keys t * E .. t * E + E - 1):
+// strides inside a thread's E keys are register swaps, strides inside a wave lane exchanges, and
+// only the strides that cross waves go through LDS (s_x, 256 * E keys). Fully unrolled, so every
+// stride and every keep-the-smaller bit of a stage is a constant.
+template <int E, typename K>
+__device__ void bitonic_blocked(K (&v)[E], K* s_x) {
 	constexpr int M = kThreads * E;
 	const int t = threadIdx.x;
-	uint64_t v[E];
 #pragma unroll
-	for (int e = 0; e < E; e++) v[e] = tile_sort_key(vals, t * E + e, n, depth_keys, n_gaussians);
 	for (int k = 2; k <= M; k <<= 1) {
+#pragma unroll
 		for (int j = k >> 1; j >= E; j >>= 1) {
 			// j >= E and k > j: bits j and k of t * E + e do not depend on e.
 			const bool keep_min = ((t * E & j) == 0) == ((t * E & k) == 0);
@@ -770,14 +800,14 @@ __device__ void tile_sort_registers(uint64_t* s_keys, int* vals, int n, const ui
 				// The partner sits in another wave.
 				__syncthreads();
 #pragma unroll
-				for (int e = 0; e < E; e++) s_keys[t * E + e] = v[e];
+				for (int e = 0; e < E; e++) s_x[t * E + e] = v[e];
 				__syncthreads();
 #pragma unroll
-				for (int e = 0; e < E; e++) v[e] = bitonic_keep(v[e], s_keys[(t * E + e) ^ j], keep_min);
+				for (int e = 0; e < E; e++) v[e] = bitonic_keep(v[e], s_x[(t * E + e) ^ j], keep_min);
 			} else {
 				// Same slot e of lane t ^ (j / E).
 #pragma unroll
-				for (int e = 0; e < E; e++) v[e] = bitonic_keep(v[e], shfl_xor_u64(v[e], j / E), keep_min);
+				for (int e = 0; e < E; e++) v[e] = bitonic_keep(v[e], shfl_xor_key(v[e], j / E), keep_min);
 			}
 		}
 		// Strides below E: both keys in this thread's registers (compile-time indices).
@@ -788,7 +818,7 @@ __device__ void tile_sort_registers(uint64_t* s_keys, int* vals, int n, const ui
 				for (int e = 0; e < E; e++) {
 					if ((e & jj) == 0) {
 						const bool ascending = ((t * E + e) & k) == 0;
-						const uint64_t a = v[e], b = v[e | jj];
+						const K a = v[e], b = v[e | jj];
 						const bool swap = (a > b) == ascending;
 						v[e] = swap ? b : a;
 						v[e | jj] = swap ? a : b;
@@ -797,9 +827,109 @@ __device__ void tile_sort_registers(uint64_t* s_keys, int* vals, int n, const ui
 			}
 		}
 	}
+}
+
+// Block-wide minimum and maximum of one value per thread (s_red: 2 * kWaves words).
+__device__ inline void block_min_max(uint32_t lo, uint32_t hi, uint32_t* s_red, uint32_t& mn, uint32_t& mx) {
+#pragma unroll
+	for (int off = HDS_WAVE / 2; off > 0; off >>= 1) {
+		lo = min(lo, (uint32_t)__shfl_xor((int)lo, off, HDS_WAVE));
+		hi = max(hi, (uint32_t)__shfl_xor((int)hi, off, HDS_WAVE));
+	}
+	const int wave = threadIdx.x / HDS_WAVE;
+	if ((threadIdx.x & (HDS_WAVE - 1)) == 0) {
+		s_red[wave] = lo;
+		s_red[kWaves + wave] = hi;
+	}
+	__syncthreads();
+	mn = s_red[0];
+	mx = s_red[kWaves];
+#pragma unroll
+	for (int w = 1; w < kWaves; w++) {
+		mn = min(mn, s_red[w]);
+		mx = max(mx, s_red[kWaves + w]);
+	}
+}
+
+// Lists of n <= 256 * E pairs. The order wanted is that of the 64-bit key (depth bits << 32 | id).
+// First pass: a network on unique 32-bit keys, the depth bits relative to the list's smallest,
+// shifted right just enough to leave the low ib bits to the list index i (n < 2^ib): (coarse
+// depth, i). That order already is the wanted one except among entries of equal coarse depth, so a
+// check of adjacent full keys follows, with odd-even transposition rounds when it finds an
+// inversion and, beyond kFixRounds rounds (many equal depths), the 64-bit network itself.
+constexpr int kFixRounds = 8;
+
+template <int E>
+__device__ __attribute__((always_inline)) void tile_sort_registers(uint64_t* s_keys, uint32_t* s_red, int* vals, int n,
+									const uint32_t* __restrict__ depth_keys, int64_t n_gaussians) {
+	const int t = threadIdx.x;
+	uint64_t* const s_full = s_keys;                                              // [n]: full key of entry i
+	uint32_t* const s_x = reinterpret_cast<uint32_t*>(s_keys + kTileSortRegMax);  // 32-bit exchange area
+	uint64_t full[E];
+	uint32_t lo = 0xffffffffu, hi = 0u;
+#pragma unroll
+	for (int e = 0; e < E; e++) {
+		const int i = t * E + e;
+		full[e] = tile_sort_key(vals, i, n, depth_keys, n_gaussians);
+		if (i < n) {
+			s_full[i] = full[e];
+			lo = min(lo, (uint32_t)(full[e] >> 32));
+			hi = max(hi, (uint32_t)(full[e] >> 32));
+		}
+	}
+	uint32_t dmin, dmax;
+	block_min_max(lo, hi, s_red, dmin, dmax);  // also orders the s_full stores before the gathers below
+	const int ib = 32 - __builtin_clz((unsigned)n);  // n < 2^ib
+	const uint32_t range = dmax - dmin;
+	const int span = range ? 32 - __builtin_clz(range) : 0;
+	const int shift = span + ib > 32 ? span + ib - 32 : 0;
+	uint32_t v[E];
+#pragma unroll
+	for (int e = 0; e < E; e++) {
+		const int i = t * E + e;
+		// Padding sorts last: a real key is at most (2^(32 - ib) - 1) << ib | (n - 1) < 2^32 - 1.
+		v[e] = i < n ? ((((uint32_t)(full[e] >> 32) - dmin) >> shift) << ib) | (uint32_t)i : 0xffffffffu;
+	}
+	bitonic_blocked<E, uint32_t>(v, s_x);
+	const uint32_t imask = (1u << ib) - 1u;
+#pragma unroll
+	for (int e = 0; e < E; e++) full[e] = t * E + e < n ? s_full[v[e] & imask] : ~0ull;
+	__syncthreads();
+	uint64_t* const s_sorted = s_keys;
 #pragma unroll
 	for (int e = 0; e < E; e++)
-		if (t * E + e < n) vals[t * E + e] = (int)(uint32_t)v[e];
+		if (t * E + e < n) s_sorted[t * E + e] = full[e];
+	__syncthreads();
+	// Odd-even transposition on the full keys: a round that swaps nothing after one that swapped
+	// nothing (or the first two rounds) leaves no adjacent inversion, i.e. sorted.
+	int clean = 0;
+	int round = 0;
+	for (; round < kFixRounds && clean < 2; round++) {
+		bool swapped = false;
+		for (int q = t; 2 * q + (round & 1) + 1 < n; q += kThreads) {
+			const int p = 2 * q + (round & 1);
+			const uint64_t a = s_sorted[p], b = s_sorted[p + 1];
+			if (a > b) {
+				s_sorted[p] = b;
+				s_sorted[p + 1] = a;
+				swapped = true;
+			}
+		}
+		clean = __syncthreads_or(swapped) ? 0 : clean + 1;
+	}
+	if (clean < 2) {
+		// Many entries of equal coarse depth: the 64-bit network over what the rounds left.
+#pragma unroll
+		for (int e = 0; e < E; e++) full[e] = t * E + e < n ? s_sorted[t * E + e] : ~0ull;
+		__syncthreads();
+		bitonic_blocked<E, uint64_t>(full, s_keys);
+		__syncthreads();
+#pragma unroll
+		for (int e = 0; e < E; e++)
+			if (t * E + e < n) s_sorted[t * E + e] = full[e];
+		__syncthreads();
+	}
+	for (int p = t; p < n; p += kThreads) vals[p] = (int)(uint32_t)s_sorted[p];
 }
 
 // n <= kTileSortMax: the network over the next power of two, all in LDS.
@@ -833,6 +963,7 @@ __global__ __launch_bounds__(kThreads) void tile_sort_kernel(const int2* __restr
 															 int64_t num_tiles, uint32_t* __restrict__ overflow,
 															 const uint64_t* __restrict__ pairs_total, int64_t cap) {
 	__shared__ uint64_t s_keys[kTileSortMax];
+	__shared__ uint32_t s_red[2 * kWaves];
 	const int64_t tile = blockIdx.x;
 	if (tile >= num_tiles) return;
 	if (pairs_total && (reinterpret_cast<const uint32_t*>(pairs_total + 1)[0] != 0u || *pairs_total > (uint64_t)cap))
@@ -845,10 +976,10 @@ __global__ __launch_bounds__(kThreads) void tile_sort_kernel(const int2* __restr
 		return;
 	}
 	int* vals = values + r.x;
-	if (n <= 256) tile_sort_registers<1>(s_keys, vals, n, depth_keys, n_gaussians);
-	else if (n <= 512) tile_sort_registers<2>(s_keys, vals, n, depth_keys, n_gaussians);
-	else if (n <= 1024) tile_sort_registers<4>(s_keys, vals, n, depth_keys, n_gaussians);
-	else if (n <= kTileSortRegMax) tile_sort_registers<8>(s_keys, vals, n, depth_keys, n_gaussians);
+	if (n <= 256) tile_sort_registers<1>(s_keys, s_red, vals, n, depth_keys, n_gaussians);
+	else if (n <= 512) tile_sort_registers<2>(s_keys, s_red, vals, n, depth_keys, n_gaussians);
+	else if (n <= 1024) tile_sort_registers<4>(s_keys, s_red, vals, n, depth_keys, n_gaussians);
+	else if (n <= kTileSortRegMax) tile_sort_registers<8>(s_keys, s_red, vals, n, depth_keys, n_gaussians);
 	else tile_sort_lds(s_keys, vals, n, depth_keys, n_gaussians);
 }
 

@@ -308,26 +308,34 @@ def test_tile_order_binning_paths_equal_the_oracle(path, frame):
     np.testing.assert_array_equal(np_(bins.tile_ranges), want_ranges)
 
 
-def _one_tile_scene(n, seed):
+def _one_tile_scene(n, seed, levels=50):
     """n small gaussians whose footprints all lie inside tile 0 of a 64x64 image (one list of n
-    pairs), with depths drawn from 50 values so that ties occur."""
+    pairs), with depths drawn from `levels` values so that ties occur (0: continuous depths)."""
     g = torch.Generator().manual_seed(seed)
     means2D = 5.0 + torch.rand(n, 2, generator=g) * 6.0
-    depths = torch.randint(0, 50, (n,), generator=g).float() * 0.25 + 1.0
+    if levels:
+        depths = torch.randint(0, levels, (n,), generator=g).float() * (12.5 / levels) + 1.0
+    else:
+        depths = 1.0 + torch.rand(n, generator=g) * 12.5
     conics = torch.tensor([[0.5, 0.0, 0.5]]).repeat(n, 1)
     return means2D, depths, torch.ones(n), conics, torch.full((n, 1), 0.5)
 
 
-@pytest.mark.parametrize("n,strided", [(3000, False), (5000, False), (5000, True)])
-def test_tile_order_binning_sorts_long_lists_in_lds_and_hands_longer_ones_back(n, strided):
-    """A tile of 3000 pairs (beyond the register network, sorted in LDS) bins bit for bit like the
-    oracle in tile order; one of 5000 pairs (beyond the per-tile sort) is flagged, resolve bins the
-    frame again with the global depth sort (same result) and the device leaves tile order. With
-    `strided`, means2D is a non-contiguous [:, :2] view of an [N, 3] tensor: the rebin must read the
-    dense copy the binning made, not the caller's view."""
+@pytest.mark.parametrize("n,strided,levels", [(1500, False, 50), (1500, False, 1500), (2000, False, 0),
+                                              (3000, False, 50), (5000, False, 50), (5000, True, 50)])
+def test_tile_order_binning_sorts_long_lists_in_lds_and_hands_longer_ones_back(n, strided, levels):
+    """Tiles of 1500-2000 pairs take the register networks: a first pass on 32-bit (coarse depth,
+    list index) keys, then odd-even rounds on the full (depth bits, index) keys where coarse depths
+    tie (depths from 1500 levels) or, with too many ties for a few rounds (50 levels), the 64-bit
+    network; with continuous depths the first pass alone. A tile of 3000 pairs (beyond the register
+    networks, sorted in LDS) bins bit for bit like the oracle in tile order; one of 5000 pairs (beyond
+    the per-tile sort) is flagged, resolve bins the frame again with the global depth sort (same
+    result) and the device leaves tile order. With `strided`, means2D is a non-contiguous [:, :2]
+    view of an [N, 3] tensor: the rebin must read the dense copy the binning made, not the caller's
+    view."""
     from gaussian_splatting.rasterizer._native import HipRasterizer
 
-    means2D, depths, radii, conics, opac = _one_tile_scene(n, 9)
+    means2D, depths, radii, conics, opac = _one_tile_scene(n, 9, levels)
     _, want_values, want_ranges = oracle.bin_gaussians(np_(means2D), np_(depths), np_(radii), np_(conics),
                                                        np_(opac), 64, 64)
     assert int(want_ranges[0, 1] - want_ranges[0, 0]) == n
@@ -341,7 +349,8 @@ def test_tile_order_binning_sorts_long_lists_in_lds_and_hands_longer_ones_back(n
         wide[:, :2] = means2D_dev
         means2D_dev = wide[:, :2]
         assert not means2D_dev.is_contiguous()
-    print(f"[test] tile-order binning, one tile of {n} pairs, strided means2D {strided}", file=sys.stderr, flush=True)
+    print(f"[test] tile-order binning, one tile of {n} pairs, {levels} depth levels, strided means2D {strided}",
+          file=sys.stderr, flush=True)
     bins = ext.bin_async(means2D_dev, depths.to(DEV), radii.to(DEV), conics.to(DEV), None, opac.to(DEV), 64, 64)
     assert bins.tile_order
     rebinned = ext.resolve(bins)
