@@ -755,31 +755,9 @@ __device__ inline K bitonic_keep(K v, K p, bool keep_min) {
 	return (v > p) == keep_min ? p : v;
 }
 
-// The value of lane (this lane ^ m), m a power of two below 64, by the cheapest exchange for each
-// stride (the network below is unrolled, so m is a constant at every call): DPP quad permutes for 1
-// and 2, ds_swizzle for 4 and 8, and the row swaps for 16 and 32 (v_permlane16/32_swap exchange the
-// odd rows of their first operand with the even rows of their second; with the same value in both,
-// r[1] holds what the lower row of each pair needs and r[0] what the upper one needs). Each value
-// passes through hds_opaque first, which keeps the compiler from merging the swaps of different
-// values into one.
-__device__ __attribute__((always_inline)) inline uint32_t lane_xor(uint32_t v, int m) {
-	const uint32_t u = hds_opaque(v);
-	if (m == 1) return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)u, 0xB1, 0xF, 0xF, false);  // quad_perm 1,0,3,2
-	if (m == 2) return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)u, 0x4E, 0xF, 0xF, false);  // quad_perm 2,3,0,1
-	if (m == 4) return (uint32_t)__builtin_amdgcn_ds_swizzle((int)u, 0x1F | (4 << 10));           // and 31, xor 4
-	if (m == 8) return (uint32_t)__builtin_amdgcn_ds_swizzle((int)u, 0x1F | (8 << 10));           // and 31, xor 8
-	const int lane = (int)(threadIdx.x & (HDS_WAVE - 1));
-	if (m == 16) {
-		const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-		return (lane & 16) ? (uint32_t)r[0] : (uint32_t)r[1];
-	}
-	const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-	return (lane & 32) ? (uint32_t)r[0] : (uint32_t)r[1];
-}
-
-__device__ __attribute__((always_inline)) inline uint32_t shfl_xor_key(uint32_t v, int mask) { return lane_xor(v, mask); }
+__device__ __attribute__((always_inline)) inline uint32_t shfl_xor_key(uint32_t v, int mask) { return hds_lane_xor(v, mask); }
 __device__ __attribute__((always_inline)) inline uint64_t shfl_xor_key(uint64_t v, int mask) {
-	return ((uint64_t)lane_xor((uint32_t)(v >> 32), mask) << 32) | lane_xor((uint32_t)v, mask);
+	return ((uint64_t)hds_lane_xor((uint32_t)(v >> 32), mask) << 32) | hds_lane_xor((uint32_t)v, mask);
 }
 
 // Ascending bitonic sort of 256 * E keys held blocked (thread t: keys t * E .. t * E + E - 1):

@@ -87,7 +87,41 @@ __device__ static inline void hds_wave_fence() {
 	asm volatile("" ::: "memory");
 }
 
-__device__ static inline float hds_shfl_xor(float v, int mask) { return __shfl_xor(v, mask, HDS_WAVE); }
+/* Pins a value in a VGPR of its own. This compiler (ROCm 7.2 clang) folds v_permlane16/32_swap
+ * calls whose operands are different elements of one MFMA result vector into a single swap, so
+ * every element after the first silently receives the first one's result; passing each element
+ * through this opaque move first keeps the swaps apart. */
+__device__ static inline uint32_t hds_opaque(uint32_t v) {
+	asm volatile("" : "+v"(v));
+	return v;
+}
+
+/* The value of lane (this lane ^ m), m a power of two below 64 that is a constant at the call
+ * (after unrolling), by the cheapest exchange for each stride instead of a ds_bpermute: DPP quad
+ * permutes for 1 and 2 (VALU), ds_swizzle for 4 and 8, and the row swaps for 16 and 32
+ * (v_permlane16/32_swap exchange the odd rows of their first operand with the even rows of their
+ * second; with the same value in both, r[1] holds what the lower row of each pair needs and r[0]
+ * what the upper one needs). Each value passes through hds_opaque first, which keeps the compiler
+ * from merging the swaps of different values into one. */
+__device__ __attribute__((always_inline)) static inline uint32_t hds_lane_xor(uint32_t v, int m) {
+	const uint32_t u = hds_opaque(v);
+	if (m == 1) return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)u, 0xB1, 0xF, 0xF, false);  // quad_perm 1,0,3,2
+	if (m == 2) return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)u, 0x4E, 0xF, 0xF, false);  // quad_perm 2,3,0,1
+	if (m == 4) return (uint32_t)__builtin_amdgcn_ds_swizzle((int)u, 0x1F | (4 << 10));           // and 31, xor 4
+	if (m == 8) return (uint32_t)__builtin_amdgcn_ds_swizzle((int)u, 0x1F | (8 << 10));           // and 31, xor 8
+	const int lane = (int)(threadIdx.x & (HDS_WAVE - 1));
+	if (m == 16) {
+		const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+		return (lane & 16) ? (uint32_t)r[0] : (uint32_t)r[1];
+	}
+	const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+	return (lane & 32) ? (uint32_t)r[0] : (uint32_t)r[1];
+}
+
+/* hds_lane_xor of a float (same conditions on the mask). */
+__device__ __attribute__((always_inline)) static inline float hds_shfl_xor(float v, int mask) {
+	return __builtin_bit_cast(float, hds_lane_xor(__builtin_bit_cast(uint32_t, v), mask));
+}
 
 /* Sum over all 64 lanes, result in every lane. */
 __device__ static inline float hds_wave_sum(float v) {
@@ -98,7 +132,7 @@ __device__ static inline float hds_wave_sum(float v) {
 
 __device__ static inline int hds_wave_max(int v) {
 #pragma unroll
-	for (int off = 32; off > 0; off >>= 1) v = max(v, __shfl_xor(v, off, HDS_WAVE));
+	for (int off = 32; off > 0; off >>= 1) v = max(v, (int)hds_lane_xor((uint32_t)v, off));
 	return v;
 }
 
@@ -196,15 +230,6 @@ __device__ static inline void hds_split_pair(float x0, float x1, uint32_t& hi, u
 	const float r0 = x0 - hds_u2f(hi << 16), r1 = x1 - hds_u2f(hi & 0xffff0000u);
 	const bf16x2 l = __builtin_convertvector((float __attribute__((ext_vector_type(2)))){r0, r1}, bf16x2);
 	lo = __builtin_bit_cast(uint32_t, l);
-}
-
-/* Pins a value in a VGPR of its own. This compiler (ROCm 7.2 clang) folds v_permlane16/32_swap
- * calls whose operands are different elements of one MFMA result vector into a single swap, so
- * every element after the first silently receives the first one's result; passing each element
- * through this opaque move first keeps the swaps apart. */
-__device__ static inline uint32_t hds_opaque(uint32_t v) {
-	asm volatile("" : "+v"(v));
-	return v;
 }
 
 /* One MFMA result element as an independent 32-bit operand for a lane swap. */
