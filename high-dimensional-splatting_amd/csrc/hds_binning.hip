@@ -142,7 +142,8 @@ __device__ inline uint64_t lookback(uint64_t* status, int64_t stride, int64_t pa
 // steps is what a look-back's time is made of.
 __device__ inline uint64_t wave_sum64(uint64_t v) {
 #pragma unroll
-	for (int off = 1; off < HDS_WAVE; off <<= 1) v += __shfl_xor(v, off, HDS_WAVE);
+	for (int off = 1; off < HDS_WAVE; off <<= 1)
+		v += ((uint64_t)hds_lane_xor((uint32_t)(v >> 32), off) << 32) | hds_lane_xor((uint32_t)v, off);
 	return v;
 }
 
@@ -198,12 +199,7 @@ __device__ inline int64_t take_ticket(uint32_t* ticket, int64_t* s_part) {
 // Exclusive scan across the block of one value per thread; also returns the block total.
 __device__ inline uint32_t block_exclusive_scan(uint32_t v, uint32_t* s_wave, uint32_t& total) {
 	const int lane = threadIdx.x & (HDS_WAVE - 1), wave = threadIdx.x / HDS_WAVE;
-	uint32_t x = v;
-#pragma unroll
-	for (int off = 1; off < HDS_WAVE; off <<= 1) {
-		const uint32_t y = __shfl_up(x, off, HDS_WAVE);
-		if (lane >= off) x += y;
-	}
+	const uint32_t x = hds_wave_inclusive_scan(v);
 	if (lane == HDS_WAVE - 1) s_wave[wave] = x;
 	__syncthreads();
 	uint32_t before = 0, sum = 0;
@@ -740,12 +736,6 @@ __device__ inline uint64_t tile_sort_key(const int* vals, int i, int n, const ui
 	return ((uint64_t)d << 32) | g;
 }
 
-__device__ inline uint64_t shfl_xor_u64(uint64_t v, int mask) {
-	const int lo = __shfl_xor((int)(uint32_t)v, mask, HDS_WAVE);
-	const int hi = __shfl_xor((int)(uint32_t)(v >> 32), mask, HDS_WAVE);
-	return ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo;
-}
-
 // One side of a bitonic compare-exchange: the element keeps the smaller of (v, partner p) when
 // keep_min (the pair's lower index in an ascending block, or its upper index in a descending one),
 // else the larger: it takes p exactly when (v > p) == keep_min. One compare and one select per
@@ -811,8 +801,8 @@ __device__ void bitonic_blocked(K (&v)[E], K* s_x) {
 __device__ inline void block_min_max(uint32_t lo, uint32_t hi, uint32_t* s_red, uint32_t& mn, uint32_t& mx) {
 #pragma unroll
 	for (int off = HDS_WAVE / 2; off > 0; off >>= 1) {
-		lo = min(lo, (uint32_t)__shfl_xor((int)lo, off, HDS_WAVE));
-		hi = max(hi, (uint32_t)__shfl_xor((int)hi, off, HDS_WAVE));
+		lo = min(lo, hds_lane_xor(lo, off));
+		hi = max(hi, hds_lane_xor(hi, off));
 	}
 	const int wave = threadIdx.x / HDS_WAVE;
 	if ((threadIdx.x & (HDS_WAVE - 1)) == 0) {
@@ -975,13 +965,8 @@ template <typename F>
 __device__ inline void for_each_pair(uint2 rc, uint32_t first, int tiles_x, uint32_t* s_off, F&& f) {
 	const int lane = threadIdx.x & (HDS_WAVE - 1);
 	const uint32_t cnt = (rc.y & 0xffffu) * (rc.y >> 16);
-	uint32_t x = cnt;
-#pragma unroll
-	for (int off = 1; off < HDS_WAVE; off <<= 1) {
-		const uint32_t y = (uint32_t)__shfl_up((int)x, off, HDS_WAVE);
-		if (lane >= off) x += y;
-	}
-	const uint32_t run = (uint32_t)__shfl((int)x, HDS_WAVE - 1, HDS_WAVE);
+	const uint32_t x = hds_wave_inclusive_scan(cnt);
+	const uint32_t run = (uint32_t)__builtin_amdgcn_readlane((int)x, HDS_WAVE - 1);
 	s_off[lane] = x - cnt;
 	hds_wave_fence();
 	for (uint32_t base = 0; base < run; base += HDS_WAVE) {

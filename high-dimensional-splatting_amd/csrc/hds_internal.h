@@ -118,6 +118,21 @@ __device__ __attribute__((always_inline)) static inline uint32_t hds_lane_xor(ui
 	return (lane & 32) ? (uint32_t)r[0] : (uint32_t)r[1];
 }
 
+/* Inclusive prefix sum over the 64 lanes (lane l gets v_0 + ... + v_l) by DPP moves instead of a
+ * chain of ds_bpermutes: row shifts by 1, 2, 4 and 8 inside each 16-lane row (lanes shifted in from
+ * outside the row read 0), then lane 15 of rows 0 and 2 added to rows 1 and 3 (row_bcast:15) and
+ * lane 31 to rows 2 and 3 (row_bcast:31); rows the row mask leaves out keep the old value 0. */
+__device__ __attribute__((always_inline)) static inline uint32_t hds_wave_inclusive_scan(uint32_t v) {
+	uint32_t x = v;
+	x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xF, 0xF, true);   // row_shr:1
+	x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xF, 0xF, true);   // row_shr:2
+	x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xF, 0xF, true);   // row_shr:4
+	x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xF, 0xF, true);   // row_shr:8
+	x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x142, 0xA, 0xF, false);  // row_bcast:15
+	x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x143, 0xC, 0xF, false);  // row_bcast:31
+	return x;
+}
+
 /* hds_lane_xor of a float (same conditions on the mask). */
 __device__ __attribute__((always_inline)) static inline float hds_shfl_xor(float v, int mask) {
 	return __builtin_bit_cast(float, hds_lane_xor(__builtin_bit_cast(uint32_t, v), mask));
