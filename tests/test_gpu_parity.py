@@ -267,14 +267,16 @@ def test_async_binning_equals_the_oracle_whatever_the_capacity(capacity, order):
 
 
 @pytest.mark.parametrize("path", ["scatter", "emit"])
-@pytest.mark.parametrize("frame", ["mid", "wide"])
+@pytest.mark.parametrize("frame", ["mid", "wide", "giants"])
 def test_tile_order_binning_paths_equal_the_oracle(path, frame):
     """Both tile-order paths bin like the oracle bit for bit: the counting scatter (per-chunk LDS tile
     histograms, one scan over the (tile, chunk) count matrix, pairs scattered into their runs, then
     the per-tile depth sort) and the emit + pair sort by tile that frames with a count matrix above
     the limit take (forced here with hds_set_tile_scatter_limit). "wide" is a 2048x1088 frame of 8704
     tiles, more than one LDS histogram holds (8192), so the counts and the scatter run in two
-    windows of tiles."""
+    windows of tiles. "giants" adds to that frame 12 gaussians of sigma 150-600 px, whose rectangles
+    cover thousands of tiles in both windows (runs of thousands of pairs per wave), and culls every
+    seventh gaussian (radius 0)."""
     from gaussian_splatting.rasterizer._native import HipRasterizer, load_library
 
     if frame == "mid":
@@ -287,8 +289,12 @@ def test_tile_order_binning_paths_equal_the_oracle(path, frame):
         m2 = torch.rand(n, 2, generator=g) * torch.tensor([float(width), float(height)])
         d = 1.0 + torch.rand(n, generator=g) * 9.0
         sigma = 0.5 + torch.rand(n, generator=g) * 6.0
+        if frame == "giants":
+            sigma[::12_500] = 150.0 + torch.rand(12, generator=g) * 450.0
         c = torch.stack([sigma ** -2, torch.zeros(n), sigma ** -2], -1)
         r = 3.0 * sigma
+        if frame == "giants":
+            r[3::7] = 0.0
         opac = (0.05 + 0.9 * torch.rand(n, generator=g))[:, None]
         m2, d, r, c, opac = (t.contiguous().to(DEV) for t in (m2, d, r, c, opac))
     counts, want_values, want_ranges = oracle.bin_gaussians(np_(m2), np_(d), np_(r), np_(c), np_(opac), width,
