@@ -714,15 +714,14 @@ __global__ __launch_bounds__(kThreads) void ranges_kernel(int64_t num_pairs, con
 }
 
 // ---------------------------------------------------------------------------------------------
-// Depth order inside each tile (the tile-order binning). The pairs were emitted in gaussian-index
-// order and sorted by tile alone, so every tile's list holds the right gaussians in index order;
-// one work-group per tile sorts it by the key (depth bits << 32 | gaussian id), which is the
-// reference's (tile, depth bits, index) order restricted to the tile. Lists of up to 2048 pairs
-// are sorted by a bitonic network with E = 256..2048 / 256 keys per thread in registers: strides
-// inside a thread's E keys are register swaps, strides inside a wave lane shuffles, and only the
-// strides that cross waves (three stages) go through LDS. Lists of up to kTileSortMax pairs take
-// the same network entirely in LDS; longer ones are left in index order and flagged (bit 1 of
-// *overflow), and the caller bins the frame again with the global depth sort.
+// Depth order inside each tile (the tile-order binning). Every tile's list holds the right gaussians
+// (placed by the counting scatter in an order the atomics chose, or, on the emit + pair sort path, in
+// index order); one work-group per tile sorts it by the key (depth bits << 32 | gaussian id), which
+// is the reference's (tile, depth bits, index) order restricted to the tile. Lists of up to 2048
+// pairs are sorted in registers with E = 256..2048 / 256 keys per thread (tile_sort_registers: a
+// 32-bit first pass, then the full keys); lists of up to kTileSortMax pairs take the 64-bit network
+// entirely in LDS; longer ones are left unsorted and flagged (bit 1 of *overflow), and the caller
+// bins the frame again with the global depth sort.
 // ---------------------------------------------------------------------------------------------
 
 constexpr int kTileSortRegMax = 2048;
@@ -996,7 +995,7 @@ __device__ inline int64_t chunk_gaussian(int64_t chunk, int r) {
 // Step 1: the records of one chunk (prepare_kernel's, without the index order) and the chunk's
 // pair count per tile, one LDS histogram of up to kHistBins tiles at a time, stored to column
 // `chunk` of the tile-major count matrix: counts[tile * chunks + chunk]. Also clears `zero` (the
-// control block the scan uses, tile_ranges) for the later launches.
+// control block and the status words the scan uses, tile_ranges) for the later launches.
 __global__ __launch_bounds__(kScatterThreads) void prepare_tiles_kernel(int64_t n, const GaussianInputs in,
 																		int64_t num_tiles, int64_t chunks,
 																		uint32_t* __restrict__ counts, ZeroRanges zero) {
@@ -1035,11 +1034,11 @@ __global__ __launch_bounds__(kScatterThreads) void prepare_tiles_kernel(int64_t 
 // of the chunk's run starts serving as write cursors (one LDS atomic per pair; the order inside a
 // run is whatever the atomics make it, and tile_sort_kernel replaces it by (depth bits, index)).
 // Every work-group also writes a share of tile_ranges: [run start of (tile, chunk 0), run start of
-// (tile + 1, chunk 0)), (0, 0) when empty. Nothing at or past limit = min(P, cap) is written and the ranges are cut
-// there, so a binning whose pair buffers were too small still leaves only written entries inside its
-// ranges (the caller bins it again with exact buffers); a failed scan, or P beyond int32 indices,
-// writes nothing (tile_ranges were cleared by prepare_tiles_kernel). With pairs_total null, cap is
-// the exact pair count.
+// (tile + 1, chunk 0)), (0, 0) when empty. Nothing at or past limit = min(P, cap) is written and the
+// ranges are cut there, so a binning whose pair buffers were too small still leaves only written
+// entries inside its ranges (the caller bins it again with exact buffers); a failed scan, or P beyond
+// int32 indices, writes nothing (tile_ranges were cleared by prepare_tiles_kernel). With pairs_total
+// null, cap is the exact pair count.
 __global__ __launch_bounds__(kScatterThreads) void scatter_kernel(int64_t n, const uint2* __restrict__ rects,
 																  int tiles_x, int64_t num_tiles, int64_t chunks,
 																  const uint32_t* __restrict__ starts,
@@ -1088,7 +1087,8 @@ __global__ __launch_bounds__(kScatterThreads) void scatter_kernel(int64_t n, con
 }
 
 // ---------------------------------------------------------------------------------------------
-// Workspace layouts. Every region is 256-byte aligned; [ctrl, bytes) is zeroed before use.
+// Workspace layouts. Every region is 256-byte aligned; what a binning reads before writing (the
+// control block, the look-back status words) is zeroed before use.
 // ---------------------------------------------------------------------------------------------
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
